@@ -1,0 +1,166 @@
+"""Benchmark of the fused output-projection + cross-entropy + pointer-mixture op (fwd+bwd) on one MI355X.
+
+A step is one forward + backward of `linear_ce_mix_biased` over one batch of the configuration's synthetic
+inputs (default: config 2, N = 32768 tokens, d = 2048, V = 50304, bf16 operands, fp32 accumulation), with
+the inputs resident in HBM before the timed region. Prints one JSON line:
+  value        tokens/s over the K timed steps (N*K / wall time between two synchronisations)
+  roofline     the dominant kernel of the step, timed with HIP events on the stream it runs on
+  op_roofline  the whole step against the bf16 MFMA peak on 6*N*V*d algorithmic FLOPs (the metric's "%")
+  cpu_baseline this repo's torch restatement of the reference eager formula (fp32, fwd+bwd) on a row sample
+               of the same inputs, on the host cores, scaled to tokens/s
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16 = 2.5e15     # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12      # MI355X HBM3E, B/s
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--cpu-rows", type=int, default=2048, help="rows of the CPU baseline sample (0: skip)")
+    ap.add_argument("--stage-reps", type=int, default=5, help="timed repetitions of each kernel stage")
+    return ap.parse_args()
+
+
+def _stage_times(inp, reps):
+    """Average duration (ms) of each C-ABI stage, with torch events on the current stream (the stream every
+    stage is launched on)."""
+    from memarch_amd import _lib
+    lib = _lib.load()
+    h, w, b = inp.h, inp.w.to(torch.bfloat16), inp.bias
+    n, k = h.shape
+    v = w.shape[0]
+    vr = inp.cfg.v_real
+    dev = h.device
+    st = torch.cuda.current_stream(dev).cuda_stream
+    f32 = dict(dtype=torch.float32, device=dev)
+    loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
+    loss_sum = torch.empty((), **f32)
+    fws = lib.mce_fwd_ws_bytes(n, k, v)
+    bws = lib.mce_bwd_ws_bytes(n, k, v)
+    wsf = torch.empty(fws, dtype=torch.uint8, device=dev)
+    wsb = torch.empty(bws, dtype=torch.uint8, device=dev)
+    go = torch.full((), 1.0 / n, **f32)
+    dbias, dgate = torch.empty(v, **f32), torch.empty(n, **f32)
+    dh = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    dw = torch.empty(v, k, **f32)
+    P = lambda t: t.data_ptr()
+    stages = {
+        "fwd": lambda: _lib.call("mce_fwd", P(h), k, P(w), k, P(b), P(inp.y), P(inp.gate), P(inp.hit), n, k, v, vr,
+                                 P(loss_rows), P(lse), P(wgt), P(dgr), P(loss_sum), P(wsf), fws, st),
+        "logits_grad": lambda: _lib.call("mce_bwd_logits_grad", P(h), k, P(w), k, P(b), P(inp.y), P(lse), P(wgt),
+                                         P(dgr), P(go), n, k, v, vr, P(dbias), P(dgate), P(wsb), bws, st),
+        "dhidden": lambda: _lib.call("mce_bwd_dhidden", P(w), k, n, k, v, P(dh), 1, k, P(wsb), bws, st),
+        "dweight": lambda: _lib.call("mce_bwd_dweight", P(h), k, n, k, v, P(dw), k, P(wsb), bws, st),
+    }
+    out = {}
+    for name, fn in stages.items():
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) / reps
+    return out
+
+
+def _cpu_baseline(cfg, rows):
+    """Reference eager formula restated in torch (oracle.mce_oracle.eager_ce_part), fp32 fwd+bwd on the host."""
+    from memarch_amd.workloads import make_inputs
+    from oracle.mce_oracle import eager_ce_part
+    inp = make_inputs(cfg, rows=rows)
+    h = inp.h.bfloat16().float().requires_grad_()
+    w = inp.w.bfloat16().float().requires_grad_()
+    b = inp.bias.clone()
+    b[cfg.v_real:] = float("-inf")  # padded ids masked, as the GPU path does with v_real
+    b.requires_grad_()
+    g = inp.gate.clone().requires_grad_()
+    t0 = time.perf_counter()
+    loss = eager_ce_part(h, w, b, inp.y, inp.c1, g) / cfg.n
+    loss.backward()
+    dt = time.perf_counter() - t0
+    return dict(value=rows / dt, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{rows} of {cfg.n} rows of config {cfg.index} (N={cfg.n}, d={cfg.d}, V={cfg.v}), fp32 "
+                       f"torch eager fwd+bwd ({dt:.2f} s), os.cpu_count()={os.cpu_count()}; tokens/s scales "
+                       f"linearly in N")
+
+
+def main():
+    args = _args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the op is single-GPU in this build (--gpus {args.gpus} refused)",
+              file=sys.stderr)
+        sys.exit(2)
+    from memarch_amd import fused_ops
+    from memarch_amd.workloads import CONFIGS, make_inputs
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    print(f"[bench] generating config {cfg.index} inputs ({cfg.name})", file=sys.stderr, flush=True)
+    inp = make_inputs(cfg).to(dev)
+    n, d, v = cfg.n, cfg.d, cfg.v
+    h = inp.h.detach().requires_grad_()
+    w = inp.w.detach().requires_grad_()
+    b = inp.bias.detach().requires_grad_()
+    gate = inp.gate.detach().requires_grad_()
+
+    def step():
+        h.grad = w.grad = b.grad = gate.grad = None
+        loss = fused_ops.linear_ce_mix_biased(h, w, b, inp.y, gate, inp.hit, v_real=cfg.v_real)
+        (loss / n).backward()
+        return loss
+
+    print("[bench] warmup", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print("[bench] timed steps", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    tok_s = n / dt
+    flops = 6.0 * n * v * d
+    print("[bench] stage timing", file=sys.stderr, flush=True)
+    stages = _stage_times(inp, args.stage_reps)
+    dom = max(stages, key=stages.get)
+    dom_flops = 2.0 * n * v * d   # every stage is one N x V x d contraction
+    ach = dom_flops / (stages[dom] * 1e-3)
+    res = {
+        "metric": "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA peak",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded, config %d distributions)" % cfg.index,
+        "config": {"workload": f"config {cfg.index}: fused linear+CE+pointer fwd+bwd", "N": n, "d": d, "V": v,
+                   "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach / 1e12, 2),
+                     "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16, 4),
+                     "traffic": None},
+        "op_roofline": {"achieved": round(flops / dt / 1e12, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                        "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
+        "stages_ms": {k: round(x, 3) for k, x in stages.items()},
+    }
+    if args.cpu_rows > 0:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = _cpu_baseline(cfg, min(args.cpu_rows, n))
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

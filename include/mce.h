@@ -1,0 +1,116 @@
+/*
+ * mce.h — C ABI of the MI355X (gfx950) fused output-projection + cross-entropy + pointer-mixture operator.
+ *
+ * This library replaces the GPU work of memarch's `fused_ops._LinearCEMix` (fused_ops.py:137-162), i.e. the
+ * per-chunk bf16 GEMM `logits = hc @ wd.T` (fused_ops.py:150), the Triton row kernel `_ce_mix_kernel`
+ * (fused_ops.py:104-134) and the two gradient GEMMs `gh = logits @ wd`, `gw += logits.T @ hc`
+ * (fused_ops.py:153-154). The Python host (memarch_amd/fused_ops.py) keeps the reference's
+ * `torch.autograd.Function` signature and calls these entry points through ctypes.
+ *
+ * Per row n (x_v = h_n . W_v + b_v in fp32 from bf16 operands; columns v >= V_real are masked to -inf):
+ *   lse_n  = log sum_v exp(x_v)          py = exp(x_y - lse)         P = (1 - g) py + g hit
+ *   loss_n = -log max(P, 1e-30)          wgt_n = (1 - g) py / P      dgr_n = (py - hit) / P
+ *   (wgt_n = dgr_n = 0 where P < 1e-30: the gradient of torch's clamp, full2.py:1925-1929)
+ *   G_nv   = go wgt_n (exp(x_v - lse_n) - [v = y_n])
+ *   dH = G W,  dW = G^T H,  dBias_v = sum_n G_nv,  dGate_n = go dgr_n
+ *
+ * Conventions (all entry points):
+ *   - bf16 tensors are passed as `const uint16_t*` (raw bf16 bits), row-major with an explicit leading dimension.
+ *   - H is [N, K] (ldh), W is [V, K] (ldw). K, ldh and ldw must be multiples of 8; H and W 16-byte aligned.
+ *   - y is int64 [N]; gate and hit are fp32 [N]. A target outside [0, V_real) has probability 0 (py = 0).
+ *   - bias may be NULL (no bias; e.g. the `_head_w` layout of full2.py:1842-1851 that folds the bias into W).
+ *   - Every call is asynchronous on `stream` (hipStream_t passed as void*); nothing synchronises the host.
+ *   - Buffers are caller-owned. The library allocates no device memory: scratch lives in the caller's
+ *     workspace `ws` of at least the size returned by the matching *_ws_bytes function (256-byte aligned).
+ *   - Return value: 0 on success, otherwise an MCE_E* code; mce_error_string() describes it.
+ */
+#ifndef MCE_H
+#define MCE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define MCE_API __attribute__((visibility("default")))
+#else
+#define MCE_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MCE_OK 0
+#define MCE_EINVAL 1     /* bad size, stride or null pointer */
+#define MCE_EALIGN 2     /* pointer or leading dimension not aligned as required */
+#define MCE_EWORKSPACE 3 /* workspace too small */
+#define MCE_ELAUNCH 4    /* a HIP launch failed (see mce_last_hip_error) */
+
+/* Library version (major*10000 + minor*100 + patch). No counterpart in the reference. */
+MCE_API int mce_version(void);
+
+/* Human-readable text for a return code. No counterpart in the reference. */
+MCE_API const char* mce_error_string(int code);
+
+/* The hipError_t of the last failed launch in this process (0 if none). No counterpart in the reference. */
+MCE_API int mce_last_hip_error(void);
+
+/* Workspace bytes needed by mce_fwd for this shape. Replaces the temporaries of fused_ops.py:143-146,150. */
+MCE_API size_t mce_fwd_ws_bytes(int64_t N, int64_t K, int64_t V);
+
+/*
+ * Forward: per-row loss, lse and the two per-row gradient coefficients, plus the fp32 loss sum.
+ * Replaces `_LinearCEMix.forward` (fused_ops.py:138-157) minus its gradient GEMMs: the logits GEMM
+ * (fused_ops.py:150) and the loss half of `_ce_mix_kernel` (fused_ops.py:113-127). The N x V logits are
+ * never written to memory. loss_sum[0] = sum_n loss_n (the value `loss.sum()` returns at fused_ops.py:157).
+ * Outputs: loss_rows, lse_rows, wgt_rows, dgr_rows: fp32 [N]; loss_sum: fp32 [1].
+ */
+MCE_API int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+            const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
+            int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
+            void* ws, size_t ws_bytes, void* stream);
+
+/* Workspace bytes needed by the backward entry points for this shape (the bf16 G buffer [N, Vp] with
+ * Vp = V rounded up to 256, plus the dBias partial sums). Replaces the bf16 logits chunk that
+ * fused_ops.py:150,134 overwrites with the gradient. */
+MCE_API size_t mce_bwd_ws_bytes(int64_t N, int64_t K, int64_t V);
+
+/*
+ * Backward step 1: recompute the logits tile by tile and write G (bf16, [N, Vp], row stride Vp) into the
+ * workspace; reduce dBias (if dBias != NULL, requires bias != NULL) and write dGate (if dGate != NULL).
+ * `go` is a device pointer to the fp32 upstream gradient of the loss sum (a 0-dim tensor).
+ * Replaces the gradient half of `_ce_mix_kernel` (fused_ops.py:127-134) and the `go` scaling of
+ * `_LinearCEMix.backward` (fused_ops.py:159-162).
+ */
+MCE_API int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                        const int64_t* y, const float* lse_rows, const float* wgt_rows, const float* dgr_rows,
+                        const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
+                        float* dGate, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Backward step 2: dH = G W (fp32 accumulation). dH is [N, K] with row stride lddh, fp32 (dh_bf16 = 0) or
+ * bf16 (dh_bf16 = 1). Needs the workspace filled by mce_bwd_logits_grad. Replaces `gh[i] = logits @ wd`
+ * (fused_ops.py:153).
+ */
+MCE_API int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16,
+                    int64_t lddh, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Backward step 3: dW = G^T H (fp32 accumulation), dW fp32 [V, K] with row stride lddw (overwritten, not
+ * accumulated). Needs the workspace filled by mce_bwd_logits_grad. Replaces `gw += (logits.T @ hc).float()`
+ * (fused_ops.py:154).
+ */
+MCE_API int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_t V, float* dW, int64_t lddw,
+                    void* ws, size_t ws_bytes, void* stream);
+
+/* The three backward steps in order (dH / dW / dBias / dGate may be NULL to skip them). */
+MCE_API int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
+            const float* lse_rows, const float* wgt_rows, const float* dgr_rows, const float* go, int64_t N,
+            int64_t K, int64_t V, int64_t V_real, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
+            float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MCE_H */

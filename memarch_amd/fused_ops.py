@@ -1,0 +1,164 @@
+"""Fused vocabulary projection + cross-entropy + pointer mixture on MI355X, as torch.autograd.Functions.
+
+Drop-in for memarch's `fused_ops.linear_ce_mix` / `_LinearCEMix` (fused_ops.py:137-167): same call signature,
+same return value (the fp32 loss SUM over rows) and the same gradient convention (grads for h, w and gate in
+their own dtypes; None for y, hit and chunk). All device work runs in libmce.so (HIP, gfx950) on torch's
+current stream; there is no other code path, and a tensor that is not on a GPU raises.
+
+Differences from the reference that autograd cannot observe: gradients are computed in `backward` by
+recomputing the logits (the reference computes them during `forward`, fused_ops.py:148-155), and `chunk` is
+accepted and ignored (tiling is internal). Logits are fp32 in both passes (never rounded to bf16), and rows
+with P below the 1e-30 clamp get zero gradient, as the reference's eager formula does (full2.py:1925-1929).
+"""
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("memarch_amd.fused_ops runs on the GPU only; got a tensor on " + str(t.device))
+
+
+def _bf16_operand(t, kp):
+    """bf16 copy/view of a 2-D operand whose row stride and width are multiples of 8 and whose base is 16-byte
+    aligned, zero-padded to `kp` columns when the width is not a multiple of 8."""
+    t = t.detach()
+    if t.dtype != _BF16:
+        t = t.to(_BF16)
+    k = t.shape[1]
+    if k == kp and t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    out = torch.zeros(t.shape[0], kp, dtype=_BF16, device=t.device)
+    out[:, :k] = t
+    return out
+
+
+def _rows(t, dtype):
+    return t.detach().reshape(-1).to(dtype).contiguous()
+
+
+def _forward(ctx, h, w, bias, y, gate, hit, v_real):
+    _check_cuda(h, w, bias, y, gate, hit)
+    if h.dim() != 2 or w.dim() != 2 or h.shape[1] != w.shape[1]:
+        raise ValueError(f"h {tuple(h.shape)} and w {tuple(w.shape)} must be [N, K] and [V, K]")
+    n, k = h.shape
+    v = w.shape[0]
+    v_real = v if v_real is None else int(v_real)
+    if not 1 <= v_real <= v:
+        raise ValueError(f"v_real={v_real} must be in [1, {v}]")
+    for name, t in (("y", y), ("gate", gate), ("hit", hit)):
+        if t.numel() != n:
+            raise ValueError(f"{name} has {t.numel()} elements, expected {n}")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != v):
+        raise ValueError(f"bias must be [V={v}], got {tuple(bias.shape)}")
+    kp = (k + 7) // 8 * 8
+    dev = h.device
+    hd, wd = _bf16_operand(h, kp), _bf16_operand(w, kp)
+    y64 = _rows(y, torch.int64)
+    gf, hf = _rows(gate, torch.float32), _rows(hit, torch.float32)
+    bf = None if bias is None else _rows(bias, torch.float32)
+    f32 = dict(dtype=torch.float32, device=dev)
+    loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
+    loss_sum = torch.empty((), **f32)
+    lib = _lib.load()
+    ws_bytes = lib.mce_fwd_ws_bytes(n, kp, v)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("mce_fwd", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf), _ptr(hf),
+              n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum), _ptr(ws),
+              ws_bytes, _stream(dev))
+    ctx.save_for_backward(hd, wd, bf, y64, lse, wgt, dgr)
+    ctx.meta = (n, k, kp, v, v_real)
+    ctx.dtypes = (h.dtype, w.dtype, gate.dtype, None if bias is None else bias.dtype)
+    ctx.loss_rows = loss_rows
+    return loss_sum
+
+
+def _backward(ctx, go, need_h, need_w, need_b, need_g):
+    hd, wd, bf, y64, lse, wgt, dgr = ctx.saved_tensors
+    n, k, kp, v, v_real = ctx.meta
+    hdt, wdt, gdt, bdt = ctx.dtypes
+    dev = hd.device
+    go32 = go.detach().reshape(()).to(torch.float32).contiguous()
+    f32 = dict(dtype=torch.float32, device=dev)
+    dgate = torch.empty(n, **f32) if need_g else None
+    dbias = torch.empty(v, **f32) if (need_b and bf is not None) else None
+    dh = dw = None
+    if need_h or need_w or need_g or dbias is not None:
+        lib = _lib.load()
+        ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        st = _stream(dev)
+        _lib.call("mce_bwd_logits_grad", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
+                  _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(go32), n, kp, v, v_real, _ptr(dbias), _ptr(dgate),
+                  _ptr(ws), ws_bytes, st)
+        if need_h:
+            out_bf16 = hdt == _BF16
+            dh = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev)
+            _lib.call("mce_bwd_dhidden", _ptr(wd), wd.stride(0), n, kp, v, _ptr(dh), int(out_bf16), dh.stride(0),
+                      _ptr(ws), ws_bytes, st)
+            dh = dh[:, :k].to(hdt)
+        if need_w:
+            dw = torch.empty(v, kp, **f32)
+            _lib.call("mce_bwd_dweight", _ptr(hd), hd.stride(0), n, kp, v, _ptr(dw), dw.stride(0), _ptr(ws),
+                      ws_bytes, st)
+            dw = dw[:, :k].to(wdt)
+    if dgate is not None:
+        dgate = dgate.to(gdt)
+    if dbias is not None:
+        dbias = dbias.to(bdt)
+    return dh, dw, dbias, dgate
+
+
+class _LinearCEMix(torch.autograd.Function):
+    """forward(ctx, h [N,K], w [V,K], y [N], gate [N], hit [N], chunk) -> fp32 loss sum (fused_ops.py:137-162)."""
+
+    @staticmethod
+    def forward(ctx, h, w, y, gate, hit, chunk):
+        return _forward(ctx, h, w, None, y, gate, hit, None)
+
+    @staticmethod
+    def backward(ctx, go):
+        nh, nw, _, ng, _, _ = ctx.needs_input_grad
+        dh, dw, _, dg = _backward(ctx, go, nh, nw, False, ng)
+        return dh, dw, None, dg, None, None
+
+
+class _LinearCEMixBiased(torch.autograd.Function):
+    """As _LinearCEMix with an explicit fp32 bias [V] (no bf16 rounding of the bias, unlike the folded layout of
+    full2.py:1842-1851) and optional masking of padded vocabulary ids v >= v_real to -inf."""
+
+    @staticmethod
+    def forward(ctx, h, w, bias, y, gate, hit, v_real):
+        return _forward(ctx, h, w, bias, y, gate, hit, v_real)
+
+    @staticmethod
+    def backward(ctx, go):
+        nh, nw, nb, _, ng, _, _ = ctx.needs_input_grad
+        dh, dw, db, dg = _backward(ctx, go, nh, nw, nb, ng)
+        return dh, dw, db, None, dg, None, None
+
+
+@torch.compiler.disable
+def linear_ce_mix(h, w, y, gate, hit, chunk=4096):
+    """Sum over rows of -log max((1-g)*softmax(h w^T)[y] + g*hit, 1e-30) (fused_ops.py:165-167)."""
+    return _LinearCEMix.apply(h.reshape(-1, h.shape[-1]), w, y.reshape(-1), gate.reshape(-1), hit.reshape(-1), chunk)
+
+
+@torch.compiler.disable
+def linear_ce_mix_biased(h, w, bias, y, gate, hit, v_real=None, chunk=4096):
+    """linear_ce_mix with logits h w^T + bias (fp32) and ids >= v_real masked out; also returns dBias."""
+    del chunk
+    return _LinearCEMixBiased.apply(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), gate.reshape(-1),
+                                    hit.reshape(-1), v_real)

@@ -1,0 +1,132 @@
+"""CPU oracle for the fused output-projection + cross-entropy + pointer-mixture operator.
+
+TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+module, and only as the checker or the timed CPU baseline; the product path (memarch_amd) never calls it.
+
+Two independent restatements of the reference's eager formula (full2.py:1917-1929, `_ce_part`):
+
+* `forward` / `backward`: numpy closed form (fp64 or fp32, chunked over rows so memory stays bounded):
+      x_v    = h . W_v + b_v            (v >= v_real masked to -inf)            full2.py:1917-1919
+      lse    = logsumexp_v x_v ; py = exp(x_y - lse)                            full2.py:1923-1926
+      P      = (1 - g) py + g hit ; loss = -log max(P, 1e-30), summed           full2.py:1927-1929
+      wgt    = (1 - g) py / P ; dgr = (py - hit) / P ; both 0 where P < 1e-30  (torch clamp backward)
+      G      = go wgt (softmax - onehot) ; dH = G W ; dW = G^T H ; dBias = sum_n G ; dGate = go dgr
+  The reference's fused Triton path computes the same quantities (fused_ops.py:113-134).
+* `eager_ce_part`: the eager formula written with torch ops exactly as `_ce_part` composes them; torch
+  autograd supplies its gradients, independently of the closed form above.
+
+Pinning (tests/test_oracle.py): closed form vs torch autograd in fp64; central finite differences on tiny
+shapes; g = 0 against torch.nn.functional.cross_entropy; hit = 0 gradient = plain CE gradient; hit = 1,
+g -> 1 gives loss -> 0; softmax null-space (sum_v G = 0); row permutation; logit-shift invariance; the
+folded-bias layout of full2.py:1842-1851; golden fixtures in tests/golden/.
+"""
+import numpy as np
+
+CLAMP_P = 1e-30
+
+
+def bf16_round(a):
+    """Round fp32 values to the nearest bf16 (ties to even), returned as fp32."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    return r.view(np.float32)
+
+
+def _logits(hc, w, bias, v_real, dt):
+    x = hc.astype(dt, copy=False) @ w.astype(dt, copy=False).T
+    if bias is not None:
+        x += bias.astype(dt, copy=False)[None, :]
+    if v_real is not None and v_real < w.shape[0]:
+        x[:, v_real:] = -np.inf
+    return x
+
+
+def _lse(x):
+    m = x.max(axis=1)
+    return m + np.log(np.exp(x - m[:, None]).sum(axis=1))
+
+
+def forward(h, w, y, gate, hit, bias=None, v_real=None, dtype=np.float64, chunk=1024):
+    """Per-row quantities of the forward pass. h [N,K], w [V,K], bias [V] or None, y/gate/hit [N]."""
+    N = h.shape[0]
+    V = w.shape[0]
+    vr = V if v_real is None else v_real
+    lse = np.empty(N, dtype)
+    xy = np.empty(N, dtype)
+    for i in range(0, N, chunk):
+        x = _logits(h[i:i + chunk], w, bias, v_real, dtype)
+        lse[i:i + chunk] = _lse(x)
+        yc = y[i:i + chunk]
+        ok = (yc >= 0) & (yc < vr)
+        xy[i:i + chunk] = np.where(ok, x[np.arange(len(yc)), np.clip(yc, 0, V - 1)], -np.inf)
+    g = gate.astype(dtype)
+    ht = hit.astype(dtype)
+    py = np.exp(xy - lse)
+    P = (1 - g) * py + g * ht
+    clamped = ~(P >= CLAMP_P)
+    Pc = np.where(clamped, CLAMP_P, P)
+    loss = -np.log(Pc)
+    wgt = np.where(clamped, 0.0, (1 - g) * py / Pc).astype(dtype)
+    dgr = np.where(clamped, 0.0, (py - ht) / Pc).astype(dtype)
+    return dict(loss_rows=loss, loss_sum=loss.sum(), lse=lse, xy=xy, py=py, P=P, wgt=wgt, dgr=dgr)
+
+
+def grad_logits(x, lse, y, wgt, go, v_real=None):
+    """G = go*wgt*(softmax - onehot) for a chunk of logits x [n, V]."""
+    p = np.exp(x - lse[:, None])
+    n, V = x.shape
+    vr = V if v_real is None else v_real
+    G = p
+    ok = (y >= 0) & (y < vr)
+    rows = np.arange(n)[ok]
+    G[rows, y[ok]] -= 1.0
+    G *= (go * wgt)[:, None]
+    return G
+
+
+def backward(h, w, y, gate, hit, bias=None, v_real=None, go=1.0, fwd=None, dtype=np.float64, chunk=1024,
+             round_g=None):
+    """Closed-form gradients (dH [N,K], dW [V,K], dBias [V], dGate [N]). `round_g` (a function) is applied to
+    G before the two contractions, e.g. bf16_round to model a bf16 G operand."""
+    if fwd is None:
+        fwd = forward(h, w, y, gate, hit, bias, v_real, dtype, chunk)
+    N, K = h.shape
+    V = w.shape[0]
+    wt = w.astype(dtype)
+    dh = np.empty((N, K), dtype)
+    dw = np.zeros((V, K), dtype)
+    db = np.zeros(V, dtype)
+    for i in range(0, N, chunk):
+        hc = h[i:i + chunk].astype(dtype)
+        x = _logits(hc, w, bias, v_real, dtype)
+        G = grad_logits(x, fwd["lse"][i:i + chunk], y[i:i + chunk], fwd["wgt"][i:i + chunk], go, v_real)
+        db += G.sum(axis=0)
+        if round_g is not None:
+            G = round_g(G.astype(np.float32)).astype(dtype)
+        dh[i:i + chunk] = G @ wt
+        dw += G.T @ hc
+    dgate = go * fwd["dgr"]
+    return dict(dh=dh, dw=dw, dbias=db, dgate=dgate)
+
+
+def eager_ce_part(hn, W, bias, y, c1, g):
+    """torch restatement of `_ce_part` (full2.py:1917-1929) for one [B, T] slab (also accepts [N] rows):
+    lo = head(hn).float() + head_bias.float(); lse = logsumexp(lo); ly = lo.gather(y);
+    py = exp(ly - lse); loss = -log(clamp((1-g) py + g [c1 == y], min=1e-30)).sum()."""
+    import torch
+    lo = (hn @ W.T).float()
+    if bias is not None:
+        lo = lo + bias.float()
+    lse = torch.logsumexp(lo, -1)
+    ly = lo.gather(-1, y[..., None])[..., 0]
+    py = (ly - lse).exp()
+    return -torch.log(((1 - g) * py + g * (c1 == y).to(py.dtype)).clamp(min=1e-30)).sum()
+
+
+def rel_fro(a, b):
+    """Relative Frobenius distance ||a - b|| / ||b|| (0 when both are 0)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    nb = np.linalg.norm(b)
+    na = np.linalg.norm(a - b)
+    return 0.0 if nb == 0 and na == 0 else na / max(nb, 1e-300)

@@ -1,0 +1,85 @@
+"""Shared helpers for the parity tests: run the fused op on the GPU and the oracle on the CPU on the same
+seeded inputs (bf16-rounded operands, fp32 bias)."""
+import numpy as np
+import torch
+
+from oracle import mce_oracle as orc
+
+LOSS_RTOL = 1e-3   # north-star bar on the loss
+GRAD_RTOL = 2e-2   # north-star bar on dH, dW, dBias, dGate (relative Frobenius)
+
+
+def random_case(N, K, V, v_real=None, bias=True, seed=0, w_scale=0.05, gate_mode="mixed", y_mode="uniform"):
+    """Small random case (CPU tensors): h ~ N(0,1), W ~ N(0, w_scale^2), bias ~ N(0,1), gate/hit per mode."""
+    g = torch.Generator().manual_seed(seed)
+    v_real = V if v_real is None else v_real
+    h = torch.randn(N, K, generator=g)
+    w = torch.randn(V, K, generator=g) * w_scale
+    b = torch.randn(V, generator=g) if bias else None
+    if y_mode == "uniform":
+        y = torch.randint(0, v_real, (N,), generator=g)
+    else:
+        y = torch.randint(0, min(8, v_real), (N,), generator=g)
+    c1 = torch.where(torch.rand(N, generator=g) < 0.5, y, torch.randint(0, v_real, (N,), generator=g))
+    c1 = torch.where(torch.rand(N, generator=g) < 0.2, torch.full_like(c1, -1), c1)
+    if gate_mode == "zero":
+        gate = torch.zeros(N)
+    elif gate_mode == "one":
+        gate = torch.full((N,), 0.999)
+    else:
+        gate = torch.sigmoid(torch.randn(N, generator=g)) * (c1 != -1).float()
+    hit = (c1 == y).float()
+    return dict(h=h, w=w, bias=b, y=y, gate=gate, hit=hit, v_real=v_real)
+
+
+def oracle_of(case, go=1.0, dtype=np.float64, round_g=None):
+    """Oracle forward/backward on the bf16-rounded operands of `case`."""
+    h = orc.bf16_round(case["h"].float().numpy())
+    w = orc.bf16_round(case["w"].float().numpy())
+    b = None if case["bias"] is None else case["bias"].float().numpy()
+    y = case["y"].numpy()
+    gate = case["gate"].float().numpy()
+    hit = case["hit"].float().numpy()
+    vr = case["v_real"] if case["v_real"] != case["w"].shape[0] else None
+    fwd = orc.forward(h, w, y, gate, hit, b, vr, dtype)
+    bwd = orc.backward(h, w, y, gate, hit, b, vr, go, fwd, dtype, round_g=round_g)
+    return fwd, bwd
+
+
+def gpu_run(case, dev="cuda", h_dtype=torch.bfloat16, go=1.0, biased=None):
+    """Forward + backward through memarch_amd.fused_ops on the GPU; returns numpy results."""
+    from memarch_amd import fused_ops
+    h = case["h"].to(dev, h_dtype).requires_grad_()
+    w = case["w"].to(dev).requires_grad_()
+    y = case["y"].to(dev)
+    gate = case["gate"].to(dev).requires_grad_()
+    hit = case["hit"].to(dev)
+    biased = case["bias"] is not None or case["v_real"] != case["w"].shape[0] if biased is None else biased
+    if biased:
+        b = (case["bias"] if case["bias"] is not None else torch.zeros(case["w"].shape[0])).to(dev)
+        b.requires_grad_()
+        loss = fused_ops.linear_ce_mix_biased(h, w, b, y, gate, hit, v_real=case["v_real"])
+    else:
+        b = None
+        loss = fused_ops.linear_ce_mix(h, w, y, gate, hit)
+    (loss * go).backward()
+    torch.cuda.synchronize()
+    out = dict(loss=float(loss), dh=h.grad.float().cpu().numpy(), dw=w.grad.float().cpu().numpy(),
+               dgate=gate.grad.float().cpu().numpy())
+    out["dbias"] = None if b is None else b.grad.float().cpu().numpy()
+    return out
+
+
+def assert_parity(got, fwd, bwd, what=""):
+    lref = float(fwd["loss_sum"])
+    lerr = abs(got["loss"] - lref) / max(abs(lref), 1e-30)
+    errs = dict(loss=lerr, dh=orc.rel_fro(got["dh"], bwd["dh"]), dw=orc.rel_fro(got["dw"], bwd["dw"]),
+                dgate=orc.rel_fro(got["dgate"], bwd["dgate"]))
+    if got.get("dbias") is not None:
+        errs["dbias"] = orc.rel_fro(got["dbias"], bwd["dbias"])
+    print(what, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert errs["loss"] <= LOSS_RTOL, (what, errs)
+    for k in ("dh", "dw", "dgate", "dbias"):
+        if k in errs:
+            assert errs[k] <= GRAD_RTOL, (what, k, errs)
+    return errs

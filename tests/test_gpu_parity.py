@@ -1,0 +1,97 @@
+"""GPU parity of the HIP path (libmce.so through memarch_amd.fused_ops) against the CPU oracle.
+
+Bar (north star): loss within 1e-3 relative, dH / dW / dBias / dGate within 2e-2 relative Frobenius, against
+the oracle's fp64 evaluation of the eager formula on the same bf16-rounded operands.
+"""
+import numpy as np
+import pytest
+import torch
+
+from cases import GRAD_RTOL, LOSS_RTOL, assert_parity, gpu_run, oracle_of, random_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+SHAPES = [
+    # (N, K, V, v_real, bias)
+    (256, 128, 512, None, False),      # whole tiles, no bias (the folded-bias drop-in form)
+    (300, 72, 1000, None, True),       # ragged N, K not a multiple of 64, V not a multiple of 256
+    (1, 64, 300, 257, True),           # one row; padded ids masked
+    (777, 520, 2051, 2000, True),      # ragged everything
+    (513, 1024, 4096, 4000, True),     # several K stages and V tiles
+    (64, 2064, 1024, None, False),     # K = d + 16, the augmented layout of full2.py:1848-1850
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "N{}_K{}_V{}_vr{}_b{}".format(*s))
+def test_parity_shapes(shape):
+    N, K, V, vr, bias = shape
+    print(f"case {shape}", flush=True)
+    case = random_case(N, K, V, vr, bias, seed=N + K + V)
+    got = gpu_run(case)
+    fwd, bwd = oracle_of(case)
+    assert_parity(got, fwd, bwd, str(shape))
+
+
+def test_parity_fp32_hidden_and_go():
+    """fp32 h (dH returned in fp32) and a non-unit upstream gradient (the 1/N scaling of full2.py:1971)."""
+    case = random_case(384, 256, 1536, None, True, seed=7)
+    go = 1.0 / 384
+    got = gpu_run(case, h_dtype=torch.float32, go=go)
+    fwd, bwd = oracle_of(case, go=go)
+    assert got["dh"].dtype == np.float32
+    assert_parity(got, fwd, bwd, "fp32 h")
+
+
+def test_parity_k_not_multiple_of_8():
+    """K = 100: the host zero-pads h and w to K = 104; gradients come back at K = 100."""
+    case = random_case(200, 100, 700, None, True, seed=3)
+    got = gpu_run(case)
+    assert got["dh"].shape == (200, 100) and got["dw"].shape == (700, 100)
+    fwd, bwd = oracle_of(case)
+    assert_parity(got, fwd, bwd, "K=100")
+
+
+def test_gate_zero_is_plain_ce():
+    """g = 0: the loss is plain cross-entropy (torch.nn.functional.cross_entropy, reduction='sum')."""
+    case = random_case(256, 256, 1024, None, True, seed=11, gate_mode="zero")
+    got = gpu_run(case)
+    h = torch.from_numpy(np.asarray(case["h"].bfloat16().float())).double()
+    w = case["w"].bfloat16().double()
+    x = h @ w.T + case["bias"].double()
+    ce = torch.nn.functional.cross_entropy(x, case["y"], reduction="sum")
+    assert abs(got["loss"] - float(ce)) <= LOSS_RTOL * abs(float(ce))
+
+
+def test_gate_one_hit_loss_vanishes():
+    """hit = 1 and g -> 1: P -> 1 and the loss -> 0 (bounded by -log(0.999) per row)."""
+    case = random_case(128, 128, 512, None, True, seed=5, gate_mode="one")
+    case["hit"] = torch.ones(128)
+    got = gpu_run(case)
+    assert 0 <= got["loss"] <= 128 * (-np.log(0.999)) * 1.01
+    fwd, bwd = oracle_of(case)
+    assert_parity(got, fwd, bwd, "g->1")
+
+
+def test_clamped_rows_have_zero_gradient():
+    """Huge logit gaps make py underflow below 1e-30 with g = 0: loss = -log(1e-30) = 69.08 per row and the
+    row's gradients vanish (torch clamp backward), as in full2.py:1929."""
+    case = random_case(64, 64, 512, None, False, seed=9, w_scale=3.0, gate_mode="zero")
+    got = gpu_run(case)
+    fwd, bwd = oracle_of(case)
+    assert (~(fwd["P"] >= 1e-30)).sum() > 0, "case must contain clamped rows"
+    assert_parity(got, fwd, bwd, "clamped")
+
+
+def test_skewed_targets():
+    """Many rows share the same few targets (the Zipf head): exercises the target-logit lanes."""
+    case = random_case(1024, 256, 2048, None, True, seed=13, y_mode="head")
+    got = gpu_run(case)
+    fwd, bwd = oracle_of(case)
+    assert_parity(got, fwd, bwd, "skewed")
