@@ -50,7 +50,6 @@ def _rows(t, dtype):
 
 
 def _forward(ctx, h, w, bias, y, gate, hit, v_real):
-    _check_cuda(h, w, bias, y, gate, hit)
     if h.dim() != 2 or w.dim() != 2 or h.shape[1] != w.shape[1]:
         raise ValueError(f"h {tuple(h.shape)} and w {tuple(w.shape)} must be [N, K] and [V, K]")
     n, k = h.shape
@@ -63,6 +62,7 @@ def _forward(ctx, h, w, bias, y, gate, hit, v_real):
             raise ValueError(f"{name} has {t.numel()} elements, expected {n}")
     if bias is not None and (bias.dim() != 1 or bias.shape[0] != v):
         raise ValueError(f"bias must be [V={v}], got {tuple(bias.shape)}")
+    _check_cuda(h, w, bias, y, gate, hit)
     kp = (k + 7) // 8 * 8
     dev = h.device
     hd, wd = _bf16_operand(h, kp), _bf16_operand(w, kp)

@@ -10,8 +10,9 @@ Distributions (per configuration):
          full2.py:1346-1357); padded ids are masked by passing v_real (their bias entry is 0).
   tokens B texts x T tokens drawn from the same Zipf(s) prior (inverse CDF); y[t] = x[t+1], with one extra
          draw for the last target of each text. Config 2 copies earlier spans over ~15% of positions (the
-         repeated-phrase template of memarch_jax/tests/test_model.py:60-70); config 3 continues an earlier
-         bigram for ~40% of tokens.
+         repeated-phrase template of memarch_jax/tests/test_model.py:60-70); config 3 starts a copy run from a
+         random earlier position with probability 0.08 per token (runs of 3-24 tokens), so that ~40% of tokens
+         continue an earlier bigram and the bigram lock fires with the right candidate.
   c1     keys-and-locks pointer candidate (full2.py:1499-1535): the token that followed the previous
          occurrence of the current key in the same text, -1 when none. Configs 0-2 and 4 use the unigram lock;
          config 3 uses the unigram and bigram locks, the longest firing lock winning.
@@ -35,7 +36,7 @@ class Config:
     zipf_s: float
     gate_mu: float
     copy_frac: float      # fraction of positions overwritten by copied earlier spans
-    bigram_frac: float    # fraction of tokens that continue an earlier bigram
+    run_start: float      # per-token probability of starting a copy run from an earlier position
     locks: int            # 1 = unigram lock, 2 = unigram + bigram
     backward: bool
     bf16: bool
@@ -57,7 +58,7 @@ CONFIGS = {
     0: Config(0, 4, 1024, 512, 50257, 50257, 1.1, 0.0, 0.0, 0.0, 1, False, False),
     1: Config(1, 16, 1024, 1024, 50304, 50257, 1.1, 0.0, 0.0, 0.0, 1, True, True),
     2: Config(2, 32, 1024, 2048, 50304, 50257, 1.1, 0.0, 0.15, 0.0, 1, True, True),
-    3: Config(3, 32, 1024, 2048, 50304, 50257, 1.1, 1.0, 0.0, 0.40, 2, True, True),
+    3: Config(3, 32, 1024, 2048, 50304, 50257, 1.1, 1.0, 0.0, 0.08, 2, True, True),
     4: Config(4, 32, 1024, 2048, 131072, 131072, 1.05, 0.0, 0.0, 0.0, 1, True, True),
 }
 
@@ -68,7 +69,7 @@ def scaled(cfg, texts=None, seq=None, d=None, v=None, v_real=None):
     if v_real is None:
         v_real = min(cfg.v_real, v) if v < cfg.v else cfg.v_real
     return Config(cfg.index, texts or cfg.texts, seq or cfg.seq, d or cfg.d, v, v_real, cfg.zipf_s, cfg.gate_mu,
-                  cfg.copy_frac, cfg.bigram_frac, cfg.locks, cfg.backward, cfg.bf16)
+                  cfg.copy_frac, cfg.run_start, cfg.locks, cfg.backward, cfg.bf16)
 
 
 def zipf_probs(v_real, s):
@@ -96,15 +97,17 @@ def token_stream(cfg):
                 dst = s + int(rng.integers(L, T + 1 - s - L))
                 xy[b, dst:dst + L] = xy[b, s:s + L]
                 copied += L
-    if cfg.bigram_frac > 0:
+    if cfg.run_start > 0:
         for b in range(B):
             row = xy[b]
-            nxt = {}
+            src, left = -1, 0
             for t in range(2, T + 1):
-                key = (int(row[t - 2]), int(row[t - 1]))
-                if key in nxt and rng.random() < cfg.bigram_frac:
-                    row[t] = row[nxt[key]]
-                nxt[key] = t
+                if left == 0 and rng.random() < cfg.run_start:
+                    src, left = int(rng.integers(0, t - 1)), int(rng.integers(3, 25))
+                if left > 0:
+                    row[t] = row[src]
+                    src += 1
+                    left -= 1
     return xy
 
 

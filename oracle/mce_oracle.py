@@ -114,9 +114,11 @@ def eager_ce_part(hn, W, bias, y, c1, g):
     lo = head(hn).float() + head_bias.float(); lse = logsumexp(lo); ly = lo.gather(y);
     py = exp(ly - lse); loss = -log(clamp((1-g) py + g [c1 == y], min=1e-30)).sum()."""
     import torch
-    lo = (hn @ W.T).float()
+    lo = hn @ W.T
+    up = torch.promote_types(lo.dtype, torch.float32)   # `.float()` of the reference; fp64 stays fp64
+    lo = lo.to(up)
     if bias is not None:
-        lo = lo + bias.float()
+        lo = lo + bias.to(up)
     lse = torch.logsumexp(lo, -1)
     ly = lo.gather(-1, y[..., None])[..., 0]
     py = (ly - lse).exp()

@@ -1,0 +1,64 @@
+"""The C ABI library: loads, exports every symbol include/mce.h declares, and rejects bad arguments on the host
+(argument checks run before any HIP call, so these need no GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from memarch_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mce.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    return re.findall(r"MCE_API\s+[\w\s\*]+?\b(mce_\w+)\s*\(", src)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libmce.so not built")
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must mirror the header"
+
+
+def test_version_and_errors(lib):
+    assert lib.mce_version() >= 100
+    for code in range(5):
+        assert lib.mce_error_string(code)
+
+
+def test_workspace_sizes(lib):
+    N, K, V = 32768, 2048, 50304
+    vp = (V + 255) // 256 * 256
+    assert lib.mce_bwd_ws_bytes(N, K, V) >= 2 * N * vp
+    assert lib.mce_fwd_ws_bytes(N, K, V) >= 8 * N * (vp // 256)
+    assert lib.mce_fwd_ws_bytes(-1, K, V) == 0
+
+
+def test_argument_checks_need_no_gpu(lib):
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256   # 256-byte aligned host address
+    args = lambda N, K, V, vr, ldh, ldw: (p, ldh, p, ldw, None, p, p, p, N, K, V, vr, p, p, p, p, p, p, 1 << 30, None)
+    assert lib.mce_fwd(*args(16, 7, 32, 32, 7, 7)) == 2          # K not a multiple of 8
+    assert lib.mce_fwd(*args(16, 8, 32, 33, 8, 8)) == 1          # V_real > V
+    assert lib.mce_fwd(*args(16, 8, 32, 0, 8, 8)) == 1           # V_real < 1
+    assert lib.mce_fwd(*args(16, 16, 32, 32, 8, 16)) == 1        # ldh < K
+    assert lib.mce_fwd(*args(-1, 8, 32, 32, 8, 8)) == 1          # negative N
+    a = list(args(16, 8, 32, 32, 8, 8))
+    a[18] = 16                                                   # workspace too small
+    assert lib.mce_fwd(*a) == 3
+    a = list(args(16, 8, 32, 32, 8, 8))
+    a[0] = p + 2                                                 # misaligned H
+    assert lib.mce_fwd(*a) == 2
+    assert lib.mce_bwd_dweight(p, 8, 16, 8, 32, p, 4, p, 1 << 30, None) == 1   # lddw < K

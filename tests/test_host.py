@@ -1,0 +1,38 @@
+"""Host-side behaviour of memarch_amd.fused_ops that needs no GPU: no CPU fallback, argument validation,
+the reference-compatible call surface."""
+import inspect
+
+import pytest
+import torch
+
+from memarch_amd import fused_ops
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    h = torch.randn(4, 8)
+    w = torch.randn(16, 8)
+    y = torch.zeros(4, dtype=torch.long)
+    with pytest.raises(ValueError, match="GPU only"):
+        fused_ops.linear_ce_mix(h, w, y, torch.zeros(4), torch.zeros(4))
+
+
+def test_reference_signatures():
+    # fused_ops.py:139 forward(ctx, h, w, y, gate, hit, chunk); :166 linear_ce_mix(h, w, y, gate, hit, chunk=4096)
+    assert list(inspect.signature(fused_ops._LinearCEMix.forward).parameters) == \
+        ["ctx", "h", "w", "y", "gate", "hit", "chunk"]
+    sig = inspect.signature(fused_ops.linear_ce_mix)
+    assert list(sig.parameters) == ["h", "w", "y", "gate", "hit", "chunk"]
+    assert sig.parameters["chunk"].default == 4096
+
+
+def test_shape_validation_before_any_launch():
+    meta = dict(device="meta")
+    with pytest.raises(ValueError, match="must be"):
+        fused_ops._forward(None, torch.randn(4, 8, **meta), torch.randn(16, 9, **meta), None,
+                           torch.zeros(4, **meta), torch.zeros(4, **meta), torch.zeros(4, **meta), None)
+    with pytest.raises(ValueError, match="v_real"):
+        fused_ops._forward(None, torch.randn(4, 8, **meta), torch.randn(16, 8, **meta), None,
+                           torch.zeros(4, **meta), torch.zeros(4, **meta), torch.zeros(4, **meta), 17)
+    with pytest.raises(ValueError, match="gate"):
+        fused_ops._forward(None, torch.randn(4, 8, **meta), torch.randn(16, 8, **meta), None,
+                           torch.zeros(4, **meta), torch.zeros(3, **meta), torch.zeros(4, **meta), None)

@@ -1,0 +1,44 @@
+"""Keys-and-locks pointer candidates (full2.py:1499-1535; induct.py:17-43): the brute-force scan, the
+stable-argsort restatement and the workload generator's producer agree exactly (integer outputs)."""
+import numpy as np
+import pytest
+
+from memarch_amd import workloads as wl
+from oracle import induct_oracle as io
+
+
+def _texts(seed, B=3, T=64, V=9):
+    r = np.random.default_rng(seed)
+    x = r.integers(0, V, (B, T))
+    x[0, 30:40] = x[0, 5:15]        # a repeated fragment (the template of test_heads.py:140-144)
+    x[1, 20:26] = 4                 # "a a a"
+    return x, V
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_sorted_scan_equals_brute_force(seed):
+    x, V = _texts(seed)
+    cb, ob = io.brute_force(x, V, 3)
+    cs, os_ = io.sorted_scan(x, V, 3)
+    np.testing.assert_array_equal(ob, os_)
+    np.testing.assert_array_equal(cb * ob, cs * os_)
+
+
+@pytest.mark.parametrize("locks", [1, 2])
+@pytest.mark.parametrize("seed", range(5))
+def test_generator_matches_oracle(locks, seed):
+    x, V = _texts(seed)
+    cb, ob = io.brute_force(x, V, locks)
+    np.testing.assert_array_equal(wl.pointer_candidates(x, locks), io.c1_of(cb, ob, none=-1))
+
+
+def test_longest_lock_wins_and_causal():
+    x = np.array([[1, 2, 3, 1, 2, 5, 1, 2, 3]])
+    cand, on = io.brute_force(x, 6, 3)
+    # t=7 (token 2, pair (1,2)): pair lock fires (last pair at t=4 -> next token x[5]=5), unigram is off
+    assert on[0, 7, 1] and not on[0, 7, 0] and cand[0, 7, 1] == 5
+    # t=8 (triple (1,2,3) seen at t=2 -> x[3] = 1)
+    assert on[0, 8, 2] and cand[0, 8, 2] == 1 and not on[0, 8, :2].any()
+    # causality: a candidate index never exceeds t
+    c1 = wl.pointer_candidates(x, 2)
+    assert c1[0, 0] == -1 and c1[0, 1] == -1
