@@ -5,32 +5,47 @@
 // GEMMs (fused_ops.py:153-154). The formula is the reference's eager one (full2.py:1917-1929).
 //
 // Four contractions share one bf16 MFMA mainloop (gemm_tile): a 256x256 output tile per workgroup of
-// 4 wave64s (2x2, 128x128 per wave, v_mfma_f32_32x32x16_bf16), K staged through LDS 64 at a time with
-// two LDS stages and a register prefetch of the next stage. Operands come in one of two global layouts:
-//   NAT: element (m, k) at p[m*ld + k]   (K contiguous, loaded as 16-byte rows)
-//   TRN: element (m, k) at p[k*ld + m]   (M contiguous, loaded as 8x8 blocks and transposed in registers)
-// Both land in LDS as [m][64 k] rows of 128 bytes with an XOR swizzle of the 16-byte chunk index, so the
-// fragment reads (ds_read_b128, one row and 8 consecutive k per lane) are bank-conflict free.
+// 4 wave64s (2x2, 128x128 per wave, v_mfma_f32_32x32x16_bf16), K streamed through LDS 64 at a time in two
+// LDS stages (2 x 64 KiB). Global memory goes straight to LDS (buffer_load ... lds, 16 bytes per lane, no
+// staging registers); the next stage's loads are in flight while the current stage is multiplied.
 //
-//   forward     S^T = W H^T  (A=W NAT, B=H NAT) -> per-tile row max / sum-exp, target logit; merge -> lse, loss
-//   logits-grad S^T = W H^T recomputed          -> G = go*wgt*(softmax - onehot) as bf16 [N, Vp]; dBias partials
-//   dhidden     dH  = G W    (A=G NAT, B=W TRN)
-//   dweight     dW  = G^T H  (A=G TRN, B=H TRN)
-// The N x V logits never reach memory; G is the only N x V intermediate (bf16).
+// Every operand is a logical [M, K] matrix with K contiguous: element (m, k) at p[m*ld + k], or, in the
+// K-blocked layout of the internal buffers, at p[(k/256)*blk + m*256 + k%256] (256-wide K blocks, each a
+// contiguous [M][256] panel). The LDS image of one stage is [256 m][64 k] with 128-byte rows and the
+// 16-byte chunk index XOR-swizzled by the row, so fragment reads (ds_read_b128) are bank-conflict free.
+// Elements outside an operand's extent read as zero (out-of-range buffer offsets), so partial tiles need
+// no special path.
+//
+//   forward     S^T = W H^T           -> per-tile row max / sum-exp, target logit; merge -> lse, loss, wgt, dgr
+//   logits-grad S^T = W H^T recomputed -> G = go*wgt*(softmax - onehot) (bf16) written twice through LDS:
+//                                         G (v contiguous, for dH) and G^T (n contiguous, for dW); dBias partials
+//   dhidden     dH  = G   . Wt  with Wt = W^T (K-blocked copy made by k_transpose_blocked)
+//   dweight     dW  = G^T . Ht  with Ht = H^T (K-blocked copy)
+// The N x V logits never reach memory; G is the only N x V intermediate.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
 
 #include "../../include/mce.h"
 
-#define MCE_VERSION 100
+#define MCE_VERSION 300
+
+typedef int32_t mce_i32x4 __attribute__((ext_vector_type(4)));
+// The LLVM intrinsic behind `buffer_load_dword... lds`: (resource, LDS base, bytes per lane, per-lane offset,
+// scalar offset, immediate offset, cache policy).
+__device__ void buffer_load_lds(mce_i32x4 rsrc, __attribute__((address_space(3))) uint32_t* lds, int size,
+                                int voffset, int soffset, int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
 
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef mce_i32x4 i32x4;
+#define LDS_AS __attribute__((address_space(3)))
 
 constexpr int BM = 256;              // tile rows (A operand rows)
 constexpr int BN = 256;              // tile cols (B operand rows)
@@ -39,111 +54,146 @@ constexpr int NTHREADS = 256;        // 4 wave64s
 constexpr int OP_BYTES = BM * BK * 2;             // one operand, one stage: 32 KiB
 constexpr int STAGE_BYTES = 2 * OP_BYTES;         // A + B
 constexpr int LDS_BYTES = 2 * STAGE_BYTES;        // two stages: 128 KiB (gfx950 has 160 KiB per CU)
+constexpr int LOADS_PER_STAGE = 2 * (OP_BYTES / 1024) / 4;  // direct-load instructions per wave per stage: 16
+constexpr int BLK = 256;             // block width of the K-blocked layout
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float CLAMP_P = 1e-30f;    // full2.py:1929, fused_ops.py:125
 
-enum { NAT = 0, TRN = 1 };
-
 struct Operand {
   const uint16_t* p;  // bf16 bits
-  int64_t ld;         // leading dimension in elements
-  int64_t mext;       // valid extent along M (rows of the logical [M, K] operand)
+  int64_t ld;         // row stride in elements (256 in the K-blocked layout)
+  int64_t mext;       // valid extent along M
   int64_t kext;       // valid extent along K
+  int64_t blk;        // 0, or the element distance between consecutive 256-wide K blocks
 };
 
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone). gfx9 encoding: vmcnt[3:0] and vmcnt[5:4] at bits 15:14.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int SG_MFMA = 0x8, SG_DS_READ = 0x100;
+
 // ---------------------------------------------------------------------------------------------------------
-// LDS layout: a [256][64] bf16 operand tile is 256 rows of 128 bytes = 8 chunks of 16 bytes. The chunk index
-// is XORed with swz(row) so that 8 (or 16) consecutive rows read at the same logical chunk hit distinct banks.
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ swz(row)) << 4); }
+// Direct global -> LDS loads through a buffer resource (buffer_load_lds, declared above): lane l of one
+// instruction writes 16 bytes at LDS m0 + 16*l. A lane whose offset is >= num_records reads zeros without
+// touching memory, which is how every out-of-range element of a partial tile is produced.
 
-// Global -> registers for one stage of one operand (8 x 16 bytes per thread).
-template <int MODE>
-__device__ __forceinline__ void stage_load(u32x4 (&r)[8], const Operand& op, int64_t m0, int64_t k0, int t) {
-  if constexpr (MODE == NAT) {
-    const int c = t & 7;
-    const int64_t k = k0 + c * 8;
-    const bool kok = k < op.kext;
+constexpr int OOB = 0x7FFFFFFF;                 // num_records of every resource, and the out-of-range offset
+constexpr int BUF_DWORD3 = 0x00020000;          // gfx9 buffer resource word 3 (raw, 32-bit data format)
+
+__device__ __forceinline__ i32x4 make_rsrc(uint64_t addr) {
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(addr >> 32) & 0xFFFFu));
+  r[2] = OOB;
+  r[3] = BUF_DWORD3;
+  return r;
+}
+
+// LDS operand image: byte (row m, 16-byte chunk c) at m*128 + ((c ^ swz(m)) << 4). Eight consecutive rows
+// read at one logical chunk land on eight distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int m) { return (m ^ (m >> 3)) & 7; }
+
+// Per-tile state of one operand stream. Stage s of this wave's 8 load instructions (instruction i = wave*8+j
+// of the stage's 32 covers 1 KiB = 8 rows of the LDS image) reads base + offset(s) + voff[j], or zeros when
+// the chunk's local k index kloc[j] is past the valid extent (kloc is OOB for rows outside the operand).
+struct Stream {
+  uint64_t base;   // bytes: element (m0, 0)
+  int64_t blk;     // element distance between K blocks, or 0
+  int64_t kext;
+  int voff[8];
+  int kloc[8];
+};
+
+__device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
+  Stream st;
+  st.kext = op.kext;
+  st.blk = op.blk;
+  st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
+  const int rsub = lane >> 3, pc = lane & 7;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t m = m0 + i * 32 + (t >> 3);
-      if (kok && m < op.mext) r[i] = *reinterpret_cast<const u32x4*>(op.p + m * op.ld + k);
-      else r[i] = u32x4{0u, 0u, 0u, 0u};
-    }
-  } else {
-    const int mb = t & 31, kb = t >> 5;
-    const int64_t m = m0 + mb * 8;
-    const bool mok = m < op.mext;  // mext % 8 == 0: a chunk of 8 is all in or all out
+  for (int j = 0; j < 8; ++j) {
+    const int row = (wave * 8 + j) * 8 + rsub;
+    const int c = pc ^ swz(row);
+    st.voff[j] = (int)(row * op.ld * 2) + c * 16;
+    st.kloc[j] = (m0 + row < op.mext) ? c * 8 : OOB;
+  }
+  return st;
+}
+
+// Resource and K limit of one stage of a stream.
+struct StageSrc {
+  i32x4 rsrc;
+  int klim;
+};
+__device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage) {
+  const int64_t k0 = (int64_t)stage * BK;
+  const int64_t klim64 = st.kext - k0;
+  const uint64_t off = st.blk ? (uint64_t)((k0 >> 8) * st.blk + (k0 & (BLK - 1))) * 2 : (uint64_t)k0 * 2;
+  return StageSrc{make_rsrc(st.base + off), klim64 < 0 ? 0 : (klim64 > BK ? BK : (int)klim64)};
+}
+
+// Load j (0..7) of this wave for one stage into the operand image at `s`.
+__device__ __forceinline__ void issue_one(const Stream& st, const StageSrc& src, int j, char* s, int wave) {
+  const int vo = st.kloc[j] < src.klim ? st.voff[j] : OOB;
+  buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(s + (wave * 8 + j) * 1024), 16, vo, 0, 0, 0);
+}
+
+// Issue this wave's 8 loads of stage `stage` into the operand image at `s`.
+__device__ __forceinline__ void issue_stage(const Stream& st, int stage, char* s, int wave) {
+  const StageSrc src = stage_src(st, stage);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t k = k0 + kb * 8 + i;
-      if (mok && k < op.kext) r[i] = *reinterpret_cast<const u32x4*>(op.p + k * op.ld + m);
-      else r[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int j = 0; j < 8; ++j) issue_one(st, src, j, s, wave);
+}
+
+// MFMA operand fragment of v_mfma_f32_32x32x16_bf16 for the 32 rows mbase..mbase+31 of the LDS operand image
+// and the K slice kk*16..kk*16+15: lane l holds element (mbase + l%32, kk*16 + 8*(l/32) + 0..7).
+__device__ __forceinline__ bf16x8 read_frag(const char* s, int mbase, int kk, int lane) {
+  const int row = mbase + (lane & 31);
+  const int c = kk * 2 + (lane >> 5);
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(s + row * 128 + ((c ^ swz(row)) << 4)));
+}
+
+__device__ __forceinline__ void read_frags(const char* stage, int wm, int wn, int kk, int lane, bf16x8 (&a)[4],
+                                           bf16x8 (&b)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = read_frag(stage, wm * 128 + i * 32, kk, lane);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b[j] = read_frag(stage + OP_BYTES, wn * 128 + j * 32, kk, lane);
+}
+
+__device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4], const bf16x8 (&b)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+// Interleave the current scheduling region: one LDS read between two MFMAs.
+__device__ __forceinline__ void sched_slice() {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
   }
 }
 
-// Registers -> LDS for one stage of one operand. TRN transposes its 8x8 bf16 block on the way.
-template <int MODE>
-__device__ __forceinline__ void stage_store(char* lds, const u32x4 (&r)[8], int t) {
-  if constexpr (MODE == NAT) {
-    const int c = t & 7;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = i * 32 + (t >> 3);
-      *reinterpret_cast<u32x4*>(lds + lds_off(row, c)) = r[i];
-    }
-  } else {
-    // r[i] holds k = kb*8+i, m = mb*8 + 0..7 (two bf16 per dword). Output row m = mb*8+j holds k = kb*8 + 0..7.
-    const int mb = t & 31, kb = t >> 5;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      u32x4 lo, hi;  // lo: m = 2w, hi: m = 2w+1; dword w2 holds k = 2*w2, 2*w2+1
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) {
-        const uint32_t a = r[2 * w2][w], b = r[2 * w2 + 1][w];
-        lo[w2] = (a & 0xFFFFu) | (b << 16);
-        hi[w2] = (a >> 16) | (b & 0xFFFF0000u);
-      }
-      const int row = mb * 8 + 2 * w;
-      *reinterpret_cast<u32x4*>(lds + lds_off(row, kb)) = lo;
-      *reinterpret_cast<u32x4*>(lds + lds_off(row + 1, kb)) = hi;
-    }
-  }
-}
-
-__device__ __forceinline__ bf16x8 frag(const char* lds, int row, int chunk) {
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + lds_off(row, chunk)));
-}
-
-// One LDS stage of MFMAs for this wave's 128x128 sub-tile.
-// v_mfma_f32_32x32x16_bf16: lane l supplies A[row l%32][k 8*(l/32)..+8] and B[col l%32][same k]; the same k
-// permutation on both sides leaves the dot products unchanged.
-__device__ __forceinline__ void stage_mma(f32x16 (&acc)[4][4], const char* As, const char* Bs, int wm, int wn,
-                                          int lane) {
-  const int lr = lane & 31, lh = lane >> 5;
-#pragma unroll
-  for (int kk = 0; kk < BK / 16; ++kk) {
-    bf16x8 a[4], b[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = frag(As, wm * 128 + i * 32 + lr, kk * 2 + lh);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = frag(Bs, wn * 128 + j * 32 + lr, kk * 2 + lh);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-  }
-}
-
-// C[m0:m0+256, n0:n0+256] = A[m, :] . B[n, :] over k < A.kext (== B.kext), fp32 accumulation.
+// C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over k < kloop, fp32 accumulation.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
 //                                              [wn*128 + nj*32 + lane%32].
-template <int AM, int BMODE>
-__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int64_t m0, int64_t n0, char* lds,
-                                          f32x16 (&acc)[4][4]) {
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+// Pipeline per 64-wide K stage (two LDS buffers): the fragments of K slice kk+1 are read while slice kk is
+// multiplied. Before the last slice's MFMAs every wave waits for the next stage's loads and passes one
+// barrier, then reads the next stage's first slice and issues the loads of the stage after next into the
+// buffer it has just finished. Loads past the last stage read nothing (all lanes out of range); the final
+// wait + barrier lets the caller reuse LDS as soon as this returns.
+__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int64_t kloop, int64_t m0, int64_t n0,
+                                          char* lds, f32x16 (&acc)[4][4]) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
   const int wm = wave >> 1, wn = wave & 1;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -152,29 +202,52 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int64_t kext = A.kext;
-  const int nk = (int)((kext + BK - 1) / BK);
-  u32x4 ra[8], rb[8];
-  stage_load<AM>(ra, A, m0, 0, t);
-  stage_load<BMODE>(rb, B, n0, 0, t);
-  stage_store<AM>(lds, ra, t);
-  stage_store<BMODE>(lds + OP_BYTES, rb, t);
+  const Stream sa = make_stream(A, m0, wave, lane);
+  const Stream sb = make_stream(B, n0, wave, lane);
+  const int nk = (int)((kloop + BK - 1) / BK);
+  issue_stage(sa, 0, lds, wave);
+  issue_stage(sb, 0, lds + OP_BYTES, wave);
+  issue_stage(sa, 1, lds + STAGE_BYTES, wave);
+  issue_stage(sb, 1, lds + STAGE_BYTES + OP_BYTES, wave);
+  wait_vmcnt<LOADS_PER_STAGE>();
   __syncthreads();
+
+  bf16x8 fa[2][4], fb[2][4];
+  read_frags(lds, wm, wn, 0, lane, fa[0], fb[0]);
   for (int kt = 0; kt < nk; ++kt) {
     char* cur = lds + (kt & 1) * STAGE_BYTES;
     char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      stage_load<AM>(ra, A, m0, (int64_t)(kt + 1) * BK, t);
-      stage_load<BMODE>(rb, B, n0, (int64_t)(kt + 1) * BK, t);
-    }
-    stage_mma(acc, cur, cur + OP_BYTES, wm, wn, lane);
-    if (more) {
-      stage_store<AM>(nxt, ra, t);
-      stage_store<BMODE>(nxt + OP_BYTES, rb, t);
-    }
+    read_frags(cur, wm, wn, 1, lane, fa[1], fb[1]);
+    mma16(acc, fa[0], fb[0]);
+    sched_slice();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, wm, wn, 2, lane, fa[0], fb[0]);
+    mma16(acc, fa[1], fb[1]);
+    sched_slice();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(cur, wm, wn, 3, lane, fa[1], fb[1]);
+    mma16(acc, fa[0], fb[0]);
+    sched_slice();
+    __builtin_amdgcn_sched_barrier(0);
+    // stage kt is fully in registers; stage kt+1 must have landed before anyone reads it
+    wait_vmcnt<0>();
     __syncthreads();
+    // last slice, interleaved in source order and pinned by scheduling barriers:
+    // (next stage's fragment read,) MFMA, load, ...
+    const StageSrc ga = stage_src(sa, kt + 2), gb = stage_src(sb, kt + 2);
+#pragma unroll
+    for (int idx = 0; idx < 16; ++idx) {
+      if (idx < 4) fa[0][idx] = read_frag(nxt, wm * 128 + idx * 32, 0, lane);
+      else if (idx < 8) fb[0][idx - 4] = read_frag(nxt + OP_BYTES, wn * 128 + (idx - 4) * 32, 0, lane);
+      acc[idx >> 2][idx & 3] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][idx >> 2], fb[1][idx & 3], acc[idx >> 2][idx & 3], 0, 0, 0);
+      if (idx < 8) issue_one(sa, ga, idx, cur, wave);
+      else issue_one(sb, gb, idx - 8, cur + OP_BYTES, wave);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+  wait_vmcnt<0>();
+  __syncthreads();
 }
 
 // Block id -> (tile_m, tile_n). Workgroups are dispatched round-robin over the 8 XCDs (block b on XCD b%8);
@@ -229,12 +302,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgp
 void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
                  int64_t N, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, float* __restrict__ part_m,
                  float* __restrict__ part_s, float* __restrict__ xy) {
-  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, 8, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile<NAT, NAT>(Wop, Hop, v0, n0, lds, acc);
+  gemm_tile(Wop, Hop, Wop.kext, v0, n0, lds, acc);
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
@@ -363,19 +436,27 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Logits-grad tile: recompute S^T for the tile, G = go*wgt*(exp(x - lse) - [v = y]) -> bf16 G[n, v];
-// column sums of G (over this tile's 256 rows) -> dbias_part[tn, v].
+// Logits-grad tile: recompute S^T for the tile, G = go*wgt*(exp(x - lse) - [v = y]), column sums of G over the
+// tile's 256 rows -> dbias_part[tn, v], and G rounded to bf16 into both K-blocked layouts:
+//   G   element (n, v) at G[(v/256)*Np*256 + n*256 + v%256]    (for dH, reduction over v)
+//   Gt  element (v, n) at Gt[(n/256)*Vp*256 + v*256 + n%256]   (for dW, reduction over n)
+// Each tile is one contiguous 128 KiB block of either buffer. The tile is staged in LDS as [256 n][256 v]
+// (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))); G rows are copied out with ds_read_b128, Gt rows are
+// assembled with ds_read_b64_tr_b16 (each 16-lane group turns a 4x16 [n][v] block into 16 columns of 4 n).
+// gsw makes both reads bank-conflict free and leaves the staging writes at most 2-way conflicted.
+__device__ __forceinline__ int gsw(int n) { return ((n & 3) << 1) | ((n >> 2) & 1); }
+
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
                 const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ go,
-                int64_t N, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, uint16_t* __restrict__ G, int64_t ldg,
-                float* __restrict__ dbias_part) {
-  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+                int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n,
+                uint16_t* __restrict__ G, uint16_t* __restrict__ Gt, float* __restrict__ dbias_part) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, 8, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile<NAT, NAT>(Wop, Hop, v0, n0, lds, acc);
+  gemm_tile(Wop, Hop, Wop.kext, v0, n0, lds, acc);
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
@@ -413,26 +494,9 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           if (acc_row(mi, r, lh) == (int)tl) acc[mi][nj][r] -= cn[nj];
     }
   }
-  // store G: each lane holds 4 consecutive v (r%4) for one row n -> one 8-byte store
-#pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
-    const int64_t n = n0 + wn * 128 + nj * 32 + lr;
-    if (n < N) {
-      uint16_t* grow = G + n * ldg;
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t v = v_lane + acc_row(mi, 4 * q, lh);
-          u32x2 pk;
-          pk[0] = pack_bf16x2(acc[mi][nj][4 * q + 0], acc[mi][nj][4 * q + 1]);
-          pk[1] = pack_bf16x2(acc[mi][nj][4 * q + 2], acc[mi][nj][4 * q + 3]);
-          *reinterpret_cast<u32x2*>(grow + v) = pk;
-        }
-    }
-  }
+
   if (dbias_part != nullptr) {
-    // column sums over n: in-lane over nj, then over the 32 lanes and the two wn waves through LDS
+    // column sums over n (fp32, before rounding): in-lane over nj, then over the 32 lanes and the two wn waves
     float* red = reinterpret_cast<float*>(lds);  // [4 waves][128 rows][33]
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -450,7 +514,56 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 #pragma unroll
       for (int l = 0; l < 32; ++l) s += src[l];
     }
-    dbias_part[(int64_t)tn * ldg + v0 + t] = s;
+    dbias_part[(int64_t)tn * Vp + v0 + t] = s;
+    __syncthreads();
+  }
+
+  // stage the bf16 tile: lane holds 4 consecutive v (r%4) of one row n -> 8-byte LDS writes
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) {
+    const int nl = wn * 128 + nj * 32 + lr;
+    char* row = lds + nl * 512;
+    const int sw = gsw(nl) << 4;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int vl = wm * 128 + acc_row(mi, 4 * q, lh);
+        u32x2 pk;
+        pk[0] = pack_bf16x2(acc[mi][nj][4 * q + 0], acc[mi][nj][4 * q + 1]);
+        pk[1] = pack_bf16x2(acc[mi][nj][4 * q + 2], acc[mi][nj][4 * q + 3]);
+        *reinterpret_cast<u32x2*>(row + ((vl * 2) ^ sw)) = pk;
+      }
+  }
+  __syncthreads();
+
+  // G block of this tile: [256 n][256 v], contiguous; thread t copies 16-byte chunks t, t+256, ...
+  char* gblk = reinterpret_cast<char*>(G + ((int64_t)tm * Np + n0) * BLK);
+#pragma unroll 8
+  for (int i = 0; i < 32; ++i) {
+    const int id = i * 256 + t;
+    const int nl = id >> 5, c = id & 31;
+    const u32x4 val = *reinterpret_cast<const u32x4*>(lds + nl * 512 + ((c ^ gsw(nl)) << 4));
+    *reinterpret_cast<u32x4*>(gblk + (int64_t)id * 16) = val;
+  }
+  // Gt block of this tile: [256 v][256 n], contiguous. Task id -> (16 v from v16, 8 n from n8); 16-lane group
+  // gi handles tasks gi, gi+16, ...; lane p of the group ends with (v16 + p, n8 .. n8+7).
+  char* gtblk = reinterpret_cast<char*>(Gt + ((int64_t)tn * Vp + v0) * BLK);
+  const int gi = t >> 4, p = t & 15;
+#pragma unroll 4
+  for (int i = 0; i < 32; ++i) {
+    const int id = i * 16 + gi;
+    const int n8 = (id & 31) * 8, v16 = (id >> 5) * 16;
+    bf16x4 h[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int nl = n8 + 4 * q + (p >> 2);
+      const int vl = v16 + 4 * (p & 3);
+      h[q] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (bf16x4 LDS_AS*)(lds + nl * 512 + ((vl * 2) ^ (gsw(nl) << 4))));
+    }
+    const bf16x8 o{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+    *reinterpret_cast<bf16x8*>(gtblk + (int64_t)(v16 + p) * 512 + n8 * 2) = o;
   }
 }
 
@@ -470,17 +583,51 @@ __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, co
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// K-blocked transpose: dst element (c, r) at dst[(r/256)*C*256 + c*256 + r%256] = src[r*ld + c] for r < R,
+// 0 for R <= r < (grid rows); c < C (C % 8 == 0). One workgroup per 64 x 64 tile, staged through LDS.
+__global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __restrict__ src, int64_t ld, int64_t R,
+                                                           int64_t C, uint16_t* __restrict__ dst) {
+  __shared__ uint16_t tile[64][66];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rl = (t >> 3) + 32 * h, cl = (t & 7) * 8;
+    const int64_t r = r0 + rl, c = c0 + cl;
+    u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < R && c < C) v = *reinterpret_cast<const u16x8*>(src + r * ld + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[rl][cl + e] = v[e];
+  }
+  __syncthreads();
+  // output: 64 rows c, each 64 consecutive r = 8 chunks of 8; lanes take consecutive c for conflict-free reads
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int id = t + 256 * h;
+    const int cl = id & 63, rq = id >> 6;
+    const int64_t c = c0 + cl;
+    if (c < C) {
+      u16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = tile[rq * 8 + e][cl];
+      const int64_t r = r0 + rq * 8;
+      *reinterpret_cast<u16x8*>(dst + (r >> 8) * C * BLK + c * BLK + (r & (BLK - 1))) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc).
-template <int AM, int BMODE, bool OUT_BF16>
+template <bool OUT_BF16>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
-void k_gemm(Operand A, Operand B, int64_t M, int64_t Nc, int tiles_m, int tiles_n, void* __restrict__ C,
-            int64_t ldc) {
-  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+void k_gemm(Operand A, Operand B, int64_t kloop, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
+            void* __restrict__ C, int64_t ldc) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, 8, tm, tn);
+  tile_coords(tiles_m, tiles_n, group, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile<AM, BMODE>(A, B, m0, n0, lds, acc);
+  gemm_tile(A, B, kloop, m0, n0, lds, acc);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
 #pragma unroll
@@ -526,19 +673,26 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
   return w;
 }
 
+// Backward workspace (Np = N and Vp = V rounded up to 256):
+//   G   [Vp/256][Np][256] bf16, Gt [Np/256][Vp][256] bf16 (written by k_bwd_grad)
+//   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
+//   dbias_part [Np/256][Vp] fp32
 struct BwdWs {
-  uint16_t* G;
+  uint16_t *G, *Gt, *Wt, *Ht;
   float* dbias_part;
-  int64_t ldg;
+  int64_t np, vp;
   size_t bytes;
 };
-BwdWs bwd_ws_layout(char* base, int64_t N, int64_t V) {
-  const int64_t vp = cdiv(V, BM) * BM;
+BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   BwdWs w{};
+  w.np = cdiv(N, BLK) * BLK;
+  w.vp = cdiv(V, BLK) * BLK;
   size_t off = 0;
-  w.ldg = vp;
-  w.G = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * vp * N);
-  w.dbias_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * vp * cdiv(N, BN));
+  w.G = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * w.np);
+  w.Gt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * w.np);
+  w.Wt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * K);
+  w.Ht = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.np * K);
+  w.dbias_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.vp * (w.np / BLK));
   w.bytes = off;
   return w;
 }
@@ -550,7 +704,9 @@ int check_common(const void* H, int64_t ldh, const void* W, int64_t ldw, int64_t
   if (ldh < K || ldw < K) return MCE_EINVAL;
   if (K % 8 || ldh % 8 || ldw % 8) return MCE_EALIGN;
   if (!aligned16(H) || !aligned16(W)) return MCE_EALIGN;
+  // tile counts fit in int; per-lane buffer offsets (256 rows of a row-major operand) stay below 2^30
   if (cdiv(N, BN) * cdiv(V, BM) > INT32_MAX || cdiv(K, BN) * cdiv(V, BM) > INT32_MAX) return MCE_EINVAL;
+  if ((int64_t)BM * (ldh > ldw ? ldh : ldw) * 2 > (int64_t(1) << 30)) return MCE_EINVAL;
   return MCE_OK;
 }
 
@@ -589,9 +745,8 @@ size_t mce_fwd_ws_bytes(int64_t N, int64_t K, int64_t V) {
 }
 
 size_t mce_bwd_ws_bytes(int64_t N, int64_t K, int64_t V) {
-  (void)K;
-  if (N < 0 || V <= 0) return 0;
-  return bwd_ws_layout(nullptr, N, V).bytes;
+  if (N < 0 || V <= 0 || K <= 0) return 0;
+  return bwd_ws_layout(nullptr, N, K, V).bytes;
 }
 
 int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
@@ -610,7 +765,7 @@ int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
   const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K}, Hop{H, ldh, N, K};
+  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, N, V, V_real, tv, tn,
                      w.part_m, w.part_s, w.xy);
   if ((rc = launch_status())) return rc;
@@ -636,15 +791,15 @@ int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64
     return launch_status();
   }
   if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows)) return MCE_EINVAL;
-  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K}, Hop{H, ldh, N, K};
+  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, go, N,
-                     V, V_real, tv, tn, w.G, w.ldg, dBias ? w.dbias_part : nullptr);
+                     w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt, dBias ? w.dbias_part : nullptr);
   if ((rc = launch_status())) return rc;
   if (dBias) {
-    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.ldg, V,
+    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
                        dBias);
     if ((rc = launch_status())) return rc;
   }
@@ -661,17 +816,22 @@ int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_
   if (rc) return rc;
   if (N == 0) return MCE_OK;
   if (!dH || !ws || lddh < K) return MCE_EINVAL;
-  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // Wt = W^T, K-blocked: element (k, v) at Wt[(v/256)*K*256 + k*256 + v%256], zero for V <= v < Vp
+  hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
+                     ldw, V, K, w.Wt);
+  if ((rc = launch_status())) return rc;
+  // dH[n, k] = sum_v G(n, v) Wt(k, v); G's columns V..Vp-1 are zero
   const int tm = (int)cdiv(N, BM), tn = (int)cdiv(K, BN);
-  const Operand Aop{w.G, w.ldg, N, w.ldg};  // G [N, Vp], natural (K = vocab)
-  const Operand Bop{W, ldw, K, V};          // W [V, K] read as [K, V]: transposed
+  const Operand Aop{w.G, BLK, N, w.vp, w.np * BLK};
+  const Operand Bop{w.Wt, BLK, K, V, K * BLK};
   if (dh_bf16)
-    hipLaunchKernelGGL((k_gemm<NAT, TRN, true>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, N, K, tm, tn, dH,
+    hipLaunchKernelGGL((k_gemm<true>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, w.vp, N, K, tm, tn, 4, dH,
                        lddh);
   else
-    hipLaunchKernelGGL((k_gemm<NAT, TRN, false>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, N, K, tm, tn, dH,
+    hipLaunchKernelGGL((k_gemm<false>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, w.vp, N, K, tm, tn, 4, dH,
                        lddh);
   return launch_status();
 }
@@ -687,13 +847,17 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
     return launch_status();
   }
   if (!ws) return MCE_EINVAL;
-  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  // Ht = H^T, K-blocked: element (k, n) at Ht[(n/256)*K*256 + k*256 + n%256], zero for N <= n < Np
+  hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, H,
+                     ldh, N, K, w.Ht);
+  if ((rc = launch_status())) return rc;
+  // dW[v, k] = sum_n Gt(v, n) Ht(k, n), reduction over n < N
   const int tm = (int)cdiv(V, BM), tn = (int)cdiv(K, BN);
-  const Operand Aop{w.G, w.ldg, w.ldg, N};  // G^T: element (v, n) at G[n*ldg + v]
-  const Operand Bop{H, ldh, K, N};          // H^T: element (k, n) at H[n*ldh + k]
-  hipLaunchKernelGGL((k_gemm<TRN, TRN, false>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, V, K, tm, tn, dW,
-                     lddw);
+  const Operand Aop{w.Gt, BLK, V, N, w.vp * BLK};
+  const Operand Bop{w.Ht, BLK, K, N, K * BLK};
+  hipLaunchKernelGGL((k_gemm<false>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, N, V, K, tm, tn, 4, dW, lddw);
   return launch_status();
 }
 
