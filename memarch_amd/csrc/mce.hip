@@ -49,15 +49,22 @@ typedef mce_i32x4 i32x4;
 
 constexpr int BM = 256;              // tile rows (A operand rows)
 constexpr int BN = 256;              // tile cols (B operand rows)
-constexpr int BK = 64;               // K per LDS stage
 constexpr int NTHREADS = 256;        // 4 wave64s
-constexpr int OP_BYTES = BM * BK * 2;             // one operand, one stage: 32 KiB
-constexpr int STAGE_BYTES = 2 * OP_BYTES;         // A + B
-constexpr int LDS_BYTES = 2 * STAGE_BYTES;        // two stages: 128 KiB (gfx950 has 160 KiB per CU)
-constexpr int LOADS_PER_STAGE = 2 * (OP_BYTES / 1024) / 4;  // direct-load instructions per wave per stage: 16
 constexpr int BLK = 256;             // block width of the K-blocked layout
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float CLAMP_P = 1e-30f;    // full2.py:1929, fused_ops.py:125
+
+// K pipeline: BK k-values per LDS stage, NS stages in the ring (NS * 2 operands * 256 rows * BK * 2 bytes).
+#ifndef MCE_BK
+#define MCE_BK 64
+#define MCE_NS 2
+#endif
+constexpr int BK = MCE_BK;
+constexpr int NS = MCE_NS;
+// LDS of the GEMM kernels: the operand ring, at least 128 KiB (the epilogues stage a 256 x 256 bf16 tile).
+constexpr int RING_BYTES = NS * 2 * BM * BK * 2;
+constexpr int LDS_BYTES = RING_BYTES > 128 * 1024 ? RING_BYTES : 128 * 1024;
+static_assert(LDS_BYTES <= 160 * 1024, "operand ring exceeds the 160 KiB of LDS per CU");
 
 struct Operand {
   const uint16_t* p;  // bf16 bits
@@ -94,19 +101,35 @@ __device__ __forceinline__ i32x4 make_rsrc(uint64_t addr) {
   return r;
 }
 
-// LDS operand image: byte (row m, 16-byte chunk c) at m*128 + ((c ^ swz(m)) << 4). Eight consecutive rows
-// read at one logical chunk land on eight distinct 16-byte bank groups.
-__device__ __forceinline__ int swz(int m) { return (m ^ (m >> 3)) & 7; }
+// Geometry of one operand's LDS image for a stage of KB k-values: [256 m][KB k], rows of KB*2 bytes holding
+// CH = KB/8 chunks of 16 bytes; chunk c of row m sits at m*KB*2 + ((c ^ swz(m)) << 4). A fragment read
+// (ds_read_b128, lane l at row mbase + l%32) touches 8 (or 16) consecutive rows at one logical chunk; the
+// swizzle puts them on distinct 16-byte bank groups for both 128- and 256-byte LDS bank rows.
+template <int KB>
+struct Img {
+  static constexpr int CH = KB / 8;                  // chunks per row
+  static constexpr int ROWB = KB * 2;                // bytes per row
+  static constexpr int OPB = BM * ROWB;              // bytes per operand per stage
+  static constexpr int STB = 2 * OPB;                // bytes per stage (A then B)
+  static constexpr int RPI = 1024 / ROWB;            // rows per 1 KiB load instruction
+  static constexpr int LPW = OPB / 1024 / 4;         // load instructions per wave per operand per stage
+  static constexpr int SLICES = KB / 16;             // MFMA K slices per stage
+  __device__ static __forceinline__ int swz(int m) {
+    if constexpr (CH == 8) return (m ^ (m >> 3)) & 7;
+    else return ((m >> 1) ^ (m >> 3)) & 3;
+  }
+};
+using I = Img<BK>;
 
-// Per-tile state of one operand stream. Stage s of this wave's 8 load instructions (instruction i = wave*8+j
-// of the stage's 32 covers 1 KiB = 8 rows of the LDS image) reads base + offset(s) + voff[j], or zeros when
-// the chunk's local k index kloc[j] is past the valid extent (kloc is OOB for rows outside the operand).
+// Per-tile state of one operand stream. Stage s of this wave's I::LPW load instructions (instruction
+// i = wave*LPW + j of the stage covers 1 KiB of the LDS image) reads base + offset(s) + voff[j], or zeros
+// when the chunk's local k index kloc[j] is past the valid extent (kloc is OOB for rows outside the operand).
 struct Stream {
   uint64_t base;   // bytes: element (m0, 0)
   int64_t blk;     // element distance between K blocks, or 0
   int64_t kext;
-  int voff[8];
-  int kloc[8];
+  int voff[I::LPW];
+  int kloc[I::LPW];
 };
 
 __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
@@ -114,11 +137,11 @@ __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int
   st.kext = op.kext;
   st.blk = op.blk;
   st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
-  const int rsub = lane >> 3, pc = lane & 7;
+  const int rsub = lane / I::CH, pc = lane % I::CH;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = (wave * 8 + j) * 8 + rsub;
-    const int c = pc ^ swz(row);
+  for (int j = 0; j < I::LPW; ++j) {
+    const int row = (wave * I::LPW + j) * I::RPI + rsub;
+    const int c = pc ^ I::swz(row);
     st.voff[j] = (int)(row * op.ld * 2) + c * 16;
     st.kloc[j] = (m0 + row < op.mext) ? c * 8 : OOB;
   }
@@ -137,17 +160,17 @@ __device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage) {
   return StageSrc{make_rsrc(st.base + off), klim64 < 0 ? 0 : (klim64 > BK ? BK : (int)klim64)};
 }
 
-// Load j (0..7) of this wave for one stage into the operand image at `s`.
+// Load j of this wave for one stage into the operand image at `s`.
 __device__ __forceinline__ void issue_one(const Stream& st, const StageSrc& src, int j, char* s, int wave) {
   const int vo = st.kloc[j] < src.klim ? st.voff[j] : OOB;
-  buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(s + (wave * 8 + j) * 1024), 16, vo, 0, 0, 0);
+  buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(s + (wave * I::LPW + j) * 1024), 16, vo, 0, 0, 0);
 }
 
-// Issue this wave's 8 loads of stage `stage` into the operand image at `s`.
+// Issue this wave's loads of stage `stage` into the operand image at `s`.
 __device__ __forceinline__ void issue_stage(const Stream& st, int stage, char* s, int wave) {
   const StageSrc src = stage_src(st, stage);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) issue_one(st, src, j, s, wave);
+  for (int j = 0; j < I::LPW; ++j) issue_one(st, src, j, s, wave);
 }
 
 // MFMA operand fragment of v_mfma_f32_32x32x16_bf16 for the 32 rows mbase..mbase+31 of the LDS operand image
@@ -155,15 +178,19 @@ __device__ __forceinline__ void issue_stage(const Stream& st, int stage, char* s
 __device__ __forceinline__ bf16x8 read_frag(const char* s, int mbase, int kk, int lane) {
   const int row = mbase + (lane & 31);
   const int c = kk * 2 + (lane >> 5);
-  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(s + row * 128 + ((c ^ swz(row)) << 4)));
+  return __builtin_bit_cast(bf16x8,
+                            *reinterpret_cast<const u32x4*>(s + row * I::ROWB + ((c ^ I::swz(row)) << 4)));
 }
 
+// Fragment reads in the order the next slice's MFMAs consume them: (0,0) (0,1) (0,2) (0,3) (1,0) ... needs
+// a0 b0 b1 b2 b3 a1 a2 a3, so every read has most of a slice to complete.
 __device__ __forceinline__ void read_frags(const char* stage, int wm, int wn, int kk, int lane, bf16x8 (&a)[4],
                                            bf16x8 (&b)[4]) {
+  a[0] = read_frag(stage, wm * 128, kk, lane);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) a[i] = read_frag(stage, wm * 128 + i * 32, kk, lane);
+  for (int j = 0; j < 4; ++j) b[j] = read_frag(stage + I::OPB, wn * 128 + j * 32, kk, lane);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) b[j] = read_frag(stage + OP_BYTES, wn * 128 + j * 32, kk, lane);
+  for (int i = 1; i < 4; ++i) a[i] = read_frag(stage, wm * 128 + i * 32, kk, lane);
 }
 
 __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4], const bf16x8 (&b)[4]) {
@@ -185,13 +212,16 @@ __device__ __forceinline__ void sched_slice() {
 // C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over k < kloop, fp32 accumulation.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
 //                                              [wn*128 + nj*32 + lane%32].
-// Pipeline per 64-wide K stage (two LDS buffers): the fragments of K slice kk+1 are read while slice kk is
-// multiplied. Before the last slice's MFMAs every wave waits for the next stage's loads and passes one
-// barrier, then reads the next stage's first slice and issues the loads of the stage after next into the
-// buffer it has just finished. Loads past the last stage read nothing (all lanes out of range); the final
-// wait + barrier lets the caller reuse LDS as soon as this returns.
+// Pipeline: an NS-stage ring of BK-wide K stages; the loads of stage s+NS go out as soon as every wave has
+// finished reading stage s, so a stage has NS-1 stages of MFMA time to arrive. Within a stage the fragments
+// of K slice kk+1 are read while slice kk is multiplied. Before the last slice's MFMAs every wave waits for
+// its own loads of the next stage and passes one barrier (which also retires the stage just read), then
+// reads the next stage's first slice and issues the loads of stage kt+NS into the freed buffer. Loads past
+// the last stage read nothing (all lanes out of range); the final wait + barrier lets the caller reuse LDS
+// as soon as this returns.
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int64_t kloop, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4]) {
+  constexpr int LPS = 2 * I::LPW;  // this wave's loads per stage
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
   const int wm = wave >> 1, wn = wave & 1;
@@ -205,44 +235,46 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   const Stream sa = make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
   const int nk = (int)((kloop + BK - 1) / BK);
-  issue_stage(sa, 0, lds, wave);
-  issue_stage(sb, 0, lds + OP_BYTES, wave);
-  issue_stage(sa, 1, lds + STAGE_BYTES, wave);
-  issue_stage(sb, 1, lds + STAGE_BYTES + OP_BYTES, wave);
-  wait_vmcnt<LOADS_PER_STAGE>();
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    issue_stage(sa, s, lds + s * I::STB, wave);
+    issue_stage(sb, s, lds + s * I::STB + I::OPB, wave);
+  }
+  wait_vmcnt<(NS - 1) * LPS>();
   __syncthreads();
 
   bf16x8 fa[2][4], fb[2][4];
   read_frags(lds, wm, wn, 0, lane, fa[0], fb[0]);
   for (int kt = 0; kt < nk; ++kt) {
-    char* cur = lds + (kt & 1) * STAGE_BYTES;
-    char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
-    read_frags(cur, wm, wn, 1, lane, fa[1], fb[1]);
-    mma16(acc, fa[0], fb[0]);
-    sched_slice();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, wm, wn, 2, lane, fa[0], fb[0]);
-    mma16(acc, fa[1], fb[1]);
-    sched_slice();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, wm, wn, 3, lane, fa[1], fb[1]);
-    mma16(acc, fa[0], fb[0]);
-    sched_slice();
-    __builtin_amdgcn_sched_barrier(0);
+    char* cur = lds + (kt % NS) * I::STB;
+    char* nxt = lds + ((kt + 1) % NS) * I::STB;
+#pragma unroll
+    for (int kk = 0; kk + 1 < I::SLICES; ++kk) {
+      read_frags(cur, wm, wn, kk + 1, lane, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      mma16(acc, fa[kk & 1], fb[kk & 1]);
+      sched_slice();
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // stage kt is fully in registers; stage kt+1 must have landed before anyone reads it
-    wait_vmcnt<0>();
+    wait_vmcnt<(NS - 2) * LPS>();
     __syncthreads();
     // last slice, interleaved in source order and pinned by scheduling barriers:
-    // (next stage's fragment read,) MFMA, load, ...
-    const StageSrc ga = stage_src(sa, kt + 2), gb = stage_src(sb, kt + 2);
+    // (next stage's fragment read,) MFMA, (load,) ...
+    const StageSrc ga = stage_src(sa, kt + NS), gb = stage_src(sb, kt + NS);
+    constexpr int LAST = (I::SLICES - 1) & 1;
+    constexpr int EVERY = 16 / LPS;  // MFMAs per load
 #pragma unroll
     for (int idx = 0; idx < 16; ++idx) {
-      if (idx < 4) fa[0][idx] = read_frag(nxt, wm * 128 + idx * 32, 0, lane);
-      else if (idx < 8) fb[0][idx - 4] = read_frag(nxt + OP_BYTES, wn * 128 + (idx - 4) * 32, 0, lane);
-      acc[idx >> 2][idx & 3] =
-          __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][idx >> 2], fb[1][idx & 3], acc[idx >> 2][idx & 3], 0, 0, 0);
-      if (idx < 8) issue_one(sa, ga, idx, cur, wave);
-      else issue_one(sb, gb, idx - 8, cur + OP_BYTES, wave);
+      if (idx == 0) fa[0][0] = read_frag(nxt, wm * 128, 0, lane);
+      else if (idx < 5) fb[0][idx - 1] = read_frag(nxt + I::OPB, wn * 128 + (idx - 1) * 32, 0, lane);
+      else if (idx < 8) fa[0][idx - 4] = read_frag(nxt, wm * 128 + (idx - 4) * 32, 0, lane);
+      acc[idx >> 2][idx & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[LAST][idx >> 2], fb[LAST][idx & 3],
+                                                                        acc[idx >> 2][idx & 3], 0, 0, 0);
+      if (idx % EVERY == 0) {
+        const int l = idx / EVERY;
+        if (l < I::LPW) issue_one(sa, ga, l, cur, wave);
+        else issue_one(sb, gb, l - I::LPW, cur + I::OPB, wave);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
