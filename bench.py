@@ -1,17 +1,25 @@
 """Benchmark of the fused output-projection + cross-entropy + pointer-mixture op (fwd+bwd) on one MI355X.
 
 A step is one forward + backward of `linear_ce_mix_biased` over one batch of the configuration's synthetic
-inputs (default: config 2, N = 32768 tokens, d = 2048, V = 50304, bf16 operands, fp32 accumulation), with
-the inputs resident in HBM before the timed region. Prints one JSON line:
-  value        tokens/s over the K timed steps (N*K / wall time between two synchronisations)
-  roofline     the dominant kernel of the step, timed with HIP events on the stream it runs on
-  op_roofline  the whole step against the bf16 MFMA peak on 6*N*V*d algorithmic FLOPs (the metric's "%")
-  cpu_baseline this repo's torch restatement of the reference eager formula (fp32, fwd+bwd) on a row sample
-               of the same inputs, on the host cores, scaled to tokens/s
+inputs (default: config 2, N = 32768 tokens, d = 2048, V = 50304 (50257 real), bf16 operands, fp32
+accumulation), with every input resident in HBM before the timed region. Prints one JSON line:
+  value         tokens/s of the whole step: N*K / (wall time of K steps between two synchronisations)
+  roofline      the dominant kernel of the step: its algorithmic FLOPs per launch (one N x V x d contraction,
+                2*N*V*d) over its average duration, timed with HIP events on the stream it is launched on;
+                `traffic` is its HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
+                profiles/ (null when that summary does not cover this kernel and configuration)
+  op_roofline   the whole step against the bf16 MFMA peak on the op's 6*N*V*d algorithmic FLOPs (the
+                logits recompute of the backward earns no credit)
+  cpu_baseline  the oracle's torch restatement of the reference eager formula (oracle.mce_oracle.eager_ce_part,
+                fp32 fwd+bwd, materialised logits) on a row sample of the same inputs, on the host cores
+
+`--calibrate-copy` instead times a plain 1 GiB device-to-device copy (the reference kernel for scaling the
+FETCH_SIZE / WRITE_SIZE counters) and prints its size.
 """
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -22,6 +30,12 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16 = 2.5e15     # MI355X dense bf16 MFMA, FLOP/s
 PEAK_HBM = 8.0e12      # MI355X HBM3E, B/s
+METRIC = "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA peak"
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
+
+# C-ABI stage -> the kernel that dominates it (the stage also runs small helpers: see stage_times)
+STAGE_KERNEL = {"fwd": "k_fwd_tiles", "logits_grad": "k_bwd_grad", "dhidden": "k_gemm<true>",
+                "dweight": "k_gemm<false>"}
 
 
 def _args():
@@ -30,14 +44,17 @@ def _args():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
-    ap.add_argument("--cpu-rows", type=int, default=2048, help="rows of the CPU baseline sample (0: skip)")
+    ap.add_argument("--cpu-rows", type=int, default=16384, help="rows of the CPU baseline sample (0: skip)")
     ap.add_argument("--stage-reps", type=int, default=5, help="timed repetitions of each kernel stage")
+    ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
     return ap.parse_args()
 
 
-def _stage_times(inp, reps):
-    """Average duration (ms) of each C-ABI stage, with torch events on the current stream (the stream every
-    stage is launched on)."""
+def stage_times(inp, reps):
+    """Average duration (ms) of each C-ABI stage, timed with torch events on the current stream (the stream
+    every stage is launched on). fwd = k_fwd_tiles + k_fwd_merge + k_sum; logits_grad = k_bwd_grad +
+    k_dbias_reduce + k_dgate; dhidden = k_transpose_blocked (W) + k_gemm<true>; dweight = k_transpose_blocked
+    (H) + k_gemm<false>."""
     from memarch_amd import _lib
     lib = _lib.load()
     h, w, b = inp.h, inp.w.to(torch.bfloat16), inp.bias
@@ -80,36 +97,72 @@ def _stage_times(inp, reps):
     return out
 
 
-def _cpu_baseline(cfg, rows):
-    """Reference eager formula restated in torch (oracle.mce_oracle.eager_ce_part), fp32 fwd+bwd on the host."""
+def traffic_bytes(kernel, cfg_index):
+    """HBM bytes per launch of `kernel` at config `cfg_index` from the committed rocprofv3 summary (a line
+    `traffic <kernel> cfg<k> <bytes>`), or None."""
+    if not os.path.exists(TRAFFIC_SUMMARY):
+        return None
+    pat = re.compile(r"^traffic\s+(\S+)\s+cfg(\d+)\s+([0-9.eE+]+)\s*$")
+    with open(TRAFFIC_SUMMARY) as f:
+        for line in f:
+            m = pat.match(line.strip())
+            if m and m.group(1) == kernel and int(m.group(2)) == cfg_index:
+                return float(m.group(3))
+    return None
+
+
+def cpu_baseline(cfg, rows, chunk=4096):
+    """The oracle's torch restatement of the reference eager formula (full2.py:1917-1929), fp32 fwd+bwd with
+    materialised logits, over the first `rows` rows of the configuration's inputs in chunks of `chunk` rows
+    (rows are independent, so the time is linear in rows). Only the compute is timed."""
     from memarch_amd.workloads import make_inputs
     from oracle.mce_oracle import eager_ce_part
     inp = make_inputs(cfg, rows=rows)
-    h = inp.h.bfloat16().float().requires_grad_()
     w = inp.w.bfloat16().float().requires_grad_()
     b = inp.bias.clone()
     b[cfg.v_real:] = float("-inf")  # padded ids masked, as the GPU path does with v_real
     b.requires_grad_()
-    g = inp.gate.clone().requires_grad_()
-    t0 = time.perf_counter()
-    loss = eager_ce_part(h, w, b, inp.y, inp.c1, g) / cfg.n
-    loss.backward()
-    dt = time.perf_counter() - t0
-    return dict(value=rows / dt, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"{rows} of {cfg.n} rows of config {cfg.index} (N={cfg.n}, d={cfg.d}, V={cfg.v}), fp32 "
-                       f"torch eager fwd+bwd ({dt:.2f} s), os.cpu_count()={os.cpu_count()}; tokens/s scales "
-                       f"linearly in N")
+    hb = inp.h.bfloat16().float()
+    dt = 0.0
+    for i in range(0, rows, chunk):
+        h = hb[i:i + chunk].clone().requires_grad_()
+        g = inp.gate[i:i + chunk].clone().requires_grad_()
+        t0 = time.perf_counter()
+        loss = eager_ce_part(h, w, b, inp.y[i:i + chunk], inp.c1[i:i + chunk], g) / cfg.n
+        loss.backward()
+        dt += time.perf_counter() - t0
+    return dict(value=round(rows / dt, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"first {rows} of {cfg.n} rows of config {cfg.index} (d={cfg.d}, V={cfg.v}), fp32 torch eager "
+                       f"fwd+bwd in {chunk}-row chunks, {dt:.1f} s on {torch.get_num_threads()} threads "
+                       f"(os.cpu_count()={os.cpu_count()}); rows are independent, so tokens/s holds for all N")
+
+
+def calibrate_copy():
+    """A plain device copy of 1 GiB, five times: each launch reads and writes exactly 2^30 bytes."""
+    dev = torch.device("cuda", 0)
+    src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30,
+                      "launches": 5}), flush=True)
 
 
 def main():
     args = _args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only: the op is single-GPU in this build (--gpus {args.gpus} refused)",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only: the fused op is single-GPU in this build, so --gpus {args.gpus} "
+              "is refused (the sharded design is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     from memarch_amd import fused_ops
     from memarch_amd.workloads import CONFIGS, make_inputs
     cfg = CONFIGS[args.config]
+    if not cfg.backward:
+        raise SystemExit(f"config {cfg.index} is the CPU-only forward case; bench configs 1-4")
     dev = torch.device("cuda", 0)
     print(f"[bench] generating config {cfg.index} inputs ({cfg.name})", file=sys.stderr, flush=True)
     inp = make_inputs(cfg).to(dev)
@@ -138,27 +191,28 @@ def main():
     tok_s = n / dt
     flops = 6.0 * n * v * d
     print("[bench] stage timing", file=sys.stderr, flush=True)
-    stages = _stage_times(inp, args.stage_reps)
+    stages = stage_times(inp, args.stage_reps)
     dom = max(stages, key=stages.get)
-    dom_flops = 2.0 * n * v * d   # every stage is one N x V x d contraction
-    ach = dom_flops / (stages[dom] * 1e-3)
+    kflops = 2.0 * n * v * d   # every stage's kernel is one N x V x d contraction
+    ach = kflops / (stages[dom] * 1e-3)
+    traffic = traffic_bytes(STAGE_KERNEL[dom], cfg.index)
     res = {
-        "metric": "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA peak",
+        "metric": METRIC,
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic (seeded, config %d distributions)" % cfg.index,
-        "config": {"workload": f"config {cfg.index}: fused linear+CE+pointer fwd+bwd", "N": n, "d": d, "V": v,
-                   "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach / 1e12, 2),
+        "dtype": "bf16", "data": f"synthetic (seeded config {cfg.index} distributions, random-init weights)",
+        "config": {"workload": f"config {cfg.index}: fused linear+CE+pointer fwd+bwd, one batch per step",
+                   "N": n, "d": d, "V": v, "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
+        "roofline": {"bound": "mfma", "kernel": STAGE_KERNEL[dom], "stage": dom, "achieved": round(ach / 1e12, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16, 4),
-                     "traffic": None},
+                     "flops_per_launch": kflops, "traffic": traffic},
         "op_roofline": {"achieved": round(flops / dt / 1e12, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
     }
     if args.cpu_rows > 0:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        res["cpu_baseline"] = _cpu_baseline(cfg, min(args.cpu_rows, n))
+        res["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_rows, n))
     print(json.dumps(res), flush=True)
 
 

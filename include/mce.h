@@ -70,14 +70,16 @@ MCE_API int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
             int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
             void* ws, size_t ws_bytes, void* stream);
 
-/* Workspace bytes needed by the backward entry points for this shape (the bf16 G buffer [N, Vp] with
- * Vp = V rounded up to 256, plus the dBias partial sums). Replaces the bf16 logits chunk that
+/* Workspace bytes needed by the backward entry points for this shape: the bf16 gradient of the logits in two
+ * K-blocked layouts (G, v contiguous, and G^T, n contiguous; each N x V rounded up to 256 x 256), the K-blocked
+ * transposed copies W^T and H^T, and the dBias partial sums. Replaces the bf16 logits chunk that
  * fused_ops.py:150,134 overwrites with the gradient. */
 MCE_API size_t mce_bwd_ws_bytes(int64_t N, int64_t K, int64_t V);
 
 /*
- * Backward step 1: recompute the logits tile by tile and write G (bf16, [N, Vp], row stride Vp) into the
- * workspace; reduce dBias (if dBias != NULL, requires bias != NULL) and write dGate (if dGate != NULL).
+ * Backward step 1: recompute the logits tile by tile and write G = go*wgt*(softmax - onehot) (bf16, both
+ * layouts) into the workspace; reduce dBias (if dBias != NULL, requires bias != NULL) and write dGate (if
+ * dGate != NULL).
  * `go` is a device pointer to the fp32 upstream gradient of the loss sum (a 0-dim tensor).
  * Replaces the gradient half of `_ce_mix_kernel` (fused_ops.py:127-134) and the `go` scaling of
  * `_LinearCEMix.backward` (fused_ops.py:159-162).
@@ -89,16 +91,16 @@ MCE_API int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* 
 
 /*
  * Backward step 2: dH = G W (fp32 accumulation). dH is [N, K] with row stride lddh, fp32 (dh_bf16 = 0) or
- * bf16 (dh_bf16 = 1). Needs the workspace filled by mce_bwd_logits_grad. Replaces `gh[i] = logits @ wd`
- * (fused_ops.py:153).
+ * bf16 (dh_bf16 = 1). Needs the workspace filled by mce_bwd_logits_grad (W^T is written into it here).
+ * Replaces `gh[i] = logits @ wd` (fused_ops.py:153).
  */
 MCE_API int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16,
                     int64_t lddh, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Backward step 3: dW = G^T H (fp32 accumulation), dW fp32 [V, K] with row stride lddw (overwritten, not
- * accumulated). Needs the workspace filled by mce_bwd_logits_grad. Replaces `gw += (logits.T @ hc).float()`
- * (fused_ops.py:154).
+ * accumulated). Needs the workspace filled by mce_bwd_logits_grad (H^T is written into it here). Replaces
+ * `gw += (logits.T @ hc).float()` (fused_ops.py:154).
  */
 MCE_API int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_t V, float* dW, int64_t lddw,
                     void* ws, size_t ws_bytes, void* stream);

@@ -49,7 +49,9 @@ def _rows(t, dtype):
     return t.detach().reshape(-1).to(dtype).contiguous()
 
 
-def _forward(ctx, h, w, bias, y, gate, hit, v_real):
+def _fwd_launch(h, w, bias, y, gate, hit, v_real):
+    """Validates the inputs, prepares the bf16 operands and runs mce_fwd on the current stream. Returns
+    (operands, per-row outputs, loss_sum, meta)."""
     if h.dim() != 2 or w.dim() != 2 or h.shape[1] != w.shape[1]:
         raise ValueError(f"h {tuple(h.shape)} and w {tuple(w.shape)} must be [N, K] and [V, K]")
     n, k = h.shape
@@ -78,11 +80,25 @@ def _forward(ctx, h, w, bias, y, gate, hit, v_real):
     _lib.call("mce_fwd", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf), _ptr(hf),
               n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum), _ptr(ws),
               ws_bytes, _stream(dev))
-    ctx.save_for_backward(hd, wd, bf, y64, lse, wgt, dgr)
-    ctx.meta = (n, k, kp, v, v_real)
+    rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
+    return (hd, wd, bf, y64), rows, loss_sum, (n, k, kp, v, v_real)
+
+
+def _forward(ctx, h, w, bias, y, gate, hit, v_real):
+    (hd, wd, bf, y64), rows, loss_sum, meta = _fwd_launch(h, w, bias, y, gate, hit, v_real)
+    ctx.save_for_backward(hd, wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"])
+    ctx.meta = meta
     ctx.dtypes = (h.dtype, w.dtype, gate.dtype, None if bias is None else bias.dtype)
-    ctx.loss_rows = loss_rows
     return loss_sum
+
+
+@torch.no_grad()
+def forward_rows(h, w, y, gate, hit, bias=None, v_real=None):
+    """The forward pass without autograd: dict of the fp32 loss sum and the per-row loss, lse (logsumexp of the
+    row's logits), wgt = (1-g)py/P and dgr = (py-hit)/P (both 0 for rows under the 1e-30 clamp)."""
+    _, rows, loss_sum, _ = _fwd_launch(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), gate.reshape(-1),
+                                       hit.reshape(-1), v_real)
+    return dict(loss_sum=loss_sum, **rows)
 
 
 def _backward(ctx, go, need_h, need_w, need_b, need_g):
