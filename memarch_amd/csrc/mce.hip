@@ -16,7 +16,8 @@
 // Elements outside an operand's extent read as zero (out-of-range buffer offsets), so partial tiles need
 // no special path.
 //
-//   forward     S^T = W H^T           -> per-tile row max / sum-exp, target logit; merge -> lse, loss, wgt, dgr
+//   forward     S^T = W H^T           -> per-half-tile row max / sum-exp; target logit by a dot product;
+//                                         merge -> lse, loss, wgt, dgr
 //   logits-grad S^T = W H^T recomputed -> G = go*wgt*(softmax - onehot) (bf16) written twice through LDS:
 //                                         G (v contiguous, for dH) and G^T (n contiguous, for dW); dBias partials
 //   dhidden     dH  = G   . Wt  with Wt = W^T (K-blocked copy made by k_transpose_blocked)
@@ -153,9 +154,9 @@ struct StageSrc {
   i32x4 rsrc;
   int klim;
 };
-__device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage) {
+__device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage, int send) {
   const int64_t k0 = (int64_t)stage * BK;
-  const int64_t klim64 = st.kext - k0;
+  const int64_t klim64 = stage < send ? st.kext - k0 : 0;  // stages past the range read nothing
   const uint64_t off = st.blk ? (uint64_t)((k0 >> 8) * st.blk + (k0 & (BLK - 1))) * 2 : (uint64_t)k0 * 2;
   return StageSrc{make_rsrc(st.base + off), klim64 < 0 ? 0 : (klim64 > BK ? BK : (int)klim64)};
 }
@@ -167,8 +168,8 @@ __device__ __forceinline__ void issue_one(const Stream& st, const StageSrc& src,
 }
 
 // Issue this wave's loads of stage `stage` into the operand image at `s`.
-__device__ __forceinline__ void issue_stage(const Stream& st, int stage, char* s, int wave) {
-  const StageSrc src = stage_src(st, stage);
+__device__ __forceinline__ void issue_stage(const Stream& st, int stage, int send, char* s, int wave) {
+  const StageSrc src = stage_src(st, stage, send);
 #pragma unroll
   for (int j = 0; j < I::LPW; ++j) issue_one(st, src, j, s, wave);
 }
@@ -209,7 +210,8 @@ __device__ __forceinline__ void sched_slice() {
   }
 }
 
-// C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over k < kloop, fp32 accumulation.
+// C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over the K stages s0 .. s0+nk-1 (k in [s0*BK, (s0+nk)*BK),
+// clipped to each operand's extent), fp32 accumulation.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
 //                                              [wn*128 + nj*32 + lane%32].
 // Pipeline: an NS-stage ring of BK-wide K stages; the loads of stage s+NS go out as soon as every wave has
@@ -219,7 +221,7 @@ __device__ __forceinline__ void sched_slice() {
 // reads the next stage's first slice and issues the loads of stage kt+NS into the freed buffer. Loads past
 // the last stage read nothing (all lanes out of range); the final wait + barrier lets the caller reuse LDS
 // as soon as this returns.
-__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int64_t kloop, int64_t m0, int64_t n0,
+__device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4]) {
   constexpr int LPS = 2 * I::LPW;  // this wave's loads per stage
   const int t = threadIdx.x, lane = t & 63;
@@ -234,11 +236,11 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 
   const Stream sa = make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
-  const int nk = (int)((kloop + BK - 1) / BK);
+  const int send = s0 + nk;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    issue_stage(sa, s, lds + s * I::STB, wave);
-    issue_stage(sb, s, lds + s * I::STB + I::OPB, wave);
+    issue_stage(sa, s0 + s, send, lds + s * I::STB, wave);
+    issue_stage(sb, s0 + s, send, lds + s * I::STB + I::OPB, wave);
   }
   wait_vmcnt<(NS - 1) * LPS>();
   __syncthreads();
@@ -260,7 +262,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
     __syncthreads();
     // last slice, interleaved in source order and pinned by scheduling barriers:
     // (next stage's fragment read,) MFMA, (load,) ...
-    const StageSrc ga = stage_src(sa, kt + NS), gb = stage_src(sb, kt + NS);
+    const StageSrc ga = stage_src(sa, s0 + kt + NS, send), gb = stage_src(sb, s0 + kt + NS, send);
     constexpr int LAST = (I::SLICES - 1) & 1;
     constexpr int EVERY = 16 / LPS;  // MFMAs per load
 #pragma unroll
@@ -285,11 +287,12 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 // Block id -> (tile_m, tile_n). Workgroups are dispatched round-robin over the 8 XCDs (block b on XCD b%8);
 // the remap gives each XCD a contiguous range of logical tiles, and the logical order walks groups of
 // `group` tile-rows column by column, so the tiles resident on one XCD share A and B panels in its L2.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group, int& tm, int& tn) {
-  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+__device__ __forceinline__ int xcd_lin(int b, int nb) {
   const int per = nb / 8, rem = nb % 8;
   const int x = b % 8, j = b / 8;
-  const int lin = (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + j;
+  return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + j;
+}
+__device__ __forceinline__ void tile_of(int lin, int tiles_m, int tiles_n, int group, int& tm, int& tn) {
   const int span = group * tiles_n;
   const int g = lin / span;
   const int first = g * group;
@@ -297,6 +300,9 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group,
   const int in = lin - g * span;
   tm = first + in % gsize;
   tn = in / gsize;
+}
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group, int& tm, int& tn) {
+  tile_of(xcd_lin((int)blockIdx.x, (int)gridDim.x), tiles_m, tiles_n, group, tm, tn);
 }
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
@@ -312,144 +318,168 @@ __device__ __forceinline__ constexpr int acc_row(int mi, int r, int lh) {
   return mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
 }
 
-// Adds the bias to every logit of this lane and masks columns v >= V_real to -inf. Rows of the MFMA tile
-// are vocabulary ids v; v_lane = v0 + wm*128 (the wave's first id).
-__device__ __forceinline__ void add_bias_mask(f32x16 (&acc)[4][4], const float* __restrict__ bias, int64_t v_lane,
-                                              int lh, int64_t V, int64_t Vreal) {
+// Bias + vocabulary mask of a tile's 256 vocabulary rows, in two steps so that only one register per thread
+// is live across the mainloop: tile_bias() (before the mainloop) reads bias[v0 + t]; stash_bias() (after it)
+// stores bias or -inf (v >= V_real) into a 1 KiB LDS slot; read_bias_mask() gives a lane the 64 values of its
+// logit rows (v = v_lane + acc_row(mi, r, lh); r%4 = 0..3 are consecutive, so 16 ds_read_b128).
+__device__ __forceinline__ float tile_bias(const float* __restrict__ bias, int64_t v0, int64_t V) {
+  const int64_t v = v0 + threadIdx.x;
+  return (bias != nullptr && v < V) ? bias[v] : 0.f;
+}
+__device__ __forceinline__ void stash_bias(float* slot, float b, int64_t v0, int64_t Vreal) {
+  slot[threadIdx.x] = (v0 + threadIdx.x < Vreal) ? b : -INFINITY;
+}
+__device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* slot, int wm, int lh) {
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t v = v_lane + acc_row(mi, r, lh);
-      const float b = (bias != nullptr && v < V) ? bias[v] : 0.f;
-      const bool ok = v < Vreal;
-#pragma unroll
-      for (int nj = 0; nj < 4; ++nj) acc[mi][nj][r] = ok ? acc[mi][nj][r] + b : -INFINITY;
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = *reinterpret_cast<const float4*>(slot + wm * 128 + acc_row(mi, 4 * q, lh));
+      bm[mi][4 * q + 0] = f.x;
+      bm[mi][4 * q + 1] = f.y;
+      bm[mi][4 * q + 2] = f.z;
+      bm[mi][4 * q + 3] = f.w;
     }
 }
 
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+
 // ---------------------------------------------------------------------------------------------------------
-// Forward tile: S^T[v, n] for a 256(v) x 256(n) tile -> per-(v-tile, row) max and sum of exp, target logit.
+// Forward tile: S^T[v, n] for a 256(v) x 256(n) tile. Each wave reduces its own 128 vocabulary rows, so the
+// partials are per half-tile: part_m / part_s [2*tiles_v][N] hold the max and sum of exp of row block
+// 2*tm + wm for every column n. No LDS and no barrier after the mainloop.
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
-void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
-                 int64_t N, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, float* __restrict__ part_m,
-                 float* __restrict__ part_s, float* __restrict__ xy) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64_t N, int64_t V, int64_t Vreal,
+                 int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + BM * 4];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, 8, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  f32x16 acc[4][4];
-  gemm_tile(Wop, Hop, Wop.kext, v0, n0, lds, acc);
-
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  const int64_t v_lane = v0 + wm * 128;
-  add_bias_mask(acc, bias, v_lane, lh, V, Vreal);
+  const float btile = tile_bias(bias, v0, V);
+  f32x16 acc[4][4];
+  gemm_tile(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
+  float* bslot = reinterpret_cast<float*>(lds + LDS_BYTES);
+  stash_bias(bslot, btile, v0, Vreal);
+  __syncthreads();
+  float bm[4][16];
+  read_bias_mask(bm, bslot, wm, lh);
 
-  // target logit: the one lane holding (row n, column y_n) writes it
-#pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
-    const int64_t n = n0 + wn * 128 + nj * 32 + lr;
-    if (n < N) {
-      const int64_t yn = y[n];
-      const int64_t tl = yn - v_lane;
-      if (yn < Vreal && tl >= 0 && tl < 128 && (((tl >> 2) & 1) == lh)) {
-        float val = 0.f;
-#pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (acc_row(mi, r, lh) == (int)tl) val = acc[mi][nj][r];
-        xy[n] = val;
-      }
-    }
-  }
-
-  float* red_m = reinterpret_cast<float*>(lds);        // [2 wm][256 cols]
-  float* red_s = red_m + 512;                          // [2 wm][256 cols]
-  float mx[4];
+  const int64_t prow = (int64_t)(2 * tm + wm) * N;
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     float m = -INFINITY;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r]);
+      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r] + bm[mi][r]);
     m = fmaxf(m, __shfl_xor(m, 32));
-    if (lh == 0) red_m[wm * 256 + wn * 128 + nj * 32 + lr] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
-    const int c = wn * 128 + nj * 32 + lr;
-    mx[nj] = fmaxf(red_m[c], red_m[256 + c]);
-  }
-#pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
     float s = 0.f;
-    if (mx[nj] != -INFINITY) {
+    if (m != -INFINITY) {
+      const float mb = m * LOG2E;
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s += fast_exp(acc[mi][nj][r] - mx[nj]);
+        for (int r = 0; r < 16; ++r)
+          s += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r] + bm[mi][r], LOG2E, -mb));
     }
     s += __shfl_xor(s, 32);
-    if (lh == 0) red_s[wm * 256 + wn * 128 + nj * 32 + lr] = s;
-  }
-  __syncthreads();
-  if (wm == 0 && lh == 0) {
-#pragma unroll
-    for (int nj = 0; nj < 4; ++nj) {
-      const int c = wn * 128 + nj * 32 + lr;
-      const int64_t n = n0 + c;
-      if (n < N) {
-        part_m[(int64_t)tm * N + n] = mx[nj];
-        part_s[(int64_t)tm * N + n] = red_s[c] + red_s[256 + c];
-      }
+    const int64_t n = n0 + wn * 128 + nj * 32 + lr;
+    if (lh == 0 && n < N) {
+      part_m[prow + n] = m;
+      part_s[prow + n] = s;
     }
   }
 }
 
-// Merge of the per-v-tile partials: lse, loss, wgt, dgr per row; one loss partial sum per block.
+// Target logit x_y = h_n . w_{y_n} + b_{y_n} of every row (fp32 dot product of the bf16 rows), -inf when y_n is
+// outside [0, V_real). One wave per row. The tile kernels compute the same sum in another order, so the two
+// agree to fp32 rounding.
+__global__ __launch_bounds__(256) void k_target_logit(const uint16_t* __restrict__ H, int64_t ldh,
+                                                      const uint16_t* __restrict__ W, int64_t ldw,
+                                                      const float* __restrict__ bias, const int64_t* __restrict__ y,
+                                                      int64_t N, int64_t K, int64_t Vreal, float* __restrict__ xy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int64_t yn = y[n];
+  if (yn < 0 || yn >= Vreal) {
+    if (lane == 0) xy[n] = -INFINITY;
+    return;
+  }
+  const uint16_t* hr = H + n * ldh;
+  const uint16_t* wr = W + yn * ldw;
+  float s = 0.f;
+  for (int64_t k = (int64_t)lane * 8; k < K; k += 512) {
+    const u16x8 a = *reinterpret_cast<const u16x8*>(hr + k);
+    const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[e]), s);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) xy[n] = s + (bias != nullptr ? bias[yn] : 0.f);
+}
+
+// Merge of the T per-half-tile partials: lse, loss, wgt, dgr per row; one loss partial sum per block.
+// 32 rows per block, 8 threads per row (an online max / rescaled sum over every 8th partial), combined in LDS.
 __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ part_m, const float* __restrict__ part_s,
-                                                   const float* __restrict__ xy, const int64_t* __restrict__ y,
-                                                   const float* __restrict__ gate, const float* __restrict__ hit,
-                                                   int64_t N, int64_t Vreal, int tiles_v, float* __restrict__ loss_rows,
-                                                   float* __restrict__ lse_rows, float* __restrict__ wgt_rows,
-                                                   float* __restrict__ dgr_rows, float* __restrict__ loss_part) {
-  __shared__ float red[256];
-  const int t = threadIdx.x;
-  const int64_t n = (int64_t)blockIdx.x * 256 + t;
-  float loss = 0.f;
+                                                   const float* __restrict__ xy, const float* __restrict__ gate,
+                                                   const float* __restrict__ hit, int64_t N, int T,
+                                                   float* __restrict__ loss_rows, float* __restrict__ lse_rows,
+                                                   float* __restrict__ wgt_rows, float* __restrict__ dgr_rows,
+                                                   float* __restrict__ loss_part) {
+  __shared__ float rm[8][32], rs[8][32], rl[32];
+  const int t = threadIdx.x, r = t & 31, sl = t >> 5;
+  const int64_t n = (int64_t)blockIdx.x * 32 + r;
+  float m = -INFINITY, s = 0.f;
   if (n < N) {
-    float m = -INFINITY;
-    for (int tb = 0; tb < tiles_v; ++tb) m = fmaxf(m, part_m[(int64_t)tb * N + n]);
-    float s = 0.f;
-    for (int tb = 0; tb < tiles_v; ++tb) {
+    for (int tb = sl; tb < T; tb += 8) {
       const float mm = part_m[(int64_t)tb * N + n];
-      if (mm != -INFINITY) s += part_s[(int64_t)tb * N + n] * expf(mm - m);
+      if (mm == -INFINITY) continue;
+      const float ss = part_s[(int64_t)tb * N + n];
+      if (mm > m) {
+        s = (m == -INFINITY ? 0.f : s * expf(m - mm)) + ss;
+        m = mm;
+      } else {
+        s += ss * expf(mm - m);
+      }
     }
-    const float lse = m + logf(s);
-    const int64_t yn = y[n];
-    const float x_y = (yn >= 0 && yn < Vreal) ? xy[n] : -INFINITY;
-    const float py = expf(x_y - lse);
-    const float g = gate[n], h = hit[n];
-    const float P = (1.f - g) * py + g * h;
-    const bool clamped = !(P >= CLAMP_P);  // torch clamp(min) passes the gradient where P >= min
-    const float Pc = clamped ? CLAMP_P : P;
-    loss = -logf(Pc);
-    loss_rows[n] = loss;
-    lse_rows[n] = lse;
-    wgt_rows[n] = clamped ? 0.f : (1.f - g) * py / Pc;
-    dgr_rows[n] = clamped ? 0.f : (py - h) / Pc;
   }
-  red[t] = loss;
+  rm[sl][r] = m;
+  rs[sl][r] = s;
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (t < s) red[t] += red[t + s];
-    __syncthreads();
+  if (sl == 0) {
+    float loss = 0.f;
+    if (n < N) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) M = fmaxf(M, rm[i][r]);
+      float S = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (rm[i][r] != -INFINITY) S += rs[i][r] * expf(rm[i][r] - M);
+      const float lse = M + logf(S);
+      const float py = expf(xy[n] - lse);
+      const float g = gate[n], h = hit[n];
+      const float P = (1.f - g) * py + g * h;
+      const bool clamped = !(P >= CLAMP_P);  // torch clamp(min) passes the gradient where P >= min
+      const float Pc = clamped ? CLAMP_P : P;
+      loss = -logf(Pc);
+      loss_rows[n] = loss;
+      lse_rows[n] = lse;
+      wgt_rows[n] = clamped ? 0.f : (1.f - g) * py / Pc;
+      dgr_rows[n] = clamped ? 0.f : (py - h) / Pc;
+    }
+    rl[r] = loss;
   }
-  if (t == 0) loss_part[blockIdx.x] = red[0];
+  __syncthreads();
+  if (t == 0) {
+    float tot = 0.f;
+    for (int i = 0; i < 32; ++i) tot += rl[i];
+    loss_part[blockIdx.x] = tot;
+  }
 }
 
 // Deterministic sum of `count` partials into out[0] (one block).
@@ -468,89 +498,62 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Logits-grad tile: recompute S^T for the tile, G = go*wgt*(exp(x - lse) - [v = y]), column sums of G over the
-// tile's 256 rows -> dbias_part[tn, v], and G rounded to bf16 into both K-blocked layouts:
+// Logits-grad tile: recompute S^T for the tile and form G = go*wgt*(exp(x - lse) - [v = y]) rounded to bf16,
+// written to both K-blocked layouts:
 //   G   element (n, v) at G[(v/256)*Np*256 + n*256 + v%256]    (for dH, reduction over v)
 //   Gt  element (v, n) at Gt[(n/256)*Vp*256 + v*256 + n%256]   (for dW, reduction over n)
 // Each tile is one contiguous 128 KiB block of either buffer. The tile is staged in LDS as [256 n][256 v]
-// (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))); G rows are copied out with ds_read_b128, Gt rows are
-// assembled with ds_read_b64_tr_b16 (each 16-lane group turns a 4x16 [n][v] block into 16 columns of 4 n).
-// gsw makes both reads bank-conflict free and leaves the staging writes at most 2-way conflicted.
+// (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))):
+//   1. every lane writes go*wgt*exp(x - lse) for its 256 logits (8-byte writes);
+//   2. one thread per row overwrites the target element with go*wgt*(exp(x_y - lse) - 1), from the row's
+//      target logit (so the one-hot term is applied in fp32 before rounding, without searching registers);
+//   3. G rows are copied out with ds_read_b128 (non-temporal stores: G is read back by another kernel, not
+//      by this one), and the same pass sums the bf16 G values of each column over
+//      the tile's rows (dBias partials, as the reference's dBias is the column sum of its bf16 G);
+//   4. Gt rows are assembled with ds_read_b64_tr_b16 (each 16-lane group turns a 4x16 [n][v] block into 16
+//      columns of 4 n).
+// gsw makes both read passes bank-conflict free and leaves the staging writes at most 2-way conflicted.
 __device__ __forceinline__ int gsw(int n) { return ((n & 3) << 1) | ((n >> 2) & 1); }
+
+constexpr int GRAD_LDS_BYTES = LDS_BYTES + 4 * 32 * 8 * 4 + BM * 4;  // tile + [4][32][8] dBias sums + bias slot
 
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
-                const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ go,
-                int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n,
-                uint16_t* __restrict__ G, uint16_t* __restrict__ Gt, float* __restrict__ dbias_part) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+                const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ xy,
+                const float* __restrict__ go, int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal,
+                int tiles_v, int tiles_n, uint16_t* __restrict__ G, uint16_t* __restrict__ Gt,
+                float* __restrict__ dbias_part) {
+  __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, 8, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  f32x16 acc[4][4];
-  gemm_tile(Wop, Hop, Wop.kext, v0, n0, lds, acc);
-
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  const int64_t v_lane = v0 + wm * 128;
-  add_bias_mask(acc, bias, v_lane, lh, V, Vreal);
-
+  // everything the epilogue needs from memory is loaded before the mainloop
+  const float btile = tile_bias(bias, v0, V);
   const float gscale = go[0];
-  float cn[4], ln[4];
-  int64_t yn[4];
+  float cn[4], lb[4];
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
     const bool ok = n < N;
     cn[nj] = ok ? gscale * wgt_rows[n] : 0.f;
-    ln[nj] = ok ? lse_rows[n] : 0.f;
-    yn[nj] = ok ? y[n] : -1;
+    lb[nj] = ok ? lse_rows[n] * LOG2E : 0.f;
   }
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-#pragma unroll
-      for (int nj = 0; nj < 4; ++nj) {
-        const float x = acc[mi][nj][r];
-        acc[mi][nj][r] = (x == -INFINITY) ? 0.f : cn[nj] * fast_exp(x - ln[nj]);
-      }
-#pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
-    const int64_t tl = yn[nj] - v_lane;
-    if (yn[nj] < Vreal && tl >= 0 && tl < 128 && (((tl >> 2) & 1) == lh)) {
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (acc_row(mi, r, lh) == (int)tl) acc[mi][nj][r] -= cn[nj];
-    }
-  }
+  const int64_t nf = n0 + t;  // the row this thread fixes up in step 2
+  const int64_t yf = nf < N ? y[nf] : -1;
+  const bool fix = yf >= v0 && yf < v0 + BM && yf < Vreal;
+  const float fval = fix ? gscale * wgt_rows[nf] * (expf(xy[nf] - lse_rows[nf]) - 1.f) : 0.f;
 
-  if (dbias_part != nullptr) {
-    // column sums over n (fp32, before rounding): in-lane over nj, then over the 32 lanes and the two wn waves
-    float* red = reinterpret_cast<float*>(lds);  // [4 waves][128 rows][33]
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float ps = acc[mi][0][r] + acc[mi][1][r] + acc[mi][2][r] + acc[mi][3][r];
-        red[(wave * 128 + acc_row(mi, r, lh)) * 33 + lr] = ps;
-      }
-    __syncthreads();
-    const int wmt = t >> 7, row = t & 127;
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      const float* src = red + ((wmt * 2 + w) * 128 + row) * 33;
-#pragma unroll
-      for (int l = 0; l < 32; ++l) s += src[l];
-    }
-    dbias_part[(int64_t)tn * Vp + v0 + t] = s;
-    __syncthreads();
-  }
+  f32x16 acc[4][4];
+  gemm_tile(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
+  float* bslot = reinterpret_cast<float*>(lds + LDS_BYTES + 4 * 32 * 8 * 4);
+  stash_bias(bslot, btile, v0, Vreal);
+  __syncthreads();
+  float bm[4][16];
+  read_bias_mask(bm, bslot, wm, lh);
 
-  // stage the bf16 tile: lane holds 4 consecutive v (r%4) of one row n -> 8-byte LDS writes
+  // 1. stage go*wgt*exp(x - lse) as bf16: lane holds 4 consecutive v (r%4) of one row n -> 8-byte LDS writes
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int nl = wn * 128 + nj * 32 + lr;
@@ -560,26 +563,50 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        float g4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          g4[e] = cn[nj] * __builtin_amdgcn_exp2f(
+                               __builtin_fmaf(acc[mi][nj][4 * q + e] + bm[mi][4 * q + e], LOG2E, -lb[nj]));
         const int vl = wm * 128 + acc_row(mi, 4 * q, lh);
         u32x2 pk;
-        pk[0] = pack_bf16x2(acc[mi][nj][4 * q + 0], acc[mi][nj][4 * q + 1]);
-        pk[1] = pack_bf16x2(acc[mi][nj][4 * q + 2], acc[mi][nj][4 * q + 3]);
+        pk[0] = pack_bf16x2(g4[0], g4[1]);
+        pk[1] = pack_bf16x2(g4[2], g4[3]);
         *reinterpret_cast<u32x2*>(row + ((vl * 2) ^ sw)) = pk;
       }
   }
   __syncthreads();
-
-  // G block of this tile: [256 n][256 v], contiguous; thread t copies 16-byte chunks t, t+256, ...
+  // 2. one-hot term of row t
+  if (fix) {
+    const int vl = (int)(yf - v0);
+    *reinterpret_cast<__bf16*>(lds + t * 512 + ((vl * 2) ^ (gsw(t) << 4))) = (__bf16)fval;
+  }
+  __syncthreads();
+  // 3. G block of this tile ([256 n][256 v], contiguous): thread t copies 16-byte chunks t, t+256, ...; its
+  //    chunk column c = t % 32 is fixed, so it also sums the 8 columns of that chunk over its 32 rows
   char* gblk = reinterpret_cast<char*>(G + ((int64_t)tm * Np + n0) * BLK);
+  float db[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
   for (int i = 0; i < 32; ++i) {
     const int id = i * 256 + t;
     const int nl = id >> 5, c = id & 31;
     const u32x4 val = *reinterpret_cast<const u32x4*>(lds + nl * 512 + ((c ^ gsw(nl)) << 4));
-    *reinterpret_cast<u32x4*>(gblk + (int64_t)id * 16) = val;
+    __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(gblk + (int64_t)id * 16));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      db[2 * e] += __uint_as_float(val[e] << 16);
+      db[2 * e + 1] += __uint_as_float(val[e] & 0xFFFF0000u);
+    }
   }
-  // Gt block of this tile: [256 v][256 n], contiguous. Task id -> (16 v from v16, 8 n from n8); 16-lane group
-  // gi handles tasks gi, gi+16, ...; lane p of the group ends with (v16 + p, n8 .. n8+7).
+  float* dbs = reinterpret_cast<float*>(lds + LDS_BYTES);  // [4 waves][32 chunks][8]
+#pragma unroll
+  for (int e = 0; e < 8; ++e) db[e] += __shfl_xor(db[e], 32);
+  if (lane < 32) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dbs[(wave * 32 + lane) * 8 + e] = db[e];
+  }
+  // 4. Gt block of this tile ([256 v][256 n], contiguous). Task id -> (16 v from v16, 8 n from n8); 16-lane
+  //    group gi handles tasks gi, gi+16, ...; lane p of the group ends with (v16 + p, n8 .. n8+7).
   char* gtblk = reinterpret_cast<char*>(Gt + ((int64_t)tn * Vp + v0) * BLK);
   const int gi = t >> 4, p = t & 15;
 #pragma unroll 4
@@ -595,7 +622,14 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           (bf16x4 LDS_AS*)(lds + nl * 512 + ((vl * 2) ^ (gsw(nl) << 4))));
     }
     const bf16x8 o{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
-    *reinterpret_cast<bf16x8*>(gtblk + (int64_t)(v16 + p) * 512 + n8 * 2) = o;
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o),
+                                reinterpret_cast<u32x4*>(gtblk + (int64_t)(v16 + p) * 512 + n8 * 2));
+  }
+  if (dbias_part != nullptr) {
+    __syncthreads();
+    const int c = t >> 3, e = t & 7;  // column v0 + t = chunk c, element e
+    dbias_part[(int64_t)tn * Vp + v0 + t] =
+        dbs[(0 * 32 + c) * 8 + e] + dbs[(1 * 32 + c) * 8 + e] + dbs[(2 * 32 + c) * 8 + e] + dbs[(3 * 32 + c) * 8 + e];
   }
 }
 
@@ -649,19 +683,46 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc).
+// Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
+// nk_total K stages. The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
+// order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
+// block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
+// 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
 template <bool OUT_BF16>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
-void k_gemm(Operand A, Operand B, int64_t kloop, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
-            void* __restrict__ C, int64_t ldc) {
+void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
+            int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+  const int b = (int)blockIdx.x;
+  int lin, s0 = 0, nk = nk_total, slot = -1;
+  if (b < full) {
+    lin = xcd_lin(b, full);
+  } else {
+    const int q = b - full;
+    lin = full + q / P;
+    const int p = q % P;
+    s0 = (int)((int64_t)nk_total * p / P);
+    nk = (int)((int64_t)nk_total * (p + 1) / P) - s0;
+    slot = q;
+  }
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, group, tm, tn);
+  tile_of(lin, tiles_m, tiles_n, group, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile(A, B, kloop, m0, n0, lds, acc);
+  gemm_tile(A, B, s0, nk, m0, n0, lds, acc);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
+  if (slot >= 0) {
+    float* pt = part + (int64_t)slot * BM * BN;
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          pt[(wm * 128 + acc_row(mi, r, lh)) * BN + wn * 128 + nj * 32 + lr] = acc[mi][nj][r];
+    return;
+  }
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int64_t j = n0 + wn * 128 + nj * 32 + lr;
@@ -681,6 +742,29 @@ void k_gemm(Operand A, Operand B, int64_t kloop, int64_t M, int64_t Nc, int tile
   }
 }
 
+// Sum of the P K-slices of each split tail tile into C (fixed order p = 0..P-1). Block (row block of 16, tile r).
+template <bool OUT_BF16>
+__global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ part, int P, int full, int tiles_m,
+                                                     int tiles_n, int group, int64_t M, int64_t Nc,
+                                                     void* __restrict__ C, int64_t ldc) {
+  const int r = (int)blockIdx.y;
+  int tm, tn;
+  tile_of(full + r, tiles_m, tiles_n, group, tm, tn);
+  const int jl = threadIdx.x;
+#pragma unroll 4
+  for (int il = (int)blockIdx.x * 16; il < (int)blockIdx.x * 16 + 16; ++il) {
+    float s = 0.f;
+    for (int p = 0; p < P; ++p) s += part[((int64_t)(r * P + p) * BM + il) * BN + jl];
+    const int64_t i = (int64_t)tm * BM + il, j = (int64_t)tn * BN + jl;
+    if (i < M && j < Nc) {
+      if constexpr (OUT_BF16)
+        reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)s;
+      else
+        reinterpret_cast<float*>(C)[i * ldc + j] = s;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // Host side: argument checks, workspace layout, launches.
 int g_last_hip_error = 0;
@@ -693,14 +777,15 @@ struct FwdWs {
   float *part_m, *part_s, *xy, *loss_part;
   size_t bytes;
 };
+// Forward workspace: per-half-tile (max, sum-exp) partials [2*tiles_v][N], target logits [N], loss partials.
 FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
-  const int64_t tv = cdiv(V, BM);
+  const int64_t T = 2 * cdiv(V, BM);
   FwdWs w{};
   size_t off = 0;
-  w.part_m = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * tv * N);
-  w.part_s = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * tv * N);
+  w.part_m = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
+  w.part_s = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N);
-  w.loss_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, 256));
+  w.loss_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, 32));
   w.bytes = off;
   return w;
 }
@@ -708,10 +793,11 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
 // Backward workspace (Np = N and Vp = V rounded up to 256):
 //   G   [Vp/256][Np][256] bf16, Gt [Np/256][Vp][256] bf16 (written by k_bwd_grad)
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
-//   dbias_part [Np/256][Vp] fp32
+//   dbias_part [Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split tails)
+constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
   uint16_t *G, *Gt, *Wt, *Ht;
-  float* dbias_part;
+  float *dbias_part, *xy, *part;
   int64_t np, vp;
   size_t bytes;
 };
@@ -725,6 +811,8 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.Wt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * K);
   w.Ht = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.np * K);
   w.dbias_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.vp * (w.np / BLK));
+  w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
+  w.part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * TAIL_SLOTS * BM * BN);
   w.bytes = off;
   return w;
 }
@@ -740,6 +828,34 @@ int check_common(const void* H, int64_t ldh, const void* W, int64_t ldw, int64_t
   if (cdiv(N, BN) * cdiv(V, BM) > INT32_MAX || cdiv(K, BN) * cdiv(V, BM) > INT32_MAX) return MCE_EINVAL;
   if ((int64_t)BM * (ldh > ldw ? ldh : ldw) * 2 > (int64_t(1) << 30)) return MCE_EINVAL;
   return MCE_OK;
+}
+
+int check_bias(const float* bias) { return (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 3)) ? MCE_EALIGN : MCE_OK; }
+
+// C = A . B^T over nk stages with the tile grid of k_gemm. When the tiles leave a partial last wave, the R tail
+// tiles are split into P = CUs / R K-slices (at least 2 stages each) so the last wave fills the GPU.
+int launch_status();
+template <bool OUT_BF16>
+int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t Nc, int group, void* C, int64_t ldc,
+                float* part, hipStream_t st) {
+  const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nc, BN), T = tiles_m * tiles_n;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess || cus <= 0)
+    cus = 256;
+  const int R = T > cus ? T % cus : 0;
+  int P = R ? cus / R : 1;
+  if (P > nk / 2) P = nk / 2;
+  if (R && P > TAIL_SLOTS / R) P = TAIL_SLOTS / R;
+  const int full = (R && P >= 2) ? T - R : T;
+  if (full == T) P = 1;
+  hipLaunchKernelGGL((k_gemm<OUT_BF16>), dim3(full + (T - full) * P), dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+                     tiles_m, tiles_n, group, full, P, C, ldc, part);
+  int rc = launch_status();
+  if (rc || full == T) return rc;
+  hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 16, T - full), dim3(BN), 0, st, part, P, full, tiles_m,
+                     tiles_n, group, M, Nc, C, ldc);
+  return launch_status();
 }
 
 int launch_status() {
@@ -786,6 +902,7 @@ int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
             float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum, void* ws, size_t ws_bytes,
             void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
   if (rc) return rc;
   if (loss_sum == nullptr) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -798,11 +915,14 @@ int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
-  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, N, V, V_real, tv, tn,
-                     w.part_m, w.part_s, w.xy);
+  hipLaunchKernelGGL(k_target_logit, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, N, K,
+                     V_real, w.xy);
   if ((rc = launch_status())) return rc;
-  const int nb = (int)cdiv(N, 256);
-  hipLaunchKernelGGL(k_fwd_merge, dim3(nb), dim3(256), 0, st, w.part_m, w.part_s, w.xy, y, gate, hit, N, V_real, tv,
+  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
+                     w.part_m, w.part_s);
+  if ((rc = launch_status())) return rc;
+  const int nb = (int)cdiv(N, 32);
+  hipLaunchKernelGGL(k_fwd_merge, dim3(nb), dim3(256), 0, st, w.part_m, w.part_s, w.xy, gate, hit, N, 2 * tv,
                      loss_rows, lse_rows, wgt_rows, dgr_rows, w.loss_part);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)nb, loss_sum);
@@ -814,6 +934,7 @@ int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64
                         const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
                         float* dGate, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
   if (rc) return rc;
   if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
   if (go == nullptr) return MCE_EINVAL;
@@ -827,8 +948,11 @@ int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
-  hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, go, N,
-                     w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt, dBias ? w.dbias_part : nullptr);
+  hipLaunchKernelGGL(k_target_logit, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, N, K,
+                     V_real, w.xy);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, w.xy,
+                     go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt, dBias ? w.dbias_part : nullptr);
   if ((rc = launch_status())) return rc;
   if (dBias) {
     hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
@@ -856,16 +980,11 @@ int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_
                      ldw, V, K, w.Wt);
   if ((rc = launch_status())) return rc;
   // dH[n, k] = sum_v G(n, v) Wt(k, v); G's columns V..Vp-1 are zero
-  const int tm = (int)cdiv(N, BM), tn = (int)cdiv(K, BN);
   const Operand Aop{w.G, BLK, N, w.vp, w.np * BLK};
   const Operand Bop{w.Wt, BLK, K, V, K * BLK};
-  if (dh_bf16)
-    hipLaunchKernelGGL((k_gemm<true>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, w.vp, N, K, tm, tn, 4, dH,
-                       lddh);
-  else
-    hipLaunchKernelGGL((k_gemm<false>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, w.vp, N, K, tm, tn, 4, dH,
-                       lddh);
-  return launch_status();
+  const int nk = (int)(w.vp / BK);
+  return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st)
+                 : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st);
 }
 
 int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_t V, float* dW, int64_t lddw,
@@ -886,11 +1005,9 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
                      ldh, N, K, w.Ht);
   if ((rc = launch_status())) return rc;
   // dW[v, k] = sum_n Gt(v, n) Ht(k, n), reduction over n < N
-  const int tm = (int)cdiv(V, BM), tn = (int)cdiv(K, BN);
   const Operand Aop{w.Gt, BLK, V, N, w.vp * BLK};
   const Operand Bop{w.Ht, BLK, K, N, K * BLK};
-  hipLaunchKernelGGL((k_gemm<false>), dim3(tm * tn), dim3(NTHREADS), 0, st, Aop, Bop, N, V, K, tm, tn, 4, dW, lddw);
-  return launch_status();
+  return launch_gemm<false>(Aop, Bop, (int)cdiv(N, BK), V, K, 4, dW, lddw, w.part, st);
 }
 
 int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
