@@ -13,11 +13,19 @@
  *   (wgt_n = dgr_n = 0 where P < 1e-30: the gradient of torch's clamp, full2.py:1925-1929)
  *   G_nv   = go wgt_n (exp(x_v - lse_n) - [v = y_n])
  *   dH = G W,  dW = G^T H,  dBias_v = sum_n G_nv,  dGate_n = go dgr_n
+ * Plain cross-entropy (gate = hit = NULL; `_LinearCE`, fused_ops.py:39-63): loss_n = lse_n - x_y, wgt_n = 1, no
+ *   clamp. A row whose target is outside [0, V_real) is ignored (loss_n = 0, wgt_n = 0), as with the
+ *   ignore_index of the reference's non-fused branch (full2.py:1864-1866).
+ * Sparse bias (`_LinearCESparse`, fused_ops.py:66-101; eager form full2.py:1920-1922): before all of the above,
+ *   x[n, cand[n, k]] += cval[n, k] for k < kc (repeated ids add up, ids outside [0, V_real) are ignored), and
+ *   dCval[n, k] = G[n, cand[n, k]].
  *
  * Conventions (all entry points):
  *   - bf16 tensors are passed as `const uint16_t*` (raw bf16 bits), row-major with an explicit leading dimension.
  *   - H is [N, K] (ldh), W is [V, K] (ldw). K, ldh and ldw must be multiples of 8; H and W 16-byte aligned.
- *   - y is int64 [N]; gate and hit are fp32 [N]. A target outside [0, V_real) has probability 0 (py = 0).
+ *   - y is int64 [N]; gate and hit are fp32 [N], or both NULL (plain cross-entropy, the `linear_ce` of
+ *     fused_ops.py:39-63,170-172). With the mixture, a target outside [0, V_real) has probability 0 (py = 0).
+ *   - cand is int64 [N, kc], cval fp32 [N, kc], 0 <= kc <= 8.
  *   - bias may be NULL (no bias; e.g. the `_head_w` layout of full2.py:1842-1851 that folds the bias into W).
  *   - Every call is asynchronous on `stream` (hipStream_t passed as void*); nothing synchronises the host.
  *   - Buffers are caller-owned. The library allocates no device memory: scratch lives in the caller's
@@ -70,6 +78,18 @@ MCE_API int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
             int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
             void* ws, size_t ws_bytes, void* stream);
 
+/*
+ * Forward of plain cross-entropy with a sparse additive logit bias (kc candidates per row, kc <= 8; kc = 0 is
+ * plain cross-entropy). Replaces `_LinearCESparse.forward` (fused_ops.py:71-91) minus its gradient GEMMs: the
+ * logits GEMM (fused_ops.py:82), the `scatter_add_` of the bias (fused_ops.py:84) and the loss half of
+ * `_ce_grad_kernel` (fused_ops.py:15-30). Outputs as mce_fwd (wgt_rows is 1, or 0 for an ignored row); uses the mce_fwd
+ * workspace.
+ */
+MCE_API int mce_fwd_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                   const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K, int64_t V,
+                   int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* ws,
+                   size_t ws_bytes, void* stream);
+
 /* Workspace bytes needed by the backward entry points for this shape: the bf16 gradient of the logits in two
  * K-blocked layouts (G, v contiguous, and G^T, n contiguous; each N x V rounded up to 256 x 256), the K-blocked
  * transposed copies W^T and H^T, and the dBias partial sums. Replaces the bf16 logits chunk that
@@ -88,6 +108,19 @@ MCE_API int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* 
                         const int64_t* y, const float* lse_rows, const float* wgt_rows, const float* dgr_rows,
                         const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
                         float* dGate, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Backward step 1 with a sparse logit bias: as mce_bwd_logits_grad for plain cross-entropy, G computed from
+ * the biased logits, plus dCval [N, kc] fp32 = go * G[n, cand[n, k]] (if dCval != NULL; 0 for ignored ids).
+ * Replaces the gradient half of `_ce_grad_kernel` (fused_ops.py:31-36), `gb = logits.gather(1, ci)`
+ * (fused_ops.py:86) and the `go` scaling of `_LinearCESparse.backward` (fused_ops.py:94-96). Steps 2 and 3
+ * (mce_bwd_dhidden, mce_bwd_dweight) follow unchanged.
+ */
+MCE_API int mce_bwd_logits_grad_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw,
+                               const float* bias, const int64_t* y, const int64_t* cand, const float* cval, int kc,
+                               const float* lse_rows, const float* wgt_rows, const float* go, int64_t N, int64_t K,
+                               int64_t V, int64_t V_real, float* dBias, float* dCval, void* ws, size_t ws_bytes,
+                               void* stream);
 
 /*
  * Backward step 2: dH = G W (fp32 accumulation). dH is [N, K] with row stride lddh, fp32 (dh_bf16 = 0) or

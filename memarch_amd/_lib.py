@@ -24,8 +24,11 @@ SIGNATURES = {
     "mce_last_hip_error": (_INT, []),
     "mce_fwd_ws_bytes": (_S, [_I, _I, _I]),
     "mce_fwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P]),
+    "mce_fwd_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _P, _P, _P, _P, _P, _S, _P]),
     "mce_bwd_ws_bytes": (_S, [_I, _I, _I]),
     "mce_bwd_logits_grad": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P]),
+    "mce_bwd_logits_grad_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _P, _P,
+                                          _P, _S, _P]),
     "mce_bwd_dhidden": (_INT, [_P, _I, _I, _I, _I, _P, _INT, _I, _P, _S, _P]),
     "mce_bwd_dweight": (_INT, [_P, _I, _I, _I, _I, _P, _I, _P, _S, _P]),
     "mce_bwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P,

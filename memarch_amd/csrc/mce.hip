@@ -29,7 +29,7 @@
 
 #include "../../include/mce.h"
 
-#define MCE_VERSION 300
+#define MCE_VERSION 310
 
 typedef int32_t mce_i32x4 __attribute__((ext_vector_type(4)));
 // The LLVM intrinsic behind `buffer_load_dword... lds`: (resource, LDS base, bytes per lane, per-lane offset,
@@ -393,23 +393,29 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
   }
 }
 
-// Target logit x_y = h_n . w_{y_n} + b_{y_n} of every row (fp32 dot product of the bf16 rows), -inf when y_n is
-// outside [0, V_real). One wave per row. The tile kernels compute the same sum in another order, so the two
-// agree to fp32 rounding.
-__global__ __launch_bounds__(256) void k_target_logit(const uint16_t* __restrict__ H, int64_t ldh,
-                                                      const uint16_t* __restrict__ W, int64_t ldw,
-                                                      const float* __restrict__ bias, const int64_t* __restrict__ y,
-                                                      int64_t N, int64_t K, int64_t Vreal, float* __restrict__ xy) {
-  const int lane = threadIdx.x & 63;
-  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;
-  const int64_t yn = y[n];
-  if (yn < 0 || yn >= Vreal) {
-    if (lane == 0) xy[n] = -INFINITY;
-    return;
-  }
-  const uint16_t* hr = H + n * ldh;
-  const uint16_t* wr = W + yn * ldw;
+// Sparse additive logit bias (`linear_ce_sparse`, fused_ops.py:66-101; the eager form full2.py:1920-1922): row
+// n adds cval[n, k] to the logit of vocabulary id cand[n, k] for k < kc. Repeated ids add up (scatter_add);
+// ids outside [0, V_real) are ignored.
+constexpr int MAX_KC = 8;  // sparse candidates per row
+
+// Total sparse bias of row n on vocabulary id c (0 when c is not a candidate).
+__device__ __forceinline__ float sparse_bias(const int64_t* cand, const float* cval, int kc, int64_t n, int64_t c) {
+  float b = 0.f;
+  for (int k = 0; k < kc; ++k)
+    if (cand[n * kc + k] == c) b += cval[n * kc + k];
+  return b;
+}
+// Is cand[n, k] a valid id that does not occur earlier in the row?
+__device__ __forceinline__ bool first_valid(const int64_t* cand, int kc, int64_t n, int k, int64_t Vreal) {
+  const int64_t c = cand[n * kc + k];
+  if (c < 0 || c >= Vreal) return false;
+  for (int j = 0; j < k; ++j)
+    if (cand[n * kc + j] == c) return false;
+  return true;
+}
+
+// h_n . w_c over K (fp32 products of the bf16 values), reduced over the wave; every lane gets the sum.
+__device__ __forceinline__ float row_dot(const uint16_t* hr, const uint16_t* wr, int64_t K, int lane) {
   float s = 0.f;
   for (int64_t k = (int64_t)lane * 8; k < K; k += 512) {
     const u16x8 a = *reinterpret_cast<const u16x8*>(hr + k);
@@ -419,13 +425,44 @@ __global__ __launch_bounds__(256) void k_target_logit(const uint16_t* __restrict
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  if (lane == 0) xy[n] = s + (bias != nullptr ? bias[yn] : 0.f);
+  return s;
+}
+
+// Per-row logits at the target and at the sparse candidates (h . w + bias, fp32 dot products of the bf16 rows):
+//   xy[n]    = x(n, y_n) + the sparse bias on y_n     (-inf when y_n is outside [0, V_real))
+//   xc[n, k] = x(n, cand[n, k]) without sparse bias   (-inf for ids outside [0, V_real); only when kc > 0)
+// One wave per row. The tile kernels compute the same sums in another order; the two agree to fp32 rounding.
+__global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__ H, int64_t ldh,
+                                                    const uint16_t* __restrict__ W, int64_t ldw,
+                                                    const float* __restrict__ bias, const int64_t* __restrict__ y,
+                                                    const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                    int kc, int64_t N, int64_t K, int64_t Vreal,
+                                                    float* __restrict__ xy, float* __restrict__ xc) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const uint16_t* hr = H + n * ldh;
+  const int64_t yn = y[n];
+  float x = -INFINITY;
+  if (yn >= 0 && yn < Vreal)
+    x = row_dot(hr, W + yn * ldw, K, lane) + (bias != nullptr ? bias[yn] : 0.f) + sparse_bias(cand, cval, kc, n, yn);
+  if (lane == 0) xy[n] = x;
+  for (int k = 0; k < kc; ++k) {
+    const int64_t c = cand[n * kc + k];
+    float xk = -INFINITY;
+    if (c >= 0 && c < Vreal) xk = row_dot(hr, W + c * ldw, K, lane) + (bias != nullptr ? bias[c] : 0.f);
+    if (lane == 0) xc[n * kc + k] = xk;
+  }
 }
 
 // Merge of the T per-half-tile partials: lse, loss, wgt, dgr per row; one loss partial sum per block.
 // 32 rows per block, 8 threads per row (an online max / rescaled sum over every 8th partial), combined in LDS.
+// With a sparse bias (kc > 0) the tiles saw the logits without it: each distinct valid candidate c then moves
+// its term of the sum from exp(x_c) to exp(x_c + B_c), with the maximum raised first so no term overflows.
 __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ part_m, const float* __restrict__ part_s,
-                                                   const float* __restrict__ xy, const float* __restrict__ gate,
+                                                   const float* __restrict__ xy, const int64_t* __restrict__ cand,
+                                                   const float* __restrict__ cval, const float* __restrict__ xc,
+                                                   int kc, int64_t Vreal, const float* __restrict__ gate,
                                                    const float* __restrict__ hit, int64_t N, int T,
                                                    float* __restrict__ loss_rows, float* __restrict__ lse_rows,
                                                    float* __restrict__ wgt_rows, float* __restrict__ dgr_rows,
@@ -460,17 +497,41 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (rm[i][r] != -INFINITY) S += rs[i][r] * expf(rm[i][r] - M);
+      if (kc > 0) {
+        float Mp = M;
+        for (int k = 0; k < kc; ++k)
+          if (first_valid(cand, kc, n, k, Vreal))
+            Mp = fmaxf(Mp, xc[n * kc + k] + sparse_bias(cand, cval, kc, n, cand[n * kc + k]));
+        float Sp = M == -INFINITY ? 0.f : S * expf(M - Mp);
+        for (int k = 0; k < kc; ++k)
+          if (first_valid(cand, kc, n, k, Vreal)) {
+            const float x = xc[n * kc + k], B = sparse_bias(cand, cval, kc, n, cand[n * kc + k]);
+            // exp(x + B - M') - exp(x - M'); expm1 keeps small |B| exact (and would overflow for large B)
+            Sp += B < 20.f ? expf(x - Mp) * expm1f(B) : expf(x + B - Mp) - expf(x - Mp);
+          }
+        M = Mp;
+        S = Sp;
+      }
       const float lse = M + logf(S);
-      const float py = expf(xy[n] - lse);
-      const float g = gate[n], h = hit[n];
-      const float P = (1.f - g) * py + g * h;
-      const bool clamped = !(P >= CLAMP_P);  // torch clamp(min) passes the gradient where P >= min
-      const float Pc = clamped ? CLAMP_P : P;
-      loss = -logf(Pc);
-      loss_rows[n] = loss;
       lse_rows[n] = lse;
-      wgt_rows[n] = clamped ? 0.f : (1.f - g) * py / Pc;
-      dgr_rows[n] = clamped ? 0.f : (py - h) / Pc;
+      if (gate == nullptr) {
+        // plain cross-entropy: loss = lse - x_y; a target outside [0, V_real) (xy = -inf) is ignored
+        const bool ok = xy[n] != -INFINITY;
+        loss = ok ? lse - xy[n] : 0.f;
+        loss_rows[n] = loss;
+        wgt_rows[n] = ok ? 1.f : 0.f;
+        if (dgr_rows != nullptr) dgr_rows[n] = 0.f;
+      } else {
+        const float py = expf(xy[n] - lse);
+        const float g = gate[n], h = hit[n];
+        const float P = (1.f - g) * py + g * h;
+        const bool clamped = !(P >= CLAMP_P);  // torch clamp(min) passes the gradient where P >= min
+        const float Pc = clamped ? CLAMP_P : P;
+        loss = -logf(Pc);
+        loss_rows[n] = loss;
+        wgt_rows[n] = clamped ? 0.f : (1.f - g) * py / Pc;
+        dgr_rows[n] = clamped ? 0.f : (py - h) / Pc;
+      }
     }
     rl[r] = loss;
   }
@@ -497,6 +558,37 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int
   if (t == 0) out[0] = red[0];
 }
 
+// Sparse fix-ups for k_bwd_grad, which writes go*wgt*exp(x - lse) from the logits without the sparse bias and
+// handles the target itself: entry (n, f) names a distinct valid candidate c != y_n of row n (fix_col, -1 when
+// unused) and its gradient go*wgt*exp(x_c + B_c - lse) (fix_val). dcval[n, k] = the logit gradient at
+// cand[n, k] (the reference's G.gather(1, cand)), 0 for ignored ids.
+__global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__ y, const int64_t* __restrict__ cand,
+                                                     const float* __restrict__ cval, int kc,
+                                                     const float* __restrict__ xy, const float* __restrict__ xc,
+                                                     const float* __restrict__ lse_rows,
+                                                     const float* __restrict__ wgt_rows, const float* __restrict__ go,
+                                                     int64_t N, int64_t Vreal, int* __restrict__ fix_col,
+                                                     float* __restrict__ fix_val, float* __restrict__ dcval) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const float cn = go[0] * wgt_rows[n], lse = lse_rows[n];
+  const int64_t yn = y[n];
+  int f = 0;
+  for (int k = 0; k < kc; ++k) {
+    const int64_t c = cand[n * kc + k];
+    float g = 0.f;
+    if (c >= 0 && c < Vreal)
+      g = c == yn ? cn * (expf(xy[n] - lse) - 1.f) : cn * expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - lse);
+    if (dcval != nullptr) dcval[n * kc + k] = g;
+    if (c != yn && first_valid(cand, kc, n, k, Vreal)) {
+      fix_col[n * MAX_KC + f] = (int)c;
+      fix_val[n * MAX_KC + f] = g;
+      ++f;
+    }
+  }
+  for (; f < MAX_KC; ++f) fix_col[n * MAX_KC + f] = -1;
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // Logits-grad tile: recompute S^T for the tile and form G = go*wgt*(exp(x - lse) - [v = y]) rounded to bf16,
 // written to both K-blocked layouts:
@@ -506,7 +598,8 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int
 // (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))):
 //   1. every lane writes go*wgt*exp(x - lse) for its 256 logits (8-byte writes);
 //   2. one thread per row overwrites the target element with go*wgt*(exp(x_y - lse) - 1), from the row's
-//      target logit (so the one-hot term is applied in fp32 before rounding, without searching registers);
+//      target logit (so the one-hot term is applied in fp32 before rounding, without searching registers),
+//      and, with a sparse bias, the row's candidate elements with their fix-up values (k_sparse_rows);
 //   3. G rows are copied out with ds_read_b128 (non-temporal stores: G is read back by another kernel, not
 //      by this one), and the same pass sums the bf16 G values of each column over
 //      the tile's rows (dBias partials, as the reference's dBias is the column sum of its bf16 G);
@@ -520,6 +613,7 @@ constexpr int GRAD_LDS_BYTES = LDS_BYTES + 4 * 32 * 8 * 4 + BM * 4;  // tile + [
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
                 const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ xy,
+                const int* __restrict__ fix_col, const float* __restrict__ fix_val, int nfix,
                 const float* __restrict__ go, int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal,
                 int tiles_v, int tiles_n, uint16_t* __restrict__ G, uint16_t* __restrict__ Gt,
                 float* __restrict__ dbias_part) {
@@ -547,6 +641,17 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 
   f32x16 acc[4][4];
   gemm_tile(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
+  // sparse fix-ups of row nf (nfix > 0 only with a sparse bias; the loads overlap the staging below)
+  int scol[MAX_KC];
+  float sval[MAX_KC];
+  if (nfix > 0) {
+#pragma unroll
+    for (int f = 0; f < MAX_KC; ++f) {
+      const bool ok = f < nfix && nf < N;
+      scol[f] = ok ? fix_col[nf * MAX_KC + f] : -1;
+      sval[f] = ok ? fix_val[nf * MAX_KC + f] : 0.f;
+    }
+  }
   float* bslot = reinterpret_cast<float*>(lds + LDS_BYTES + 4 * 32 * 8 * 4);
   stash_bias(bslot, btile, v0, Vreal);
   __syncthreads();
@@ -580,6 +685,14 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   if (fix) {
     const int vl = (int)(yf - v0);
     *reinterpret_cast<__bf16*>(lds + t * 512 + ((vl * 2) ^ (gsw(t) << 4))) = (__bf16)fval;
+  }
+  if (nfix > 0) {
+#pragma unroll
+    for (int f = 0; f < MAX_KC; ++f) {
+      const int64_t vl = (int64_t)scol[f] - v0;
+      if (scol[f] >= 0 && vl >= 0 && vl < BM)
+        *reinterpret_cast<__bf16*>(lds + t * 512 + ((int)(vl * 2) ^ (gsw(t) << 4))) = (__bf16)sval[f];
+    }
   }
   __syncthreads();
   // 3. G block of this tile ([256 n][256 v], contiguous): thread t copies 16-byte chunks t, t+256, ...; its
@@ -774,10 +887,11 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 struct FwdWs {
-  float *part_m, *part_s, *xy, *loss_part;
+  float *part_m, *part_s, *xy, *xc, *loss_part;
   size_t bytes;
 };
-// Forward workspace: per-half-tile (max, sum-exp) partials [2*tiles_v][N], target logits [N], loss partials.
+// Forward workspace: per-half-tile (max, sum-exp) partials [2*tiles_v][N], target logits [N], candidate
+// logits [N][MAX_KC] (sparse bias only), loss partials.
 FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
   const int64_t T = 2 * cdiv(V, BM);
   FwdWs w{};
@@ -785,6 +899,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
   w.part_m = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.part_s = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N);
+  w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * MAX_KC);
   w.loss_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, 32));
   w.bytes = off;
   return w;
@@ -794,10 +909,12 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
 //   G   [Vp/256][Np][256] bf16, Gt [Np/256][Vp][256] bf16 (written by k_bwd_grad)
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
 //   dbias_part [Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split tails)
+//   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), fix_col int32 / fix_val fp32 [Np][MAX_KC]
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
   uint16_t *G, *Gt, *Wt, *Ht;
-  float *dbias_part, *xy, *part;
+  float *dbias_part, *xy, *part, *xc, *fix_val;
+  int* fix_col;
   int64_t np, vp;
   size_t bytes;
 };
@@ -813,6 +930,9 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.dbias_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.vp * (w.np / BLK));
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
   w.part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * TAIL_SLOTS * BM * BN);
+  w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
+  w.fix_col = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * w.np * MAX_KC);
+  w.fix_val = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
   w.bytes = off;
   return w;
 }
@@ -867,6 +987,93 @@ int launch_status() {
   return MCE_OK;
 }
 
+int check_sparse(const int64_t* cand, const float* cval, int kc) {
+  if (kc < 0 || kc > MAX_KC) return MCE_EINVAL;
+  if (kc > 0 && (cand == nullptr || cval == nullptr)) return MCE_EINVAL;
+  return MCE_OK;
+}
+
+// Forward of every variant: gate and hit both given (mixture) or both null (plain cross-entropy); kc sparse
+// candidates per row (0: none).
+int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
+             const float* gate, const float* hit, const int64_t* cand, const float* cval, int kc, int64_t N,
+             int64_t K, int64_t V, int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows,
+             float* dgr_rows, float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
+  if (!rc) rc = check_sparse(cand, cval, kc);
+  if (rc) return rc;
+  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr)) return MCE_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N == 0) {
+    (void)hipMemsetAsync(loss_sum, 0, sizeof(float), st);
+    return launch_status();
+  }
+  if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
+  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
+  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
+  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
+                     kc, N, K, V_real, w.xy, w.xc);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
+                     w.part_m, w.part_s);
+  if ((rc = launch_status())) return rc;
+  const int nb = (int)cdiv(N, 32);
+  hipLaunchKernelGGL(k_fwd_merge, dim3(nb), dim3(256), 0, st, w.part_m, w.part_s, w.xy, cand, cval, w.xc, kc, V_real,
+                     gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, w.loss_part);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)nb, loss_sum);
+  return launch_status();
+}
+
+// Logits gradient of every variant: G (and G^T) into the workspace, plus dBias, dGate (mixture) and dCval
+// (sparse bias) when requested.
+int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
+              const int64_t* cand, const float* cval, int kc, const float* lse_rows, const float* wgt_rows,
+              const float* dgr_rows, const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
+              float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
+  if (!rc) rc = check_sparse(cand, cval, kc);
+  if (rc) return rc;
+  if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
+  if (go == nullptr) return MCE_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N == 0) {
+    if (dBias) (void)hipMemsetAsync(dBias, 0, sizeof(float) * V, st);
+    return launch_status();
+  }
+  if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows)) return MCE_EINVAL;
+  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
+  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
+  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
+                     kc, N, K, V_real, w.xy, w.xc);
+  if ((rc = launch_status())) return rc;
+  if (kc > 0) {
+    hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, y, cand, cval, kc, w.xy, w.xc,
+                       lse_rows, wgt_rows, go, N, V_real, w.fix_col, w.fix_val, dCval);
+    if ((rc = launch_status())) return rc;
+  }
+  hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, w.xy,
+                     w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                     dBias ? w.dbias_part : nullptr);
+  if ((rc = launch_status())) return rc;
+  if (dBias) {
+    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
+                       dBias);
+    if ((rc = launch_status())) return rc;
+  }
+  if (dGate) {
+    hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
+    if ((rc = launch_status())) return rc;
+  }
+  return MCE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -901,69 +1108,33 @@ int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
             const float* gate, const float* hit, int64_t N, int64_t K, int64_t V, int64_t V_real, float* loss_rows,
             float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum, void* ws, size_t ws_bytes,
             void* stream) {
-  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
-  if (!rc) rc = check_bias(bias);
-  if (rc) return rc;
-  if (loss_sum == nullptr) return MCE_EINVAL;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (N == 0) {
-    (void)hipMemsetAsync(loss_sum, 0, sizeof(float), st);
-    return launch_status();
-  }
-  if (!y || !gate || !hit || !loss_rows || !lse_rows || !wgt_rows || !dgr_rows || !ws) return MCE_EINVAL;
-  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
-  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
-  hipLaunchKernelGGL(k_target_logit, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, N, K,
-                     V_real, w.xy);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
-                     w.part_m, w.part_s);
-  if ((rc = launch_status())) return rc;
-  const int nb = (int)cdiv(N, 32);
-  hipLaunchKernelGGL(k_fwd_merge, dim3(nb), dim3(256), 0, st, w.part_m, w.part_s, w.xy, gate, hit, N, 2 * tv,
-                     loss_rows, lse_rows, wgt_rows, dgr_rows, w.loss_part);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)nb, loss_sum);
-  return launch_status();
+  return fwd_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, loss_rows, lse_rows,
+                  wgt_rows, dgr_rows, loss_sum, ws, ws_bytes, stream);
+}
+
+int mce_fwd_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                   const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K, int64_t V,
+                   int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* ws,
+                   size_t ws_bytes, void* stream) {
+  return fwd_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, cand, cval, kc, N, K, V, V_real, loss_rows, lse_rows,
+                  wgt_rows, nullptr, loss_sum, ws, ws_bytes, stream);
 }
 
 int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                         const int64_t* y, const float* lse_rows, const float* wgt_rows, const float* dgr_rows,
                         const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
                         float* dGate, void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
-  if (!rc) rc = check_bias(bias);
-  if (rc) return rc;
-  if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
-  if (go == nullptr) return MCE_EINVAL;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (N == 0) {
-    if (dBias) (void)hipMemsetAsync(dBias, 0, sizeof(float) * V, st);
-    return launch_status();
-  }
-  if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows)) return MCE_EINVAL;
-  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
-  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
-  hipLaunchKernelGGL(k_target_logit, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, N, K,
-                     V_real, w.xy);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, w.xy,
-                     go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt, dBias ? w.dbias_part : nullptr);
-  if ((rc = launch_status())) return rc;
-  if (dBias) {
-    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
-                       dBias);
-    if ((rc = launch_status())) return rc;
-  }
-  if (dGate) {
-    hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
-    if ((rc = launch_status())) return rc;
-  }
-  return MCE_OK;
+  return grad_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, 0, lse_rows, wgt_rows, dgr_rows, go, N, K, V, V_real,
+                   dBias, dGate, nullptr, ws, ws_bytes, stream);
+}
+
+int mce_bwd_logits_grad_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                               const int64_t* y, const int64_t* cand, const float* cval, int kc,
+                               const float* lse_rows, const float* wgt_rows, const float* go, int64_t N, int64_t K,
+                               int64_t V, int64_t V_real, float* dBias, float* dCval, void* ws, size_t ws_bytes,
+                               void* stream) {
+  return grad_impl(H, ldh, W, ldw, bias, y, cand, cval, kc, lse_rows, wgt_rows, nullptr, go, N, K, V, V_real, dBias,
+                   nullptr, dCval, ws, ws_bytes, stream);
 }
 
 int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16,

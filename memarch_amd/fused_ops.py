@@ -1,8 +1,9 @@
 """Fused vocabulary projection + cross-entropy + pointer mixture on MI355X, as torch.autograd.Functions.
 
-Drop-in for memarch's `fused_ops.linear_ce_mix` / `_LinearCEMix` (fused_ops.py:137-167): same call signature,
-same return value (the fp32 loss SUM over rows) and the same gradient convention (grads for h, w and gate in
-their own dtypes; None for y, hit and chunk). All device work runs in libmce.so (HIP, gfx950) on torch's
+Drop-in for memarch's `fused_ops.linear_ce_mix` / `_LinearCEMix` (fused_ops.py:137-167), `linear_ce` /
+`_LinearCE` (fused_ops.py:39-63,170-172) and `linear_ce_sparse` / `_LinearCESparse` (fused_ops.py:66-101): same
+call signatures, same return value (the fp32 loss SUM over rows) and the same gradient convention (grads for h,
+w, gate and the sparse values b in their own dtypes; None for y, hit, cand and chunk). All device work runs in libmce.so (HIP, gfx950) on torch's
 current stream; there is no other code path, and a tensor that is not on a GPU raises.
 
 Differences from the reference that autograd cannot observe: gradients are computed in `backward` by
@@ -15,6 +16,7 @@ import torch
 from . import _lib
 
 _BF16 = torch.bfloat16
+MAX_KC = 8   # sparse candidates per row of linear_ce_sparse (the library's limit)
 
 
 def _stream(dev):
@@ -49,9 +51,25 @@ def _rows(t, dtype):
     return t.detach().reshape(-1).to(dtype).contiguous()
 
 
-def _fwd_launch(h, w, bias, y, gate, hit, v_real):
-    """Validates the inputs, prepares the bf16 operands and runs mce_fwd on the current stream. Returns
-    (operands, per-row outputs, loss_sum, meta)."""
+def _check_sparse(cand, cval, n, gate):
+    """Validates the sparse-bias candidates / values [N, kc]; returns kc (0 without them)."""
+    if cand is None and cval is None:
+        return 0
+    if cand is None or cval is None:
+        raise ValueError("cand and b must be given together")
+    if cand.shape != cval.shape or cand.dim() != 2 or cand.shape[0] != n:
+        raise ValueError(f"cand {tuple(cand.shape)} and b {tuple(cval.shape)} must both be [N={n}, k]")
+    kc = cand.shape[1]
+    if kc > MAX_KC:
+        raise ValueError(f"at most {MAX_KC} sparse candidates per row are supported, got {kc}")
+    if kc and gate is not None:
+        raise ValueError("a sparse bias is supported with plain cross-entropy only (no gate/hit)")
+    return kc
+
+
+def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
+    """Validates the inputs, prepares the bf16 operands and runs mce_fwd (or mce_fwd_sparse when a sparse bias
+    cand/cval [N, k] is given) on the current stream. Returns (operands, per-row outputs, loss_sum, meta)."""
     if h.dim() != 2 or w.dim() != 2 or h.shape[1] != w.shape[1]:
         raise ValueError(f"h {tuple(h.shape)} and w {tuple(w.shape)} must be [N, K] and [V, K]")
     n, k = h.shape
@@ -60,65 +78,93 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real):
     if not 1 <= v_real <= v:
         raise ValueError(f"v_real={v_real} must be in [1, {v}]")
     for name, t in (("y", y), ("gate", gate), ("hit", hit)):
-        if t.numel() != n:
+        if t is not None and t.numel() != n:
             raise ValueError(f"{name} has {t.numel()} elements, expected {n}")
     if bias is not None and (bias.dim() != 1 or bias.shape[0] != v):
         raise ValueError(f"bias must be [V={v}], got {tuple(bias.shape)}")
-    _check_cuda(h, w, bias, y, gate, hit)
+    kc = _check_sparse(cand, cval, n, gate)
+    _check_cuda(h, w, bias, y, gate, hit, cand, cval)
     kp = (k + 7) // 8 * 8
     dev = h.device
     hd, wd = _bf16_operand(h, kp), _bf16_operand(w, kp)
     y64 = _rows(y, torch.int64)
-    gf, hf = _rows(gate, torch.float32), _rows(hit, torch.float32)
+    gf = None if gate is None else _rows(gate, torch.float32)   # None: g = 0 (plain cross-entropy)
+    hf = None if hit is None else _rows(hit, torch.float32)
     bf = None if bias is None else _rows(bias, torch.float32)
+    cand64 = cval32 = None
+    if kc:
+        cand64, cval32 = cand.detach().to(torch.int64).contiguous(), cval.detach().to(torch.float32).contiguous()
     f32 = dict(dtype=torch.float32, device=dev)
     loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
     loss_sum = torch.empty((), **f32)
     lib = _lib.load()
     ws_bytes = lib.mce_fwd_ws_bytes(n, kp, v)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    _lib.call("mce_fwd", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf), _ptr(hf),
-              n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum), _ptr(ws),
-              ws_bytes, _stream(dev))
+    if cand64 is not None:
+        _lib.call("mce_fwd_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
+                  _ptr(cand64), _ptr(cval32), kc, n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt),
+                  _ptr(loss_sum), _ptr(ws), ws_bytes, _stream(dev))
+        dgr.zero_()
+    else:
+        _lib.call("mce_fwd", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
+                  _ptr(hf), n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum),
+                  _ptr(ws), ws_bytes, _stream(dev))
     rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
-    return (hd, wd, bf, y64), rows, loss_sum, (n, k, kp, v, v_real)
+    return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real)
 
 
-def _forward(ctx, h, w, bias, y, gate, hit, v_real):
-    (hd, wd, bf, y64), rows, loss_sum, meta = _fwd_launch(h, w, bias, y, gate, hit, v_real)
-    ctx.save_for_backward(hd, wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"])
+def _forward(ctx, h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
+    (hd, wd, bf, y64, c64, cv32), rows, loss_sum, meta = _fwd_launch(h, w, bias, y, gate, hit, v_real, cand, cval)
+    ctx.save_for_backward(hd, wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"], c64, cv32)
     ctx.meta = meta
-    ctx.dtypes = (h.dtype, w.dtype, gate.dtype, None if bias is None else bias.dtype)
+    ctx.dtypes = (h.dtype, w.dtype, None if gate is None else gate.dtype, None if bias is None else bias.dtype,
+                  None if cval is None else cval.dtype)
     return loss_sum
 
 
+def _flat(t):
+    return None if t is None else t.reshape(-1)
+
+
+def _flat_k(t):
+    return None if t is None else t.reshape(-1, t.shape[-1])
+
+
 @torch.no_grad()
-def forward_rows(h, w, y, gate, hit, bias=None, v_real=None):
+def forward_rows(h, w, y, gate, hit, bias=None, v_real=None, cand=None, cval=None):
     """The forward pass without autograd: dict of the fp32 loss sum and the per-row loss, lse (logsumexp of the
-    row's logits), wgt = (1-g)py/P and dgr = (py-hit)/P (both 0 for rows under the 1e-30 clamp)."""
-    _, rows, loss_sum, _ = _fwd_launch(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), gate.reshape(-1),
-                                       hit.reshape(-1), v_real)
+    row's logits), wgt = (1-g)py/P and dgr = (py-hit)/P (both 0 for rows under the 1e-30 clamp). gate = hit =
+    None is plain cross-entropy (wgt = 1, dgr = 0), optionally with a sparse bias cand/cval [..., k]."""
+    _, rows, loss_sum, _ = _fwd_launch(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), _flat(gate), _flat(hit),
+                                       v_real, _flat_k(cand), _flat_k(cval))
     return dict(loss_sum=loss_sum, **rows)
 
 
-def _backward(ctx, go, need_h, need_w, need_b, need_g):
-    hd, wd, bf, y64, lse, wgt, dgr = ctx.saved_tensors
+def _backward(ctx, go, need_h, need_w, need_b, need_g, need_c=False):
+    """Gradients (dh, dw, dbias, dgate, dcval) for the inputs that need them (None for the others)."""
+    hd, wd, bf, y64, lse, wgt, dgr, c64, cv32 = ctx.saved_tensors
     n, k, kp, v, v_real = ctx.meta
-    hdt, wdt, gdt, bdt = ctx.dtypes
+    hdt, wdt, gdt, bdt, cdt = ctx.dtypes
     dev = hd.device
     go32 = go.detach().reshape(()).to(torch.float32).contiguous()
     f32 = dict(dtype=torch.float32, device=dev)
     dgate = torch.empty(n, **f32) if need_g else None
     dbias = torch.empty(v, **f32) if (need_b and bf is not None) else None
+    dcval = torch.empty(c64.shape, **f32) if (need_c and c64 is not None) else None
     dh = dw = None
-    if need_h or need_w or need_g or dbias is not None:
+    if need_h or need_w or need_g or dbias is not None or dcval is not None:
         lib = _lib.load()
         ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         st = _stream(dev)
-        _lib.call("mce_bwd_logits_grad", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
-                  _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(go32), n, kp, v, v_real, _ptr(dbias), _ptr(dgate),
-                  _ptr(ws), ws_bytes, st)
+        if c64 is not None:
+            _lib.call("mce_bwd_logits_grad_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf),
+                      _ptr(y64), _ptr(c64), _ptr(cv32), c64.shape[1], _ptr(lse), _ptr(wgt), _ptr(go32), n, kp, v,
+                      v_real, _ptr(dbias), _ptr(dcval), _ptr(ws), ws_bytes, st)
+        else:
+            _lib.call("mce_bwd_logits_grad", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
+                      _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(go32), n, kp, v, v_real, _ptr(dbias), _ptr(dgate),
+                      _ptr(ws), ws_bytes, st)
         if need_h:
             out_bf16 = hdt == _BF16
             dh = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev)
@@ -134,7 +180,9 @@ def _backward(ctx, go, need_h, need_w, need_b, need_g):
         dgate = dgate.to(gdt)
     if dbias is not None:
         dbias = dbias.to(bdt)
-    return dh, dw, dbias, dgate
+    if dcval is not None:
+        dcval = dcval.to(cdt)
+    return dh, dw, dbias, dgate, dcval
 
 
 class _LinearCEMix(torch.autograd.Function):
@@ -147,8 +195,40 @@ class _LinearCEMix(torch.autograd.Function):
     @staticmethod
     def backward(ctx, go):
         nh, nw, _, ng, _, _ = ctx.needs_input_grad
-        dh, dw, _, dg = _backward(ctx, go, nh, nw, False, ng)
+        dh, dw, _, dg, _ = _backward(ctx, go, nh, nw, False, ng)
         return dh, dw, None, dg, None, None
+
+
+class _LinearCE(torch.autograd.Function):
+    """forward(ctx, h [N,K], w [V,K], y [N], chunk) -> fp32 sum over rows of lse - x_y (fused_ops.py:39-63);
+    gradients softmax - onehot. Rows whose target is outside [0, V) are ignored (loss 0, no gradient)."""
+
+    @staticmethod
+    def forward(ctx, h, w, y, chunk):
+        return _forward(ctx, h, w, None, y, None, None, None)
+
+    @staticmethod
+    def backward(ctx, go):
+        nh, nw, _, _ = ctx.needs_input_grad
+        dh, dw, _, _, _ = _backward(ctx, go, nh, nw, False, False)
+        return dh, dw, None, None
+
+
+class _LinearCESparse(torch.autograd.Function):
+    """forward(ctx, h [N,K], w [V,K], y [N], cand [N,k] int64, b [N,k], chunk) -> fp32 cross-entropy sum of the
+    logits h w^T with b[n, j] added at column cand[n, j] (repeated ids add up) (fused_ops.py:66-96). The
+    gradient of b is the logit gradient at the candidates, G.gather(1, cand) (fused_ops.py:86); b is not rounded
+    to bf16 (the reference adds it to bf16 logits; the eager form full2.py:1920-1922 adds it in fp32)."""
+
+    @staticmethod
+    def forward(ctx, h, w, y, cand, b, chunk):
+        return _forward(ctx, h, w, None, y, None, None, None, cand, b)
+
+    @staticmethod
+    def backward(ctx, go):
+        nh, nw, _, _, nb, _ = ctx.needs_input_grad
+        dh, dw, _, _, dc = _backward(ctx, go, nh, nw, False, False, nb)
+        return dh, dw, None, None, dc, None
 
 
 class _LinearCEMixBiased(torch.autograd.Function):
@@ -162,7 +242,7 @@ class _LinearCEMixBiased(torch.autograd.Function):
     @staticmethod
     def backward(ctx, go):
         nh, nw, nb, _, ng, _, _ = ctx.needs_input_grad
-        dh, dw, db, dg = _backward(ctx, go, nh, nw, nb, ng)
+        dh, dw, db, dg, _ = _backward(ctx, go, nh, nw, nb, ng)
         return dh, dw, db, None, dg, None, None
 
 
@@ -173,8 +253,22 @@ def linear_ce_mix(h, w, y, gate, hit, chunk=4096):
 
 
 @torch.compiler.disable
+def linear_ce(h, w, y, chunk=4096):
+    """Sum over rows of cross-entropy of logits h w^T against y, logits never stored (fused_ops.py:170-172)."""
+    return _LinearCE.apply(h.reshape(-1, h.shape[-1]), w, y.reshape(-1), chunk)
+
+
+@torch.compiler.disable
+def linear_ce_sparse(h, w, y, cand, b, chunk=4096):
+    """linear_ce with the sparse logit bias logits[n, cand[n, j]] += b[n, j], j < k <= 8 (fused_ops.py:99-101)."""
+    return _LinearCESparse.apply(h.reshape(-1, h.shape[-1]), w, y.reshape(-1),
+                                 cand.reshape(-1, cand.shape[-1]).long(), b.reshape(-1, b.shape[-1]), chunk)
+
+
+@torch.compiler.disable
 def linear_ce_mix_biased(h, w, bias, y, gate, hit, v_real=None, chunk=4096):
-    """linear_ce_mix with logits h w^T + bias (fp32) and ids >= v_real masked out; also returns dBias."""
+    """linear_ce_mix with logits h w^T + bias (fp32) and ids >= v_real masked out; also returns dBias. gate and
+    hit may both be None (plain cross-entropy)."""
     del chunk
-    return _LinearCEMixBiased.apply(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), gate.reshape(-1),
-                                    hit.reshape(-1), v_real)
+    return _LinearCEMixBiased.apply(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), _flat(gate), _flat(hit),
+                                    v_real)

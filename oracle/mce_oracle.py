@@ -12,8 +12,14 @@ Two independent restatements of the reference's eager formula (full2.py:1917-192
       wgt    = (1 - g) py / P ; dgr = (py - hit) / P ; both 0 where P < 1e-30  (torch clamp backward)
       G      = go wgt (softmax - onehot) ; dH = G W ; dW = G^T H ; dBias = sum_n G ; dGate = go dgr
   The reference's fused Triton path computes the same quantities (fused_ops.py:113-134).
+  Plain cross-entropy (gate = hit = None; `_LinearCE`, fused_ops.py:39-63): loss = lse - x_y, wgt = 1, no
+  clamp; a target outside [0, v_real) is ignored (loss 0, wgt 0).
+  Sparse bias (cand, cval [N, k]; `_LinearCESparse`, fused_ops.py:66-96, eager form full2.py:1920-1922):
+  x[n, cand[n, j]] += cval[n, j] before everything else (repeated ids add up; ids outside [0, v_real) are
+  ignored); dcval[n, j] = G[n, cand[n, j]].
 * `eager_ce_part`: the eager formula written with torch ops exactly as `_ce_part` composes them; torch
   autograd supplies its gradients, independently of the closed form above.
+* `eager_ce_sparse`: the sparse-bias eager form (scatter_add on fp32 logits, full2.py:1920-1923) in torch.
 
 Pinning (tests/test_oracle.py): closed form vs torch autograd in fp64; central finite differences on tiny
 shapes; g = 0 against torch.nn.functional.cross_entropy; hit = 0 gradient = plain CE gradient; hit = 1,
@@ -32,10 +38,15 @@ def bf16_round(a):
     return r.view(np.float32)
 
 
-def _logits(hc, w, bias, v_real, dt):
+def _logits(hc, w, bias, v_real, dt, cand=None, cval=None):
     x = hc.astype(dt, copy=False) @ w.astype(dt, copy=False).T
     if bias is not None:
         x += bias.astype(dt, copy=False)[None, :]
+    if cand is not None:
+        vr = w.shape[0] if v_real is None else v_real
+        ok = (cand >= 0) & (cand < vr)
+        rows = np.broadcast_to(np.arange(len(cand))[:, None], cand.shape)
+        np.add.at(x, (rows[ok], cand[ok]), cval[ok].astype(dt))
     if v_real is not None and v_real < w.shape[0]:
         x[:, v_real:] = -np.inf
     return x
@@ -46,19 +57,30 @@ def _lse(x):
     return m + np.log(np.exp(x - m[:, None]).sum(axis=1))
 
 
-def forward(h, w, y, gate, hit, bias=None, v_real=None, dtype=np.float64, chunk=1024):
-    """Per-row quantities of the forward pass. h [N,K], w [V,K], bias [V] or None, y/gate/hit [N]."""
+def _chunk(a, i, chunk):
+    return None if a is None else a[i:i + chunk]
+
+
+def forward(h, w, y, gate, hit, bias=None, v_real=None, dtype=np.float64, chunk=1024, cand=None, cval=None):
+    """Per-row quantities of the forward pass. h [N,K], w [V,K], bias [V] or None, y/gate/hit [N] (gate = hit =
+    None: plain cross-entropy), cand/cval [N, k] or None (sparse logit bias)."""
     N = h.shape[0]
     V = w.shape[0]
     vr = V if v_real is None else v_real
     lse = np.empty(N, dtype)
     xy = np.empty(N, dtype)
     for i in range(0, N, chunk):
-        x = _logits(h[i:i + chunk], w, bias, v_real, dtype)
+        x = _logits(h[i:i + chunk], w, bias, v_real, dtype, _chunk(cand, i, chunk), _chunk(cval, i, chunk))
         lse[i:i + chunk] = _lse(x)
         yc = y[i:i + chunk]
         ok = (yc >= 0) & (yc < vr)
         xy[i:i + chunk] = np.where(ok, x[np.arange(len(yc)), np.clip(yc, 0, V - 1)], -np.inf)
+    if gate is None:
+        ok = (y >= 0) & (y < vr)
+        loss = np.where(ok, lse - np.where(ok, xy, 0), 0.0)
+        wgt = ok.astype(dtype)
+        return dict(loss_rows=loss, loss_sum=loss.sum(), lse=lse, xy=xy, py=np.exp(xy - lse), wgt=wgt,
+                    dgr=np.zeros(N, dtype))
     g = gate.astype(dtype)
     ht = hit.astype(dtype)
     py = np.exp(xy - lse)
@@ -85,28 +107,35 @@ def grad_logits(x, lse, y, wgt, go, v_real=None):
 
 
 def backward(h, w, y, gate, hit, bias=None, v_real=None, go=1.0, fwd=None, dtype=np.float64, chunk=1024,
-             round_g=None):
-    """Closed-form gradients (dH [N,K], dW [V,K], dBias [V], dGate [N]). `round_g` (a function) is applied to
-    G before the two contractions, e.g. bf16_round to model a bf16 G operand."""
+             round_g=None, cand=None, cval=None):
+    """Closed-form gradients (dH [N,K], dW [V,K], dBias [V], dGate [N], dCval [N, k] with a sparse bias).
+    `round_g` (a function) is applied to G before the two contractions, e.g. bf16_round to model a bf16 G
+    operand."""
     if fwd is None:
-        fwd = forward(h, w, y, gate, hit, bias, v_real, dtype, chunk)
+        fwd = forward(h, w, y, gate, hit, bias, v_real, dtype, chunk, cand, cval)
     N, K = h.shape
     V = w.shape[0]
+    vr = V if v_real is None else v_real
     wt = w.astype(dtype)
     dh = np.empty((N, K), dtype)
     dw = np.zeros((V, K), dtype)
     db = np.zeros(V, dtype)
+    dc = None if cand is None else np.zeros(cand.shape, dtype)
     for i in range(0, N, chunk):
         hc = h[i:i + chunk].astype(dtype)
-        x = _logits(hc, w, bias, v_real, dtype)
+        cc = _chunk(cand, i, chunk)
+        x = _logits(hc, w, bias, v_real, dtype, cc, _chunk(cval, i, chunk))
         G = grad_logits(x, fwd["lse"][i:i + chunk], y[i:i + chunk], fwd["wgt"][i:i + chunk], go, v_real)
         db += G.sum(axis=0)
+        if cc is not None:
+            ok = (cc >= 0) & (cc < vr)
+            dc[i:i + chunk] = np.where(ok, G[np.arange(len(cc))[:, None], np.clip(cc, 0, V - 1)], 0.0)
         if round_g is not None:
             G = round_g(G.astype(np.float32)).astype(dtype)
         dh[i:i + chunk] = G @ wt
         dw += G.T @ hc
     dgate = go * fwd["dgr"]
-    return dict(dh=dh, dw=dw, dbias=db, dgate=dgate)
+    return dict(dh=dh, dw=dw, dbias=db, dgate=dgate, dcval=dc)
 
 
 def eager_ce_part(hn, W, bias, y, c1, g):
@@ -123,6 +152,20 @@ def eager_ce_part(hn, W, bias, y, c1, g):
     ly = lo.gather(-1, y[..., None])[..., 0]
     py = (ly - lse).exp()
     return -torch.log(((1 - g) * py + g * (c1 == y).to(py.dtype)).clamp(min=1e-30)).sum()
+
+
+def eager_ce_sparse(hn, W, bias, y, cand, val):
+    """torch restatement of the sparse-bias branch of `_ce_part` (full2.py:1917-1923,1930): lo = head(hn).float()
+    (+ head_bias); lo = lo.scatter_add(-1, cand, val); loss = (logsumexp(lo) - lo.gather(y)).sum()."""
+    import torch
+    lo = hn @ W.T
+    lo = lo.to(torch.promote_types(lo.dtype, torch.float32))
+    if bias is not None:
+        lo = lo + bias.to(lo.dtype)
+    lo = lo.scatter_add(-1, cand.long(), val.to(lo.dtype))
+    lse = torch.logsumexp(lo, -1)
+    ly = lo.gather(-1, y[..., None])[..., 0]
+    return (lse - ly).sum()
 
 
 def rel_fro(a, b):

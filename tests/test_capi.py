@@ -62,3 +62,23 @@ def test_argument_checks_need_no_gpu(lib):
     a[0] = p + 2                                                 # misaligned H
     assert lib.mce_fwd(*a) == 2
     assert lib.mce_bwd_dweight(p, 8, 16, 8, 32, p, 4, p, 1 << 30, None) == 1   # lddw < K
+
+
+def test_sparse_and_plain_argument_checks(lib):
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256
+    # mce_fwd: gate given without hit (or the reverse) is rejected; both NULL is plain cross-entropy
+    assert lib.mce_fwd(p, 8, p, 8, None, p, p, None, 16, 8, 32, 32, p, p, p, p, p, p, 1 << 30, None) == 1
+    assert lib.mce_fwd(p, 8, p, 8, None, p, None, p, 16, 8, 32, 32, p, p, p, p, p, p, 1 << 30, None) == 1
+    sp = lambda kc, cand, cval: (p, 8, p, 8, None, p, cand, cval, kc, 16, 8, 32, 32, p, p, p, p, p, 1 << 30, None)
+    assert lib.mce_fwd_sparse(*sp(9, p, p)) == 1                 # kc above the limit of 8
+    assert lib.mce_fwd_sparse(*sp(-1, p, p)) == 1
+    assert lib.mce_fwd_sparse(*sp(2, None, p)) == 1              # candidates without values
+    a = list(sp(2, p, p))
+    a[18] = 16
+    assert lib.mce_fwd_sparse(*a) == 3                           # workspace too small
+    g = lambda kc: (p, 8, p, 8, None, p, p, p, kc, p, p, p, 16, 8, 32, 32, None, p, p, 1 << 30, None)
+    assert lib.mce_bwd_logits_grad_sparse(*g(9)) == 1
+    a = list(g(2))
+    a[16] = p                                                    # dBias without a bias
+    assert lib.mce_bwd_logits_grad_sparse(*a) == 1

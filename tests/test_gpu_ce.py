@@ -1,0 +1,168 @@
+"""GPU parity of plain cross-entropy (`linear_ce`, reference fused_ops.py:39-63,170-172) and of cross-entropy
+with a sparse logit bias (`linear_ce_sparse`, fused_ops.py:66-101) against the CPU oracle's fp64 evaluation on
+the same bf16-rounded operands. Bar: loss within 1e-3 relative; dH, dW, dBias and the gradient of the sparse
+values within 2e-2 relative Frobenius.
+"""
+import numpy as np
+import pytest
+import torch
+
+from cases import GRAD_RTOL, LOSS_RTOL
+from oracle import mce_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _case(N, K, V, kc=0, seed=0, w_scale=0.05, v_scale=2.0, v_real=None, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    vr = V if v_real is None else v_real
+    c = dict(h=torch.randn(N, K, generator=g), w=torch.randn(V, K, generator=g) * w_scale,
+             y=torch.randint(0, vr, (N,), generator=g), v_real=vr,
+             bias=torch.randn(V, generator=g) if bias else None)
+    if kc:
+        cand = torch.randint(0, vr, (N, kc), generator=g)
+        # candidates near the target, a repeated id, the target itself and ignored ids
+        cand[::3, 0] = c["y"][::3]
+        if kc > 1:
+            cand[1::4, 1] = cand[1::4, 0]
+            cand[2::5, kc - 1] = -1
+            cand[3::7, kc - 1] = V + 5
+        c["cand"] = cand
+        c["cval"] = torch.randn(N, kc, generator=g) * v_scale
+    return c
+
+
+def _oracle(c, go=1.0):
+    h = orc.bf16_round(c["h"].numpy())
+    w = orc.bf16_round(c["w"].numpy())
+    b = None if c["bias"] is None else c["bias"].numpy()
+    vr = c["v_real"] if c["v_real"] != c["w"].shape[0] else None
+    cand = c.get("cand")
+    cand = None if cand is None else cand.numpy()
+    cval = c.get("cval")
+    cval = None if cval is None else cval.numpy()
+    y = c["y"].numpy()
+    fwd = orc.forward(h, w, y, None, None, b, vr, np.float64, cand=cand, cval=cval)
+    bwd = orc.backward(h, w, y, None, None, b, vr, go, fwd, np.float64, cand=cand, cval=cval)
+    return fwd, bwd
+
+
+def _check(what, loss, fwd, grads, bwd):
+    lref = float(fwd["loss_sum"])
+    errs = dict(loss=abs(float(loss) - lref) / max(abs(lref), 1e-30))
+    for k, v in grads.items():
+        errs[k] = orc.rel_fro(v.float().cpu().numpy(), bwd[k])
+    print(what, {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert errs["loss"] <= LOSS_RTOL, (what, errs)
+    for k in grads:
+        assert errs[k] <= GRAD_RTOL, (what, k, errs)
+
+
+@pytest.mark.parametrize("shape", [(256, 128, 512), (300, 72, 1000), (777, 520, 2051), (64, 2064, 1024)],
+                         ids=lambda s: "N{}_K{}_V{}".format(*s))
+def test_linear_ce_parity(shape):
+    from memarch_amd import fused_ops
+    N, K, V = shape
+    print(f"linear_ce {shape}", flush=True)
+    c = _case(N, K, V, seed=N + V)
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    loss = fused_ops.linear_ce(h, w, c["y"].cuda())
+    loss.backward()
+    fwd, bwd = _oracle(c)
+    _check(f"linear_ce {shape}", loss, fwd, dict(dh=h.grad, dw=w.grad), bwd)
+    # the same loss as torch's cross_entropy on the bf16 operands
+    x = h.detach().double() @ w.detach().bfloat16().double().T
+    ce = torch.nn.functional.cross_entropy(x, c["y"].cuda(), reduction="sum")
+    assert abs(float(loss) - float(ce)) <= LOSS_RTOL * abs(float(ce))
+
+
+def test_linear_ce_large_losses_are_not_clamped():
+    """Logits with spread ~25: many rows have lse - x_y above -log(1e-30) = 69.08, which the mixture would clamp."""
+    from memarch_amd import fused_ops
+    c = _case(200, 64, 700, seed=5, w_scale=3.0)
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    loss = fused_ops.linear_ce(h, w, c["y"].cuda())
+    (loss * 0.01).backward()
+    fwd, bwd = _oracle(c, go=0.01)
+    assert (fwd["loss_rows"] > 69.1).sum() > 10
+    _check("linear_ce large", loss, fwd, dict(dh=h.grad, dw=w.grad), bwd)
+
+
+def test_plain_ce_with_bias_mask_and_ignored_rows():
+    """gate = hit = None through the bias-explicit form: fp32 bias, padded ids masked, y = -100 rows ignored."""
+    from memarch_amd import fused_ops
+    c = _case(513, 256, 1300, seed=9, v_real=1250, bias=True)
+    c["y"][::17] = -100
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    b = c["bias"].cuda().requires_grad_()
+    loss = fused_ops.linear_ce_mix_biased(h, w, b, c["y"].cuda(), None, None, v_real=1250)
+    loss.backward()
+    fwd, bwd = _oracle(c)
+    assert fwd["loss_rows"][0] == 0.0
+    _check("plain biased", loss, fwd, dict(dh=h.grad, dw=w.grad, dbias=b.grad), bwd)
+    rows = fused_ops.forward_rows(h.detach(), w.detach(), c["y"].cuda(), None, None, bias=b.detach(), v_real=1250)
+    assert float(rows["loss_rows"][0]) == 0.0 and float(rows["wgt"][0]) == 0.0
+
+
+SPARSE = [
+    # (N, K, V, kc, value scale)
+    (256, 128, 512, 3, 2.0),
+    (300, 72, 1000, 1, 1.0),
+    (777, 520, 2051, 8, 3.0),     # the largest kc
+    (129, 2064, 1024, 2, 8.0),    # candidates dominate their rows
+    (200, 256, 800, 4, -20.0),    # candidates pushed far below the rest
+]
+
+
+@pytest.mark.parametrize("shape", SPARSE, ids=lambda s: "N{}_K{}_V{}_kc{}_s{}".format(*s))
+def test_linear_ce_sparse_parity(shape):
+    from memarch_amd import fused_ops
+    N, K, V, kc, scale = shape
+    print(f"linear_ce_sparse {shape}", flush=True)
+    c = _case(N, K, V, kc, seed=N + kc, v_scale=scale)
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    b = c["cval"].cuda().requires_grad_()
+    loss = fused_ops.linear_ce_sparse(h, w, c["y"].cuda(), c["cand"].cuda(), b)
+    (loss * 0.5).backward()
+    fwd, bwd = _oracle(c, go=0.5)
+    assert b.grad.shape == (N, kc) and b.grad.dtype == torch.float32
+    _check(f"sparse {shape}", loss, fwd, dict(dh=h.grad, dw=w.grad, dcval=b.grad), bwd)
+    # repeated ids share one gradient; ignored ids get none
+    cand, g = c["cand"], b.grad.cpu()
+    if kc > 1:
+        same = cand[:, 1] == cand[:, 0]
+        assert torch.equal(g[same, 1], g[same, 0])
+        assert torch.all(g[(cand < 0) | (cand >= V)] == 0)
+
+
+def test_sparse_with_bias_forward_rows():
+    """The sparse forward with an fp32 bias and masked padded ids (mce_fwd_sparse with bias != NULL)."""
+    from memarch_amd import fused_ops
+    c = _case(300, 128, 900, 3, seed=21, v_real=880, bias=True)
+    rows = fused_ops.forward_rows(c["h"].cuda().bfloat16(), c["w"].cuda(), c["y"].cuda(), None, None,
+                                  bias=c["bias"].cuda(), v_real=880, cand=c["cand"].cuda(), cval=c["cval"].cuda())
+    fwd, _ = _oracle(c)
+    got = rows["loss_rows"].cpu().numpy()
+    assert orc.rel_fro(got, fwd["loss_rows"]) <= LOSS_RTOL
+    assert orc.rel_fro(rows["lse"].cpu().numpy(), fwd["lse"]) <= LOSS_RTOL
+
+
+def test_sparse_zero_values_equal_plain():
+    from memarch_amd import fused_ops
+    c = _case(256, 128, 700, 3, seed=4)
+    h, w, y = c["h"].cuda().bfloat16(), c["w"].cuda(), c["y"].cuda()
+    plain = fused_ops.forward_rows(h, w, y, None, None)
+    sp = fused_ops.forward_rows(h, w, y, None, None, cand=c["cand"].cuda(), cval=torch.zeros(256, 3).cuda())
+    # equal up to fp32 rounding (the merge's running maximum may move by the candidate logits' rounding)
+    torch.testing.assert_close(sp["loss_rows"], plain["loss_rows"], rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(sp["lse"], plain["lse"], rtol=1e-6, atol=1e-6)

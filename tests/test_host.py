@@ -36,3 +36,32 @@ def test_shape_validation_before_any_launch():
     with pytest.raises(ValueError, match="gate"):
         fused_ops._forward(None, torch.randn(4, 8, **meta), torch.randn(16, 8, **meta), None,
                            torch.zeros(4, **meta), torch.zeros(3, **meta), torch.zeros(4, **meta), None)
+
+
+def test_reference_signatures_ce_and_sparse():
+    # fused_ops.py:41 forward(ctx, h, w, y, chunk); :71 forward(ctx, h, w, y, cand, b, chunk);
+    # :99 linear_ce_sparse(h, w, y, cand, b, chunk=4096); :170 linear_ce(h, w, y, chunk=4096)
+    assert list(inspect.signature(fused_ops._LinearCE.forward).parameters) == ["ctx", "h", "w", "y", "chunk"]
+    assert list(inspect.signature(fused_ops._LinearCESparse.forward).parameters) == \
+        ["ctx", "h", "w", "y", "cand", "b", "chunk"]
+    assert list(inspect.signature(fused_ops.linear_ce).parameters) == ["h", "w", "y", "chunk"]
+    sig = inspect.signature(fused_ops.linear_ce_sparse)
+    assert list(sig.parameters) == ["h", "w", "y", "cand", "b", "chunk"]
+    assert sig.parameters["chunk"].default == 4096
+
+
+def test_sparse_validation_before_any_launch():
+    meta = dict(device="meta")
+    h, w, y = torch.randn(4, 8, **meta), torch.randn(16, 8, **meta), torch.zeros(4, dtype=torch.long, **meta)
+    with pytest.raises(ValueError, match="at most 8"):
+        fused_ops._forward(None, h, w, None, y, None, None, None, torch.zeros(4, 9, dtype=torch.long, **meta),
+                           torch.zeros(4, 9, **meta))
+    with pytest.raises(ValueError, match="must both be"):
+        fused_ops._forward(None, h, w, None, y, None, None, None, torch.zeros(4, 3, dtype=torch.long, **meta),
+                           torch.zeros(4, 2, **meta))
+    with pytest.raises(ValueError, match="plain cross-entropy only"):
+        fused_ops._forward(None, h, w, None, y, torch.zeros(4, **meta), torch.zeros(4, **meta), None,
+                           torch.zeros(4, 3, dtype=torch.long, **meta), torch.zeros(4, 3, **meta))
+    with pytest.raises(ValueError, match="GPU only"):
+        fused_ops.linear_ce_sparse(torch.randn(4, 8), torch.randn(16, 8), torch.zeros(4, dtype=torch.long),
+                                   torch.zeros(4, 2, dtype=torch.long), torch.zeros(4, 2))
