@@ -19,6 +19,8 @@
  * Sparse bias (`_LinearCESparse`, fused_ops.py:66-101; eager form full2.py:1920-1922): before all of the above,
  *   x[n, cand[n, k]] += cval[n, k] for k < kc (repeated ids add up, ids outside [0, V_real) are ignored), and
  *   dCval[n, k] = G[n, cand[n, k]].
+ * (lse, x_y) per row (`_ChunkCE`, full2.py:753-836): the forward returns lse_n and ly_n = x_y; for upstream
+ *   gradients g_lse, g_ly [N] the gradient of the logits is G_nv = g_lse_n exp(x_v - lse_n) + g_ly_n [v = y_n].
  *
  * Conventions (all entry points):
  *   - bf16 tensors are passed as `const uint16_t*` (raw bf16 bits), row-major with an explicit leading dimension.
@@ -121,6 +123,26 @@ MCE_API int mce_bwd_logits_grad_sparse(const uint16_t* H, int64_t ldh, const uin
                                const float* lse_rows, const float* wgt_rows, const float* go, int64_t N, int64_t K,
                                int64_t V, int64_t V_real, float* dBias, float* dCval, void* ws, size_t ws_bytes,
                                void* stream);
+
+/*
+ * Forward of `chunk_ce` (full2.py:753-790): per row the logsumexp of the logits (lse_rows) and the target logit
+ * ly_rows = h . W_y + b_y (fp32 [N] each; -inf where y is outside [0, V_real)). Replaces the vocabulary-chunk
+ * loop of `_ChunkCE.forward` (full2.py:766-778) and its target dot product (full2.py:785-787). Uses the mce_fwd
+ * workspace.
+ */
+MCE_API int mce_lse_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                const int64_t* y, int64_t N, int64_t K, int64_t V, int64_t V_real, float* lse_rows, float* ly_rows,
+                void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Backward step 1 of `chunk_ce`: G = g_lse softmax + g_ly onehot (bf16, both layouts) into the workspace from the
+ * forward's lse_rows and the upstream gradients g_lse, g_ly (fp32 [N], device); dBias (if dBias != NULL) is the
+ * column sum of G. Replaces the per-chunk G of `_ChunkCE.backward` (full2.py:814-815) and `db` (full2.py:828-829);
+ * steps 2 and 3 (mce_bwd_dhidden, mce_bwd_dweight) replace its dh and dW products (full2.py:816-827).
+ */
+MCE_API int mce_bwd_lse_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                     const int64_t* y, const float* lse_rows, const float* g_lse, const float* g_ly, int64_t N,
+                     int64_t K, int64_t V, int64_t V_real, float* dBias, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Backward step 2: dH = G W (fp32 accumulation). dH is [N, K] with row stride lddh, fp32 (dh_bf16 = 0) or

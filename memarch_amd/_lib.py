@@ -29,6 +29,8 @@ SIGNATURES = {
     "mce_bwd_logits_grad": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P]),
     "mce_bwd_logits_grad_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _P, _P,
                                           _P, _S, _P]),
+    "mce_lse_fwd": (_INT, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P]),
+    "mce_bwd_lse_grad": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _S, _P]),
     "mce_bwd_dhidden": (_INT, [_P, _I, _I, _I, _I, _P, _INT, _I, _P, _S, _P]),
     "mce_bwd_dweight": (_INT, [_P, _I, _I, _I, _I, _P, _I, _P, _S, _P]),
     "mce_bwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P,

@@ -515,11 +515,14 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
       const float lse = M + logf(S);
       lse_rows[n] = lse;
       if (gate == nullptr) {
-        // plain cross-entropy: loss = lse - x_y; a target outside [0, V_real) (xy = -inf) is ignored
+        // plain cross-entropy: loss = lse - x_y; a target outside [0, V_real) (xy = -inf) is ignored.
+        // (loss_rows == nullptr: only lse is wanted.)
         const bool ok = xy[n] != -INFINITY;
         loss = ok ? lse - xy[n] : 0.f;
-        loss_rows[n] = loss;
-        wgt_rows[n] = ok ? 1.f : 0.f;
+        if (loss_rows != nullptr) {
+          loss_rows[n] = loss;
+          wgt_rows[n] = ok ? 1.f : 0.f;
+        }
         if (dgr_rows != nullptr) dgr_rows[n] = 0.f;
       } else {
         const float py = expf(xy[n] - lse);
@@ -536,7 +539,7 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
     rl[r] = loss;
   }
   __syncthreads();
-  if (t == 0) {
+  if (t == 0 && loss_part != nullptr) {
     float tot = 0.f;
     for (int i = 0; i < 32; ++i) tot += rl[i];
     loss_part[blockIdx.x] = tot;
@@ -590,14 +593,16 @@ __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Logits-grad tile: recompute S^T for the tile and form G = go*wgt*(exp(x - lse) - [v = y]) rounded to bf16,
-// written to both K-blocked layouts:
+// Logits-grad tile: recompute S^T for the tile and form G = go*(wgt*exp(x - lse) + c*[v = y]) rounded to bf16,
+// with c = ycoef[n] when given (the (lse, x_y) gradient of chunk_ce: wgt = g_lse, c = g_ly, go = 1 when null)
+// and c = -wgt otherwise (cross-entropy and the mixture: go*wgt*(softmax - onehot)), written to both K-blocked
+// layouts:
 //   G   element (n, v) at G[(v/256)*Np*256 + n*256 + v%256]    (for dH, reduction over v)
 //   Gt  element (v, n) at Gt[(n/256)*Vp*256 + v*256 + n%256]   (for dW, reduction over n)
 // Each tile is one contiguous 128 KiB block of either buffer. The tile is staged in LDS as [256 n][256 v]
 // (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))):
 //   1. every lane writes go*wgt*exp(x - lse) for its 256 logits (8-byte writes);
-//   2. one thread per row overwrites the target element with go*wgt*(exp(x_y - lse) - 1), from the row's
+//   2. one thread per row overwrites the target element with go*(wgt*exp(x_y - lse) + c), from the row's
 //      target logit (so the one-hot term is applied in fp32 before rounding, without searching registers),
 //      and, with a sparse bias, the row's candidate elements with their fix-up values (k_sparse_rows);
 //   3. G rows are copied out with ds_read_b128 (non-temporal stores: G is read back by another kernel, not
@@ -614,7 +619,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgp
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
                 const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ xy,
                 const int* __restrict__ fix_col, const float* __restrict__ fix_val, int nfix,
-                const float* __restrict__ go, int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal,
+                const float* __restrict__ ycoef, const float* __restrict__ go, int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal,
                 int tiles_v, int tiles_n, uint16_t* __restrict__ G, uint16_t* __restrict__ Gt,
                 float* __restrict__ dbias_part) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
@@ -625,7 +630,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   const int lr = lane & 31, lh = lane >> 5;
   // everything the epilogue needs from memory is loaded before the mainloop
   const float btile = tile_bias(bias, v0, V);
-  const float gscale = go[0];
+  const float gscale = go != nullptr ? go[0] : 1.f;
   float cn[4], lb[4];
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
@@ -637,7 +642,9 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   const int64_t nf = n0 + t;  // the row this thread fixes up in step 2
   const int64_t yf = nf < N ? y[nf] : -1;
   const bool fix = yf >= v0 && yf < v0 + BM && yf < Vreal;
-  const float fval = fix ? gscale * wgt_rows[nf] * (expf(xy[nf] - lse_rows[nf]) - 1.f) : 0.f;
+  const float fval =
+      fix ? gscale * (wgt_rows[nf] * expf(xy[nf] - lse_rows[nf]) + (ycoef != nullptr ? ycoef[nf] : -wgt_rows[nf]))
+          : 0.f;
 
   f32x16 acc[4][4];
   gemm_tile(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
@@ -993,6 +1000,26 @@ int check_sparse(const int64_t* cand, const float* cval, int kc) {
   return MCE_OK;
 }
 
+// The forward kernels: row logits (xy, and the candidate logits), tiles, merge. Outputs the merge does not
+// need to write may be null (loss_rows with wgt_rows, dgr_rows, loss_part).
+int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+               const int64_t* y, const float* gate, const float* hit, const int64_t* cand, const float* cval, int kc,
+               int64_t N, int64_t K, int64_t V, int64_t V_real, float* xy, float* loss_rows, float* lse_rows,
+               float* wgt_rows, float* dgr_rows, float* loss_part, hipStream_t st) {
+  int rc;
+  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
+  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
+  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
+                     kc, N, K, V_real, xy, w.xc);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
+                     w.part_m, w.part_s);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, cand, cval,
+                     w.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, loss_part);
+  return launch_status();
+}
+
 // Forward of every variant: gate and hit both given (mixture) or both null (plain cross-entropy); kc sparse
 // candidates per row (0: none).
 int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
@@ -1012,19 +1039,10 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
   if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
   const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
-  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
-                     kc, N, K, V_real, w.xy, w.xc);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
-                     w.part_m, w.part_s);
-  if ((rc = launch_status())) return rc;
-  const int nb = (int)cdiv(N, 32);
-  hipLaunchKernelGGL(k_fwd_merge, dim3(nb), dim3(256), 0, st, w.part_m, w.part_s, w.xy, cand, cval, w.xc, kc, V_real,
-                     gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, w.loss_part);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)nb, loss_sum);
+  if ((rc = fwd_launch(w, H, ldh, W, ldw, bias, y, gate, hit, cand, cval, kc, N, K, V, V_real, w.xy, loss_rows,
+                       lse_rows, wgt_rows, dgr_rows, w.loss_part, st)))
+    return rc;
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)cdiv(N, 32), loss_sum);
   return launch_status();
 }
 
@@ -1032,14 +1050,14 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
 // (sparse bias) when requested.
 int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
               const int64_t* cand, const float* cval, int kc, const float* lse_rows, const float* wgt_rows,
-              const float* dgr_rows, const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
-              float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
+              const float* dgr_rows, const float* ycoef, const float* go, int64_t N, int64_t K, int64_t V,
+              int64_t V_real, float* dBias, float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (!rc) rc = check_bias(bias);
   if (!rc) rc = check_sparse(cand, cval, kc);
   if (rc) return rc;
   if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
-  if (go == nullptr) return MCE_EINVAL;
+  if (go == nullptr && ycoef == nullptr) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
     if (dBias) (void)hipMemsetAsync(dBias, 0, sizeof(float) * V, st);
@@ -1059,7 +1077,7 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
     if ((rc = launch_status())) return rc;
   }
   hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, w.xy,
-                     w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                     w.fix_col, w.fix_val, kc, ycoef, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
                      dBias ? w.dbias_part : nullptr);
   if ((rc = launch_status())) return rc;
   if (dBias) {
@@ -1124,8 +1142,8 @@ int mce_bwd_logits_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64
                         const int64_t* y, const float* lse_rows, const float* wgt_rows, const float* dgr_rows,
                         const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real, float* dBias,
                         float* dGate, void* ws, size_t ws_bytes, void* stream) {
-  return grad_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, 0, lse_rows, wgt_rows, dgr_rows, go, N, K, V, V_real,
-                   dBias, dGate, nullptr, ws, ws_bytes, stream);
+  return grad_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, 0, lse_rows, wgt_rows, dgr_rows, nullptr, go, N, K, V,
+                   V_real, dBias, dGate, nullptr, ws, ws_bytes, stream);
 }
 
 int mce_bwd_logits_grad_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
@@ -1133,8 +1151,30 @@ int mce_bwd_logits_grad_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W
                                const float* lse_rows, const float* wgt_rows, const float* go, int64_t N, int64_t K,
                                int64_t V, int64_t V_real, float* dBias, float* dCval, void* ws, size_t ws_bytes,
                                void* stream) {
-  return grad_impl(H, ldh, W, ldw, bias, y, cand, cval, kc, lse_rows, wgt_rows, nullptr, go, N, K, V, V_real, dBias,
-                   nullptr, dCval, ws, ws_bytes, stream);
+  return grad_impl(H, ldh, W, ldw, bias, y, cand, cval, kc, lse_rows, wgt_rows, nullptr, nullptr, go, N, K, V, V_real,
+                   dBias, nullptr, dCval, ws, ws_bytes, stream);
+}
+
+int mce_lse_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
+                int64_t N, int64_t K, int64_t V, int64_t V_real, float* lse_rows, float* ly_rows, void* ws,
+                size_t ws_bytes, void* stream) {
+  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
+  if (rc) return rc;
+  if (N == 0) return MCE_OK;
+  if (!y || !lse_rows || !ly_rows || !ws) return MCE_EINVAL;
+  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  return fwd_launch(w, H, ldh, W, ldw, bias, y, nullptr, nullptr, nullptr, nullptr, 0, N, K, V, V_real, ly_rows,
+                    nullptr, lse_rows, nullptr, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mce_bwd_lse_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                     const int64_t* y, const float* lse_rows, const float* g_lse, const float* g_ly, int64_t N,
+                     int64_t K, int64_t V, int64_t V_real, float* dBias, void* ws, size_t ws_bytes, void* stream) {
+  if (N > 0 && (g_lse == nullptr || g_ly == nullptr)) return MCE_EINVAL;
+  return grad_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, 0, lse_rows, g_lse, nullptr, g_ly, nullptr, N, K, V,
+                   V_real, dBias, nullptr, nullptr, ws, ws_bytes, stream);
 }
 
 int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16,

@@ -19,6 +19,9 @@ Two independent restatements of the reference's eager formula (full2.py:1917-192
   ignored); dcval[n, j] = G[n, cand[n, j]].
 * `eager_ce_part`: the eager formula written with torch ops exactly as `_ce_part` composes them; torch
   autograd supplies its gradients, independently of the closed form above.
+* `lse_backward`: the (lse, x_y) gradient of `_ChunkCE` (full2.py:813-829): G = g_lse softmax + g_ly onehot,
+  dH = G W, dW = G^T H, dBias = sum_n G; its forward values are `forward`'s lse and xy.
+* `eager_chunk_ce`: `_ChunkCE`'s forward as plain torch ops (logsumexp and gather), for autograd.
 * `eager_ce_sparse`: the sparse-bias eager form (scatter_add on fp32 logits, full2.py:1920-1923) in torch.
 
 Pinning (tests/test_oracle.py): closed form vs torch autograd in fp64; central finite differences on tiny
@@ -152,6 +155,41 @@ def eager_ce_part(hn, W, bias, y, c1, g):
     ly = lo.gather(-1, y[..., None])[..., 0]
     py = (ly - lse).exp()
     return -torch.log(((1 - g) * py + g * (c1 == y).to(py.dtype)).clamp(min=1e-30)).sum()
+
+
+def lse_backward(h, w, y, g_lse, g_ly, bias=None, v_real=None, fwd=None, dtype=np.float64, chunk=1024):
+    """Gradients (dh, dw, dbias) of sum_n g_lse[n] lse_n + g_ly[n] x_{n, y_n} (full2.py:813-829)."""
+    if fwd is None:
+        fwd = forward(h, w, y, None, None, bias, v_real, dtype, chunk)
+    N, K = h.shape
+    V = w.shape[0]
+    vr = V if v_real is None else v_real
+    wt = w.astype(dtype)
+    dh = np.empty((N, K), dtype)
+    dw = np.zeros((V, K), dtype)
+    db = np.zeros(V, dtype)
+    for i in range(0, N, chunk):
+        hc = h[i:i + chunk].astype(dtype)
+        x = _logits(hc, w, bias, v_real, dtype)
+        G = np.exp(x - fwd["lse"][i:i + chunk, None]) * g_lse[i:i + chunk, None]
+        yc = y[i:i + chunk]
+        ok = (yc >= 0) & (yc < vr)
+        G[np.arange(len(yc))[ok], yc[ok]] += g_ly[i:i + chunk][ok]
+        db += G.sum(axis=0)
+        dh[i:i + chunk] = G @ wt
+        dw += G.T @ hc
+    return dict(dh=dh, dw=dw, dbias=db)
+
+
+def eager_chunk_ce(h, W, b, y):
+    """`_ChunkCE.forward` (full2.py:758-790) without the vocabulary chunking: lse = logsumexp(h W^T + b),
+    ly = h . W_y + b_y, in the promoted float type."""
+    import torch
+    lo = h @ W.T
+    lo = lo.to(torch.promote_types(lo.dtype, torch.float32))
+    if b is not None:
+        lo = lo + b.to(lo.dtype)
+    return torch.logsumexp(lo, -1), lo.gather(-1, y[:, None])[:, 0]
 
 
 def eager_ce_sparse(hn, W, bias, y, cand, val):

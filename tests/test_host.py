@@ -65,3 +65,13 @@ def test_sparse_validation_before_any_launch():
     with pytest.raises(ValueError, match="GPU only"):
         fused_ops.linear_ce_sparse(torch.randn(4, 8), torch.randn(16, 8), torch.zeros(4, dtype=torch.long),
                                    torch.zeros(4, 2, dtype=torch.long), torch.zeros(4, 2))
+
+
+def test_reference_signature_chunk_ce():
+    # full2.py:758 forward(ctx, h, W, b, y, ch); :792 backward(ctx, g_lse, g_ly); :834 chunk_ce(h, W, b, y, ch)
+    from memarch_amd import chunk_ce
+    assert list(inspect.signature(chunk_ce._ChunkCE.forward).parameters) == ["ctx", "h", "W", "b", "y", "ch"]
+    assert list(inspect.signature(chunk_ce._ChunkCE.backward).parameters) == ["ctx", "g_lse", "g_ly"]
+    assert list(inspect.signature(chunk_ce.chunk_ce).parameters) == ["h", "W", "b", "y", "ch"]
+    with pytest.raises(ValueError, match="GPU only"):
+        chunk_ce.chunk_ce(torch.randn(4, 8), torch.randn(16, 8), None, torch.zeros(4, dtype=torch.long))
