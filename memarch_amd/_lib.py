@@ -17,7 +17,7 @@ _I = ctypes.c_int64
 _S = ctypes.c_size_t
 _INT = ctypes.c_int
 
-# name -> (restype, argtypes); kept in the order of include/mce.h
+# name -> (restype, argtypes); kept in the order of include/mce.h, then include/mce_induct.h
 SIGNATURES = {
     "mce_version": (_INT, []),
     "mce_error_string": (ctypes.c_char_p, [_INT]),
@@ -35,6 +35,9 @@ SIGNATURES = {
     "mce_bwd_dweight": (_INT, [_P, _I, _I, _I, _I, _P, _I, _P, _S, _P]),
     "mce_bwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P,
                        _S, _P]),
+    # include/mce_induct.h
+    "mce_induct": (_INT, [_P, _I, _I, _INT, _INT, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "mce_induct_max_len": (_INT, []),
 }
 
 _lib = None

@@ -9,7 +9,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "mce.hip")
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("mce.hip", "induct.hip")]
 LIB = os.path.join(HERE, "libmce.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -25,7 +25,7 @@ FLAGS = [
 def build(verbose=False):
     """Compile libmce.so from source every time it is called; raises CalledProcessError on failure."""
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, SRC, "-o", tmp]
+    cmd = [HIPCC, *FLAGS, *SRCS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

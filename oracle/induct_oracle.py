@@ -14,33 +14,38 @@ import numpy as np
 
 def _keys(x, V, locks):
     B, T = x.shape
-    prev = np.concatenate([np.full((B, 1), V, np.int64), x[:, :-1]], 1)
-    prev2 = np.concatenate([np.full((B, 2), V, np.int64), x[:, :-2]], 1)
+    prev = np.concatenate([np.full((B, 1), V, np.int64), x[:, :-1]], 1)[:, :T]
+    prev2 = np.concatenate([np.full((B, 2), V, np.int64), x[:, :-2]], 1)[:, :T]
     ks = [x, prev * (V + 1) + x, (prev2 * (V + 1) + prev) * (V + 1) + x]
     return ks[:locks]
 
 
-def brute_force(x, V, locks=3):
+def brute_force(x, V, locks=3, longest=True, want_src=False):
+    """(cand, on[, src]) by a backward scan per position. `longest` keeps only the longest firing lock on (the
+    INDUCT=lock model, full2.py:1528-1530); without it every firing lock is on (INDUCT=1)."""
     x = np.asarray(x, np.int64)
     B, T = x.shape
     keys = _keys(x, V, locks)
     cand = np.zeros((B, T, locks), np.int64)
+    src = np.zeros((B, T, locks), np.int64)
     on = np.zeros((B, T, locks), bool)
     for k, key in enumerate(keys):
         for b in range(B):
             for t in range(T):
                 for j in range(t - 1, -1, -1):
                     if key[b, j] == key[b, t]:
-                        cand[b, t, k] = x[b, min(j + 1, T - 1)]
+                        src[b, t, k] = min(j + 1, T - 1)
+                        cand[b, t, k] = x[b, src[b, t, k]]
                         on[b, t, k] = True
                         break
-    for k in range(locks - 1):
-        on[..., k] &= ~on[..., k + 1:].any(-1)
-    cand = np.where(on, cand, cand)  # cand keeps the raw value of each lock; `on` selects
-    return cand, on
+    if longest:
+        for k in range(locks - 1):
+            on[..., k] &= ~on[..., k + 1:].any(-1)
+    # cand and src keep each firing lock's value (0 where it does not fire); `on` selects
+    return (cand, on, src) if want_src else (cand, on)
 
 
-def sorted_scan(x, V, locks=3):
+def sorted_scan(x, V, locks=3, longest=True):
     x = np.asarray(x, np.int64)
     B, T = x.shape
     rows = np.arange(B)[:, None]
@@ -56,9 +61,16 @@ def sorted_scan(x, V, locks=3):
         src = np.minimum(last + 1, T - 1)
         cands.append(np.where(ok, np.take_along_axis(x, src, 1), 0))
         ons.append(ok)
-    for k in range(locks - 1):
-        ons[k] = ons[k] & ~np.stack(ons[k + 1:], 0).any(0)
+    if longest:
+        for k in range(locks - 1):
+            ons[k] = ons[k] & ~np.stack(ons[k + 1:], 0).any(0)
     return np.stack(cands, -1), np.stack(ons, -1)
+
+
+def buckets(x, bucket):
+    """The rarity bucket per position, bucket[min(x, len(bucket) - 1)] (full2.py:1513)."""
+    bucket = np.asarray(bucket, np.int64)
+    return bucket[np.clip(np.asarray(x, np.int64), 0, len(bucket) - 1)]
 
 
 def c1_of(cand, on, none=0):

@@ -9,12 +9,12 @@ import pytest
 from memarch_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "mce.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("mce.h", "mce_induct.h")]
 
 
 def _declared():
-    src = open(HEADER).read()
-    return re.findall(r"MCE_API\s+[\w\s\*]+?\b(mce_\w+)\s*\(", src)
+    src = "".join(open(h).read() for h in HEADERS)
+    return re.findall(r"MCE(?:_INDUCT)?_API\s+[\w\s\*]+?\b(mce_\w+)\s*\(", src)
 
 
 @pytest.fixture(scope="module")
@@ -82,3 +82,15 @@ def test_sparse_and_plain_argument_checks(lib):
     a = list(g(2))
     a[16] = p                                                    # dBias without a bias
     assert lib.mce_bwd_logits_grad_sparse(*a) == 1
+
+
+def test_induct_argument_checks(lib):
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf)
+    assert lib.mce_induct_max_len() == 8192
+    assert lib.mce_induct(p, 2, 16, 4, 1, None, 0, 0, p, p, p, p, p, None) == 1      # locks > 3
+    assert lib.mce_induct(p, 2, 16, 0, 1, None, 0, 0, p, p, p, p, p, None) == 1      # locks < 1
+    assert lib.mce_induct(p, 2, 8193, 3, 1, None, 0, 0, p, p, p, p, p, None) == 1    # T above the limit
+    assert lib.mce_induct(p, 2, 16, 3, 1, p, 0, 0, p, p, p, p, p, None) == 1         # empty bucket table
+    assert lib.mce_induct(None, 0, 16, 3, 1, None, 0, 0, None, None, None, None, None, None) == 0   # no texts
+    assert lib.mce_induct(None, 2, 16, 3, 1, None, 0, 0, p, p, p, p, p, None) == 1   # null x

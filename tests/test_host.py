@@ -75,3 +75,13 @@ def test_reference_signature_chunk_ce():
     assert list(inspect.signature(chunk_ce.chunk_ce).parameters) == ["h", "W", "b", "y", "ch"]
     with pytest.raises(ValueError, match="GPU only"):
         chunk_ce.chunk_ce(torch.randn(4, 8), torch.randn(16, 8), None, torch.zeros(4, dtype=torch.long))
+
+
+def test_induct_host_checks():
+    from memarch_amd import induct
+    with pytest.raises(ValueError, match="GPU only"):
+        induct.induct_raw(torch.zeros(2, 8, dtype=torch.long))
+    with pytest.raises(ValueError, match="at most 8192"):
+        induct.induct_raw(torch.zeros(1, 8193, dtype=torch.long, device="meta"))
+    with pytest.raises(ValueError, match="locks"):
+        induct.pointer_candidate(torch.zeros(1, 8, dtype=torch.long, device="meta"), locks=4)

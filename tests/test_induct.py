@@ -42,3 +42,33 @@ def test_longest_lock_wins_and_causal():
     # causality: a candidate index never exceeds t
     c1 = wl.pointer_candidates(x, 2)
     assert c1[0, 0] == -1 and c1[0, 1] == -1
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_all_locks_on_mode_and_src(seed):
+    """INDUCT=1 (two locks, every firing lock on, full2.py:1531-1532) and the src output (want_src)."""
+    x, V = _texts(seed)
+    cb, ob, sb = io.brute_force(x, V, 2, longest=False, want_src=True)
+    cs, os_ = io.sorted_scan(x, V, 2, longest=False)
+    np.testing.assert_array_equal(ob, os_)
+    np.testing.assert_array_equal(cb, cs)
+    t = np.arange(x.shape[1])[None, :, None]
+    assert np.all(sb <= t)                                            # causal
+    np.testing.assert_array_equal(np.take_along_axis(x[..., None].repeat(2, -1), sb, 1)[ob], cb[ob])
+    assert (ob[..., 0] & ob[..., 1]).any()                            # both locks on somewhere
+    assert np.all(cb[~ob] == 0) and np.all(sb[~ob] == 0)              # without longest-wins, on = fired
+
+
+def test_buckets_clamp():
+    np.testing.assert_array_equal(io.buckets(np.array([[0, 3, 9, 100]]), [5, 6, 7, 8]), [[5, 8, 8, 8]])
+
+
+@pytest.mark.parametrize("T", [1, 2, 3])
+def test_tiny_texts(T):
+    x = np.array([[4, 4, 4][:T], [1, 2, 1][:T]])
+    cb, ob = io.brute_force(x, 5, 3)
+    cs, os_ = io.sorted_scan(x, 5, 3)
+    np.testing.assert_array_equal(ob, os_)
+    assert not ob[:, 0].any()                                         # nothing precedes t = 0
+    if T == 3:
+        assert ob[0, 2, 1] and cb[0, 2, 1] == 4 and ob[1, 2, 0] and cb[1, 2, 0] == 2
