@@ -15,6 +15,11 @@ accumulation), with every input resident in HBM before the timed region. Prints 
 
 `--calibrate-copy` instead times a plain 1 GiB device-to-device copy (the reference kernel for scaling the
 FETCH_SIZE / WRITE_SIZE counters) and prints its size.
+
+`--op swiglu` instead measures the SwiGLU gate kernels (memarch fused_ops.py:175-228) on the FFN of the same
+d = 2048 model (rows = N = 32768, H = 4d = 8192, bf16, lm.py:45-50): one line with the forward + backward HBM
+throughput against the 8 TB/s roofline (algorithmic bytes: forward reads gu and writes out, 3 rows x H
+elements; backward reads gu and go and writes d gu, 5 rows x H elements).
 """
 import argparse
 import json
@@ -47,6 +52,8 @@ def _args():
     ap.add_argument("--cpu-rows", type=int, default=16384, help="rows of the CPU baseline sample (0: skip)")
     ap.add_argument("--stage-reps", type=int, default=5, help="timed repetitions of each kernel stage")
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
+    ap.add_argument("--op", choices=("fused_ce", "swiglu"), default="fused_ce",
+                    help="fused_ce: the north-star operator (default); swiglu: the SwiGLU gate kernels")
     return ap.parse_args()
 
 
@@ -149,14 +156,76 @@ def calibrate_copy():
                       "launches": 5}), flush=True)
 
 
+def bench_swiglu(args):
+    """Forward and backward of the SwiGLU gate at rows = 32768, H = 8192, bf16; each kernel timed with torch events
+    on the current stream (the stream the C-ABI calls launch on)."""
+    from memarch_amd import _lib
+    dev = torch.device("cuda", 0)
+    rows, H = 32768, 8192
+    gen = torch.Generator().manual_seed(2024)
+    gu = (torch.randn(rows, 2 * H, generator=gen) * 2).bfloat16().to(dev)
+    go = torch.randn(rows, H, generator=gen).bfloat16().to(dev)
+    out = torch.empty(rows, H, dtype=torch.bfloat16, device=dev)
+    dgu = torch.empty_like(gu)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    fwd = lambda: _lib.call("mce_swiglu_fwd", gu.data_ptr(), rows, H, 1, out.data_ptr(), st)
+    bwd = lambda: _lib.call("mce_swiglu_bwd", gu.data_ptr(), go.data_ptr(), 1, rows, H, 1, dgu.data_ptr(), st)
+    times = {}
+    for name, fn in (("fwd", fwd), ("bwd", bwd)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        times[name] = e0.elapsed_time(e1) / args.steps * 1e-3
+    # a plain device copy of 1 GiB on the same stream: the practical HBM ceiling of a streaming kernel
+    src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_bw = 2 * (1 << 30) / (e0.elapsed_time(e1) / args.steps * 1e-3)
+    del src, dst
+    nbytes = {"fwd": 3 * rows * H * 2, "bwd": 5 * rows * H * 2}
+    dt = times["fwd"] + times["bwd"]
+    bw = {k: nbytes[k] / times[k] for k in times}
+    dom = max(times, key=times.get)
+    res = {
+        "metric": "GB/s swiglu fwd+bwd (HBM)", "value": round((nbytes["fwd"] + nbytes["bwd"]) / dt / 1e9, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded normal gu, go)",
+        "config": {"workload": "swiglu fwd+bwd, FFN of d=2048 (H=4d)", "rows": rows, "H": H},
+        "roofline": {"bound": "hbm", "kernel": f"k_swiglu_{dom}", "achieved": round(bw[dom] / 1e9, 1),
+                     "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(bw[dom] / PEAK_HBM, 4),
+                     "bytes_per_launch": nbytes[dom], "traffic": None},
+        "kernels_ms": {k: round(v * 1e3, 4) for k, v in times.items()},
+        "kernels_GBps": {k: round(v / 1e9, 1) for k, v in bw.items()},
+        "device_copy_GBps": round(copy_bw / 1e9, 1),
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = _args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the fused op is single-GPU in this build, so --gpus {args.gpus} "
-              "is refused (the sharded design is described in DESIGN.md)", file=sys.stderr)
+              "is refused (the op would shard over rows, each GPU running it on its N/G rows)", file=sys.stderr)
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.op == "swiglu":
+        bench_swiglu(args)
         return
     from memarch_amd import fused_ops
     from memarch_amd.workloads import CONFIGS, make_inputs

@@ -17,7 +17,7 @@ _I = ctypes.c_int64
 _S = ctypes.c_size_t
 _INT = ctypes.c_int
 
-# name -> (restype, argtypes); kept in the order of include/mce.h, then include/mce_induct.h
+# name -> (restype, argtypes); kept in the order of include/mce.h, include/mce_induct.h, include/mce_swiglu.h
 SIGNATURES = {
     "mce_version": (_INT, []),
     "mce_error_string": (ctypes.c_char_p, [_INT]),
@@ -38,6 +38,10 @@ SIGNATURES = {
     # include/mce_induct.h
     "mce_induct": (_INT, [_P, _I, _I, _INT, _INT, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "mce_induct_max_len": (_INT, []),
+    # include/mce_swiglu.h
+    "mce_swiglu_fwd": (_INT, [_P, _I, _I, _INT, _P, _P]),
+    "mce_swiglu_bwd": (_INT, [_P, _P, _INT, _I, _I, _INT, _P, _P]),
+    "mce_swiglu_last_hip_error": (_INT, []),
 }
 
 _lib = None

@@ -9,7 +9,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRCS = [os.path.join(HERE, "csrc", f) for f in ("mce.hip", "induct.hip")]
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("mce.hip", "induct.hip", "swiglu.hip")]
 LIB = os.path.join(HERE, "libmce.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -9,12 +9,12 @@ import pytest
 from memarch_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("mce.h", "mce_induct.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("mce.h", "mce_induct.h", "mce_swiglu.h")]
 
 
 def _declared():
     src = "".join(open(h).read() for h in HEADERS)
-    return re.findall(r"MCE(?:_INDUCT)?_API\s+[\w\s\*]+?\b(mce_\w+)\s*\(", src)
+    return re.findall(r"MCE(?:_INDUCT|_SWIGLU)?_API\s+[\w\s\*]+?\b(mce_\w+)\s*\(", src)
 
 
 @pytest.fixture(scope="module")

@@ -85,3 +85,28 @@ def test_induct_host_checks():
         induct.induct_raw(torch.zeros(1, 8193, dtype=torch.long, device="meta"))
     with pytest.raises(ValueError, match="locks"):
         induct.pointer_candidate(torch.zeros(1, 8, dtype=torch.long, device="meta"), locks=4)
+
+
+def test_swiglu_surface_and_no_cpu_fallback():
+    from memarch_amd import swiglu as sw
+    # fused_ops.py:200-228: _SwiGLU.forward(ctx, gu), backward(ctx, go), swiglu(gu)
+    assert list(inspect.signature(sw._SwiGLU.forward).parameters) == ["ctx", "gu"]
+    assert list(inspect.signature(sw._SwiGLU.backward).parameters) == ["ctx", "go"]
+    assert list(inspect.signature(sw.swiglu).parameters) == ["gu"]
+    with pytest.raises(ValueError, match="GPU only"):
+        sw.swiglu(torch.randn(3, 8))
+
+
+def test_swiglu_c_abi_argument_checks_need_no_gpu():
+    import ctypes
+    from memarch_amd import _lib
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.addressof(buf)
+    assert lib.mce_swiglu_fwd(p, 4, 8, 3, p, None) == 1          # unknown element type
+    assert lib.mce_swiglu_fwd(p, -1, 8, 1, p, None) == 1         # negative rows
+    assert lib.mce_swiglu_fwd(None, 4, 8, 1, p, None) == 1       # null input
+    assert lib.mce_swiglu_fwd(None, 0, 8, 1, None, None) == 0    # nothing to do
+    assert lib.mce_swiglu_bwd(p, p, 7, 4, 8, 1, p, None) == 1    # unknown upstream type
+    assert lib.mce_swiglu_bwd(p, None, 1, 4, 8, 1, p, None) == 1
+    assert lib.mce_swiglu_bwd(None, None, 1, 4, 0, 1, None, None) == 0
