@@ -121,73 +121,125 @@ using I = Img<BK>;
 // Per-tile state of one operand stream. Stage s of this wave's I::LPW load instructions (instruction
 // i = wave*LPW + j of the stage covers 1 KiB of the LDS image) reads base + offset(s) + voff[j], or zeros
 // when the chunk's local k index kloc[j] is past the valid extent (kloc is OOB for rows outside the operand).
+// vfull[j] is the offset for a stage whose 64 k-values are all inside the operand (OOB for rows outside it),
+// so operands whose K extent is a multiple of 64 need no per-load check in the mainloop.
 struct Stream {
   uint64_t base;   // bytes: element (m0, 0)
-  int64_t blk;     // element distance between K blocks, or 0
+  int64_t blk;     // element distance between 256-wide K blocks (256 for a row-major operand)
   int64_t kext;
   int voff[I::LPW];
   int kloc[I::LPW];
+  int vfull[I::LPW];
 };
 
 __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
   Stream st;
   st.kext = op.kext;
-  st.blk = op.blk;
+  st.blk = op.blk ? op.blk : BLK;  // row-major: K block b starts 256*b elements into the row
   st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
   const int rsub = lane / I::CH, pc = lane % I::CH;
 #pragma unroll
   for (int j = 0; j < I::LPW; ++j) {
     const int row = (wave * I::LPW + j) * I::RPI + rsub;
     const int c = pc ^ I::swz(row);
+    const bool in = m0 + row < op.mext;
     st.voff[j] = (int)(row * op.ld * 2) + c * 16;
-    st.kloc[j] = (m0 + row < op.mext) ? c * 8 : OOB;
+    st.kloc[j] = in ? c * 8 : OOB;
+    st.vfull[j] = in ? st.voff[j] : OOB;
   }
   return st;
 }
 
-// Resource and K limit of one stage of a stream.
+// Resource and K limit of one stage of a stream. A stage past the range gets a resource with no records, so
+// every lane reads zeros without touching memory.
 struct StageSrc {
   i32x4 rsrc;
   int klim;
 };
 __device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage, int send) {
   const int64_t k0 = (int64_t)stage * BK;
-  const int64_t klim64 = stage < send ? st.kext - k0 : 0;  // stages past the range read nothing
-  const uint64_t off = st.blk ? (uint64_t)((k0 >> 8) * st.blk + (k0 & (BLK - 1))) * 2 : (uint64_t)k0 * 2;
-  return StageSrc{make_rsrc(st.base + off), klim64 < 0 ? 0 : (klim64 > BK ? BK : (int)klim64)};
+  const int64_t klim64 = stage < send ? st.kext - k0 : 0;
+  const uint64_t off = (uint64_t)((k0 >> 8) * st.blk + (k0 & (BLK - 1))) * 2;
+  StageSrc g{make_rsrc(st.base + off), klim64 < 0 ? 0 : (klim64 > BK ? BK : (int)klim64)};
+  if (stage >= send) g.rsrc[2] = 0;
+  return g;
 }
 
-// Load j of this wave for one stage into the operand image at `s`.
-__device__ __forceinline__ void issue_one(const Stream& st, const StageSrc& src, int j, char* s, int wave) {
-  const int vo = st.kloc[j] < src.klim ? st.voff[j] : OOB;
-  buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(s + (wave * I::LPW + j) * 1024), 16, vo, 0, 0, 0);
+// LDS of the mainloop: the A image of ring buffer b at b*OPB, the B image at 2*OPB + b*OPB (each image
+// [256][64] bf16 with 128-byte rows). Keeping the two A images 32 KiB apart lets a fragment read reach either
+// buffer through the 16-bit immediate offset of ds_read_b128.
+constexpr int AOFF = 0, BOFF = 2 * I::OPB;
+
+// Load j of this wave for one stage into the LDS byte offset `dst` (relative to the kernel's LDS base);
+// KF: the stage lies inside K (or past the range), so the precomputed offset needs no check.
+template <bool KF>
+__device__ __forceinline__ void issue_one(const Stream& st, const StageSrc& src, int j, char* lds, int dst) {
+  int vo;
+  if constexpr (KF) vo = st.vfull[j];
+  else vo = st.kloc[j] < src.klim ? st.voff[j] : OOB;
+  buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(lds + dst), 16, vo, 0, 0, 0);
 }
 
-// Issue this wave's loads of stage `stage` into the operand image at `s`.
-__device__ __forceinline__ void issue_stage(const Stream& st, int stage, int send, char* s, int wave) {
+// This wave's loads of one operand of stage `stage` into the image at LDS byte offset `img`.
+__device__ __forceinline__ void issue_stage(const Stream& st, int stage, int send, char* lds, int img, int wave) {
   const StageSrc src = stage_src(st, stage, send);
 #pragma unroll
-  for (int j = 0; j < I::LPW; ++j) issue_one(st, src, j, s, wave);
+  for (int j = 0; j < I::LPW; ++j) issue_one<false>(st, src, j, lds, img + (wave * I::LPW + j) * 1024);
 }
 
-// MFMA operand fragment of v_mfma_f32_32x32x16_bf16 for the 32 rows mbase..mbase+31 of the LDS operand image
-// and the K slice kk*16..kk*16+15: lane l holds element (mbase + l%32, kk*16 + 8*(l/32) + 0..7).
-__device__ __forceinline__ bf16x8 read_frag(const char* s, int mbase, int kk, int lane) {
-  const int row = mbase + (lane & 31);
-  const int c = kk * 2 + (lane >> 5);
-  return __builtin_bit_cast(bf16x8,
-                            *reinterpret_cast<const u32x4*>(s + row * I::ROWB + ((c ^ I::swz(row)) << 4)));
+// Per-lane LDS byte offsets of the MFMA operand fragments (v_mfma_f32_32x32x16_bf16: lane l holds element
+// (row0 + l%32, kk*16 + 8*(l/32) + 0..7) of a 32-row block), computed once per tile. Fragment i of slice kk is
+// at a[kk][i&1] + (i>>1)*64 rows: rows 64 apart share the XOR swizzle, so the rest is a compile-time offset,
+// as is the ring buffer (b*OPB). The mainloop then reads with immediates only.
+struct FragAddr {
+  uint32_t a[4][2];  // [kk][i & 1], A image of buffer 0
+  uint32_t b[4][2];  // [kk][j & 1], B image of buffer 0
+};
+__device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
+  FragAddr ad;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int c = kk * 2 + (lane >> 5);
+      const int ra = wm * 128 + p * 32 + (lane & 31);
+      const int rb = wn * 128 + p * 32 + (lane & 31);
+      ad.a[kk][p] = AOFF + ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
+      ad.b[kk][p] = BOFF + rb * I::ROWB + ((c ^ I::swz(rb)) << 4);
+    }
+  return ad;
 }
-
-// Fragment reads in the order the next slice's MFMAs consume them: (0,0) (0,1) (0,2) (0,3) (1,0) ... needs
-// a0 b0 b1 b2 b3 a1 a2 a3, so every read has most of a slice to complete.
-__device__ __forceinline__ void read_frags(const char* stage, int wm, int wn, int kk, int lane, bf16x8 (&a)[4],
-                                           bf16x8 (&b)[4]) {
-  a[0] = read_frag(stage, wm * 128, kk, lane);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) b[j] = read_frag(stage + I::OPB, wn * 128 + j * 32, kk, lane);
-#pragma unroll
-  for (int i = 1; i < 4; ++i) a[i] = read_frag(stage, wm * 128 + i * 32, kk, lane);
+template <int OFF>
+__device__ __forceinline__ bf16x8 frag_at(const char* lds, uint32_t addr) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + addr + OFF));
+}
+// A fragment I_ / B fragment J_ of slice KK in ring buffer BUF
+template <int BUF, int KK, int I_>
+__device__ __forceinline__ bf16x8 frag_a(const char* lds, const FragAddr& ad) {
+  return frag_at<BUF * I::OPB + (I_ >> 1) * 64 * I::ROWB>(lds, ad.a[KK][I_ & 1]);
+}
+template <int BUF, int KK, int J_>
+__device__ __forceinline__ bf16x8 frag_b(const char* lds, const FragAddr& ad) {
+  return frag_at<BUF * I::OPB + (J_ >> 1) * 64 * I::ROWB>(lds, ad.b[KK][J_ & 1]);
+}
+// Read r (0..7) of a slice, in the order the next slice's MFMAs consume them: a0 b0 b1 b2 b3 a1 a2 a3 (the
+// MFMAs run (0,0) (0,1) (0,2) (0,3) (1,0) ...), so every read has most of a slice to complete.
+template <int BUF, int KK, int R>
+__device__ __forceinline__ void frag_read(const char* lds, const FragAddr& ad, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+  if constexpr (R == 0) a[0] = frag_a<BUF, KK, 0>(lds, ad);
+  else if constexpr (R < 5) b[R - 1] = frag_b<BUF, KK, R - 1>(lds, ad);
+  else a[R - 4] = frag_a<BUF, KK, R - 4>(lds, ad);
+}
+template <int BUF, int KK>
+__device__ __forceinline__ void read_frags(const char* lds, const FragAddr& ad, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+  frag_read<BUF, KK, 0>(lds, ad, a, b);
+  frag_read<BUF, KK, 1>(lds, ad, a, b);
+  frag_read<BUF, KK, 2>(lds, ad, a, b);
+  frag_read<BUF, KK, 3>(lds, ad, a, b);
+  frag_read<BUF, KK, 4>(lds, ad, a, b);
+  frag_read<BUF, KK, 5>(lds, ad, a, b);
+  frag_read<BUF, KK, 6>(lds, ad, a, b);
+  frag_read<BUF, KK, 7>(lds, ad, a, b);
 }
 
 __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4], const bf16x8 (&b)[4]) {
@@ -206,51 +258,86 @@ __device__ __forceinline__ void sched_slice() {
   }
 }
 
-// One MFMA slice with its side work, in a fixed order (a scheduling barrier after every MFMA): the 16 MFMAs of
-// (ua, ub); the 8 fragment reads of K slice rk of the stage image `rs` into (da, db), one before every even MFMA,
-// in the order the next slice consumes them; and load instruction l0 + idx/2 of this wave's share of a stage
-// (A loads first, then B) after every odd MFMA.
-__device__ __forceinline__ void slice_with_loads(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
-                                                 const char* rs, int rk, bf16x8 (&da)[4], bf16x8 (&db)[4],
-                                                 const Stream& sa, const Stream& sb, const StageSrc& ga,
-                                                 const StageSrc& gb, int l0, char* ls, int wm, int wn, int lane,
-                                                 int wave) {
+// A slice without loads: reads of slice RK of buffer RBUF into (da, db), the 16 MFMAs of (ua, ub), interleaved by
+// the compiler one read per two MFMAs.
+template <int RBUF, int RK>
+__device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
+                                            const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4]) {
+  read_frags<RBUF, RK>(lds, ad, da, db);
+  mma16(acc, ua, ub);
+  sched_slice();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// A slice with loads, in a fixed order (a scheduling barrier after every MFMA): the 16 MFMAs of (ua, ub); the 8
+// fragment reads of slice RK of buffer RBUF into (da, db), one before every even MFMA; and this wave's 8 load
+// instructions of one operand of a stage into that operand's image of buffer LBUF, one after every odd MFMA.
+template <int RBUF, int RK, bool OPB_, int LBUF, bool KF>
+__device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
+                                            char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
+                                            const Stream& st, const StageSrc& g, int wave) {
+  constexpr int IMG = (OPB_ ? BOFF : AOFF) + LBUF * I::OPB;
 #pragma unroll
   for (int idx = 0; idx < 16; ++idx) {
     if ((idx & 1) == 0) {
-      const int r = idx >> 1;
-      if (r == 0) da[0] = read_frag(rs, wm * 128, rk, lane);
-      else if (r < 5) db[r - 1] = read_frag(rs + I::OPB, wn * 128 + (r - 1) * 32, rk, lane);
-      else da[r - 4] = read_frag(rs, wm * 128 + (r - 4) * 32, rk, lane);
+      if (idx == 0) frag_read<RBUF, RK, 0>(lds, ad, da, db);
+      else if (idx == 2) frag_read<RBUF, RK, 1>(lds, ad, da, db);
+      else if (idx == 4) frag_read<RBUF, RK, 2>(lds, ad, da, db);
+      else if (idx == 6) frag_read<RBUF, RK, 3>(lds, ad, da, db);
+      else if (idx == 8) frag_read<RBUF, RK, 4>(lds, ad, da, db);
+      else if (idx == 10) frag_read<RBUF, RK, 5>(lds, ad, da, db);
+      else if (idx == 12) frag_read<RBUF, RK, 6>(lds, ad, da, db);
+      else frag_read<RBUF, RK, 7>(lds, ad, da, db);
     }
     acc[idx >> 2][idx & 3] =
         __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua[idx >> 2], ub[idx & 3], acc[idx >> 2][idx & 3], 0, 0, 0);
     if (idx & 1) {
-      const int l = l0 + (idx >> 1);
-      if (l < I::LPW) issue_one(sa, ga, l, ls, wave);
-      else issue_one(sb, gb, l - I::LPW, ls + I::OPB, wave);
+      const int j = idx >> 1;
+      issue_one<KF>(st, g, j, lds, IMG + (wave * I::LPW + j) * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
+// One 64-wide K stage kt held in ring buffer CB (the other buffer, NB, holds stage kt+1):
+//   slice 0: MFMAs on slice 0 (already in registers), reads of slice 1, loads of stage kt+1's B operand into NB;
+//   slices 1, 2: MFMAs, reads of slices 2, 3;
+//   wait for this wave's loads of stage kt+1, barrier: every wave has read all of stage kt and stage kt+1 landed;
+//   slice 3: MFMAs on slice 3, reads of slice 0 of stage kt+1 (NB), loads of stage kt+2's A operand into CB.
+// A stage's loads are thus split in two halves, one load per two MFMAs, landing over three slices of MFMAs.
+template <int CB, bool KF>
+__device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4][4], bf16x8 (&fa)[2][4],
+                                           bf16x8 (&fb)[2][4], char* lds, const FragAddr& ad, const Stream& sa,
+                                           const Stream& sb, int wave) {
+  constexpr int NB = CB ^ 1;
+  {
+    const StageSrc gb = stage_src(sb, stage + 1, send);
+    slice_loads<CB, 1, true, NB, KF>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave);
+  }
+  slice_plain<CB, 2>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0]);
+  slice_plain<CB, 3>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1]);
+  wait_vmcnt<0>();
+  __syncthreads();
+  {
+    const StageSrc ga = stage_src(sa, stage + 2, send);
+    slice_loads<NB, 0, false, CB, KF>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
+  }
+}
+
 // C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over the K stages s0 .. s0+nk-1 (k in [s0*BK, (s0+nk)*BK),
-// clipped to each operand's extent), fp32 accumulation.
+// clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
 //                                              [wn*128 + nj*32 + lane%32].
-// Pipeline (two 64 KiB LDS stages, four 16-wide K slices per stage): the fragments of slice kk+1 are read while
-// slice kk is multiplied. The one barrier of a stage sits before its last slice: every wave has then read all
-// of stage kt (its last slice's fragments were read during slice 2) and has waited for its own loads of stage
-// kt+1. The loads of stage kt+2 go into stage kt's buffer in two halves, one load instruction per two MFMAs:
-// the A half during the last slice of stage kt, the B half during the first slice of stage kt+1, so they land
-// over three slices of MFMAs. Spreading them this way instead of issuing all 16 in one slice keeps the
-// address/texture queue from backing up into the MFMA issue stream (about 10% faster on the dH shape).
-// Loads past the last stage read nothing (all lanes out of range); the final wait + barrier lets the caller
-// reuse LDS as soon as this returns.
+// Two 64 KiB LDS stages, four 16-wide K slices per stage; the fragments of slice kk+1 are read while slice kk is
+// multiplied, and the one barrier of a stage sits before its last slice (gemm_stage). Splitting a stage's loads
+// over two slices keeps the address/texture queue from backing up into the MFMA issue stream, and the
+// loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
+// interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
+// The final wait + barrier lets the caller reuse LDS as soon as this returns.
+template <bool KF>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4]) {
-  constexpr int HALF = I::LPW;  // load instructions per wave per operand per stage (the A or B half)
-  static_assert(HALF == 8 && I::SLICES == 4, "slice_with_loads issues 8 loads over a 16-MFMA slice");
+  static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
   const int wm = wave >> 1, wn = wave & 1;
@@ -263,40 +350,23 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 
   const Stream sa = make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
+  const FragAddr ad = make_frag_addr(wm, wn, lane);
   const int send = s0 + nk;
-  // prologue: stage s0 in full, the A half of stage s0+1 (its B half goes out during the first slice)
-  issue_stage(sa, s0, send, lds, wave);
-  issue_stage(sb, s0, send, lds + I::OPB, wave);
-  issue_stage(sa, s0 + 1, send, lds + I::STB, wave);
-  wait_vmcnt<HALF>();
+  // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
+  issue_stage(sa, s0, send, lds, AOFF, wave);
+  issue_stage(sb, s0, send, lds, BOFF, wave);
+  issue_stage(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
+  wait_vmcnt<I::LPW>();
   __syncthreads();
 
   bf16x8 fa[2][4], fb[2][4];
-  read_frags(lds, wm, wn, 0, lane, fa[0], fb[0]);
-  for (int kt = 0; kt < nk; ++kt) {
-    char* cur = lds + (kt & 1) * I::STB;
-    char* nxt = lds + ((kt + 1) & 1) * I::STB;
-    // slice 0: the B half of stage kt+1 (into nxt, whose A half went out in the previous stage's last slice)
-    {
-      const StageSrc ga = stage_src(sa, s0 + kt + 1, send), gb = stage_src(sb, s0 + kt + 1, send);
-      slice_with_loads(acc, fa[0], fb[0], cur, 1, fa[1], fb[1], sa, sb, ga, gb, HALF, nxt, wm, wn, lane, wave);
-    }
-#pragma unroll
-    for (int kk = 1; kk + 1 < I::SLICES; ++kk) {
-      read_frags(cur, wm, wn, kk + 1, lane, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
-      mma16(acc, fa[kk & 1], fb[kk & 1]);
-      sched_slice();
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // stage kt is fully in registers; stage kt+1 must have landed before anyone reads it
-    wait_vmcnt<0>();
-    __syncthreads();
-    // last slice: the next stage's first fragments, and the A half of stage kt+2 into the freed buffer
-    {
-      const StageSrc ga = stage_src(sa, s0 + kt + 2, send), gb = stage_src(sb, s0 + kt + 2, send);
-      slice_with_loads(acc, fa[1], fb[1], nxt, 0, fa[0], fb[0], sa, sb, ga, gb, 0, cur, wm, wn, lane, wave);
-    }
+  read_frags<0, 0>(lds, ad, fa[0], fb[0]);
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    gemm_stage<0, KF>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave);
+    gemm_stage<1, KF>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave);
   }
+  if (kt < nk) gemm_stage<0, KF>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave);
   wait_vmcnt<0>();
   __syncthreads();
 }
@@ -364,7 +434,8 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t x) { return __uint_as_floa
 // ---------------------------------------------------------------------------------------------------------
 // Forward tile: S^T[v, n] for a 256(v) x 256(n) tile. Each wave reduces its own 128 vocabulary rows, so the
 // partials are per half-tile: part_m / part_s [2*tiles_v][N] hold the max and sum of exp of row block
-// 2*tm + wm for every column n. No LDS and no barrier after the mainloop.
+// 2*tm + wm for every column n. No LDS and no barrier after the mainloop. KF: K is a multiple of BK.
+template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64_t N, int64_t V, int64_t Vreal,
                  int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s) {
@@ -376,7 +447,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
   const int lr = lane & 31, lh = lane >> 5;
   const float btile = tile_bias(bias, v0, V);
   f32x16 acc[4][4];
-  gemm_tile(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
+  gemm_tile<KF>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
   float* bslot = reinterpret_cast<float*>(lds + LDS_BYTES);
   stash_bias(bslot, btile, v0, Vreal);
   __syncthreads();
@@ -632,6 +703,7 @@ __device__ __forceinline__ int gsw(int n) { return ((n & 3) << 1) | ((n >> 2) & 
 
 constexpr int GRAD_LDS_BYTES = LDS_BYTES + 4 * 32 * 8 * 4 + BM * 4;  // tile + [4][32][8] dBias sums + bias slot
 
+template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
                 const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ xy,
@@ -664,7 +736,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           : 0.f;
 
   f32x16 acc[4][4];
-  gemm_tile(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
+  gemm_tile<KF>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
   // sparse fix-ups of row nf (nfix > 0 only with a sparse bias; the loads overlap the staging below)
   int scol[MAX_KC];
   float sval[MAX_KC];
@@ -825,7 +897,7 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16>
+template <bool OUT_BF16, bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part) {
@@ -846,7 +918,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   tile_of(lin, tiles_m, tiles_n, group, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile(A, B, s0, nk, m0, n0, lds, acc);
+  gemm_tile<KF>(A, B, s0, nk, m0, n0, lds, acc);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   if (slot >= 0) {
@@ -993,8 +1065,12 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (R && P > TAIL_SLOTS / R) P = TAIL_SLOTS / R;
   const int full = (R && P >= 2) ? T - R : T;
   if (full == T) P = 1;
-  hipLaunchKernelGGL((k_gemm<OUT_BF16>), dim3(full + (T - full) * P), dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                     tiles_m, tiles_n, group, full, P, C, ldc, part);
+  if (A.kext % BK == 0 && B.kext % BK == 0)
+    hipLaunchKernelGGL((k_gemm<OUT_BF16, true>), dim3(full + (T - full) * P), dim3(NTHREADS), 0, st, A, B, nk, M,
+                       Nc, tiles_m, tiles_n, group, full, P, C, ldc, part);
+  else
+    hipLaunchKernelGGL((k_gemm<OUT_BF16, false>), dim3(full + (T - full) * P), dim3(NTHREADS), 0, st, A, B, nk, M,
+                       Nc, tiles_m, tiles_n, group, full, P, C, ldc, part);
   int rc = launch_status();
   if (rc || full == T) return rc;
   hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 16, T - full), dim3(BN), 0, st, part, P, full, tiles_m,
@@ -1029,8 +1105,12 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
                      kc, N, K, V_real, xy, w.xc);
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_fwd_tiles, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
-                     w.part_m, w.part_s);
+  if (K % BK == 0)
+    hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
+                       tn, w.part_m, w.part_s);
+  else
+    hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
+                       tn, w.part_m, w.part_s);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, cand, cval,
                      w.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, loss_part);
@@ -1093,9 +1173,14 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
                        lse_rows, wgt_rows, go, N, V_real, w.fix_col, w.fix_val, dCval);
     if ((rc = launch_status())) return rc;
   }
-  hipLaunchKernelGGL(k_bwd_grad, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows, w.xy,
-                     w.fix_col, w.fix_val, kc, ycoef, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
-                     dBias ? w.dbias_part : nullptr);
+  if (K % BK == 0)
+    hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows,
+                       w.xy, w.fix_col, w.fix_val, kc, ycoef, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                       dBias ? w.dbias_part : nullptr);
+  else
+    hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows,
+                       w.xy, w.fix_col, w.fix_val, kc, ycoef, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                       dBias ? w.dbias_part : nullptr);
   if ((rc = launch_status())) return rc;
   if (dBias) {
     hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
@@ -1207,9 +1292,9 @@ int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_
   hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
                      ldw, V, K, w.Wt);
   if ((rc = launch_status())) return rc;
-  // dH[n, k] = sum_v G(n, v) Wt(k, v); G's columns V..Vp-1 are zero
+  // dH[n, k] = sum_v G(n, v) Wt(k, v); G's and Wt's columns V..Vp-1 are zero
   const Operand Aop{w.G, BLK, N, w.vp, w.np * BLK};
-  const Operand Bop{w.Wt, BLK, K, V, K * BLK};
+  const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
   const int nk = (int)(w.vp / BK);
   return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st)
                  : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st);
