@@ -39,8 +39,8 @@ METRIC = "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA pea
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 
 # C-ABI stage -> the kernel that dominates it (the stage also runs small helpers: see stage_times)
-STAGE_KERNEL = {"fwd": "k_fwd_tiles", "logits_grad": "k_bwd_grad", "dhidden": "k_gemm<true>",
-                "dweight": "k_gemm<false>"}
+STAGE_KERNEL = {"fwd": "k_fwd_tiles<true>", "logits_grad": "k_bwd_grad<true>", "dhidden": "k_gemm<true, true>",
+                "dweight": "k_gemm<false, true>"}
 
 
 def _args():
@@ -106,14 +106,15 @@ def stage_times(inp, reps):
 
 def traffic_bytes(kernel, cfg_index):
     """HBM bytes per launch of `kernel` at config `cfg_index` from the committed rocprofv3 summary (a line
-    `traffic <kernel> cfg<k> <bytes>`), or None."""
+    `traffic <kernel> cfg<k> <bytes>`, kernel names written without spaces), or None."""
     if not os.path.exists(TRAFFIC_SUMMARY):
         return None
     pat = re.compile(r"^traffic\s+(\S+)\s+cfg(\d+)\s+([0-9.eE+]+)\s*$")
+    want = kernel.replace(" ", "")
     with open(TRAFFIC_SUMMARY) as f:
         for line in f:
             m = pat.match(line.strip())
-            if m and m.group(1) == kernel and int(m.group(2)) == cfg_index:
+            if m and m.group(1) == want and int(m.group(2)) == cfg_index:
                 return float(m.group(3))
     return None
 
