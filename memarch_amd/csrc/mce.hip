@@ -69,6 +69,7 @@ struct Operand {
   int64_t mext;       // valid extent along M
   int64_t kext;       // valid extent along K
   int64_t blk;        // 0, or the element distance between consecutive 256-wide K blocks
+  int chunked;        // 1: K-blocked and, within a block, [M/16][32-wide K chunk][16 m][32 k] (1 KiB pieces)
 };
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone). gfx9 encoding: vmcnt[3:0] and vmcnt[5:4] at bits 15:14.
@@ -127,6 +128,7 @@ struct Stream {
   uint64_t base;   // bytes: element (m0, 0)
   int64_t blk;     // element distance between 256-wide K blocks (256 for a row-major operand)
   int64_t kext;
+  int kmul;        // bytes per k inside a 256-wide K block (2, or 32 for the chunked layout)
   int voff[I::LPW];
   int kloc[I::LPW];
   int vfull[I::LPW];
@@ -136,6 +138,7 @@ __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int
   Stream st;
   st.kext = op.kext;
   st.blk = op.blk ? op.blk : BLK;  // row-major: K block b starts 256*b elements into the row
+  st.kmul = 2;
   st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
   const int rsub = lane / I::CH, pc = lane % I::CH;
 #pragma unroll
@@ -150,6 +153,31 @@ __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int
   return st;
 }
 
+// The chunked layout (Operand::chunked): inside each 256-wide K block, the 16 x 32 piece of rows 16a.. and k
+// 32b.. is 1 KiB contiguous, [16 m][32 k], at ((a*8 + b) * 512) elements from the block's row 0. A 64-wide stage
+// of a 256-row tile is then 32 such pieces, one per load instruction (instruction l = 2*(row block) + k half),
+// and its LDS image is the same pieces back to back, with the 16-byte chunks of a 64-byte piece row XOR-swizzled
+// by swzc(row % 16) so that fragment reads are bank-conflict free.
+__device__ __forceinline__ int swzc(int r16) { return (r16 >> 1) & 3; }
+
+__device__ __forceinline__ Stream make_stream_chunked(const Operand& op, int64_t m0, int wave, int lane) {
+  Stream st;
+  st.kext = op.kext;
+  st.blk = op.blk;
+  st.kmul = 32;  // a 64-wide stage advances two 1 KiB pieces
+  st.base = reinterpret_cast<uint64_t>(op.p + m0 * 256);
+  const int r16 = lane >> 2, c = (lane & 3) ^ swzc(lane >> 2);
+#pragma unroll
+  for (int j = 0; j < I::LPW; ++j) {
+    const int l = wave * I::LPW + j, rb = l >> 1, h = l & 1;
+    const bool in = m0 + rb * 16 + r16 < op.mext;
+    st.voff[j] = (rb * 8 + h) * 1024 + r16 * 64 + c * 16;
+    st.kloc[j] = in ? h * 32 + c * 8 : OOB;
+    st.vfull[j] = in ? st.voff[j] : OOB;
+  }
+  return st;
+}
+
 // Resource and K limit of one stage of a stream. A stage past the range gets a resource with no records, so
 // every lane reads zeros without touching memory.
 struct StageSrc {
@@ -159,7 +187,7 @@ struct StageSrc {
 __device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage, int send) {
   const int64_t k0 = (int64_t)stage * BK;
   const int64_t klim64 = stage < send ? st.kext - k0 : 0;
-  const uint64_t off = (uint64_t)((k0 >> 8) * st.blk + (k0 & (BLK - 1))) * 2;
+  const uint64_t off = (uint64_t)((k0 >> 8) * st.blk) * 2 + (uint64_t)((k0 & (BLK - 1)) * st.kmul);
   StageSrc g{make_rsrc(st.base + off), klim64 < 0 ? 0 : (klim64 > BK ? BK : (int)klim64)};
   if (stage >= send) g.rsrc[2] = 0;
   return g;
@@ -195,6 +223,9 @@ struct FragAddr {
   uint32_t a[4][2];  // [kk][i & 1], A image of buffer 0
   uint32_t b[4][2];  // [kk][j & 1], B image of buffer 0
 };
+// ACH: the A image holds the chunked layout, where row r, 8-wide k chunk c is at (r/16)*2048 + (c/4)*1024 +
+// (r%16)*64 + ((c%4) ^ swzc(r%16))*16; rows 64 apart are again 8 KiB apart, so the same immediates apply.
+template <bool ACH>
 __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
   FragAddr ad;
 #pragma unroll
@@ -204,7 +235,10 @@ __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
       const int c = kk * 2 + (lane >> 5);
       const int ra = wm * 128 + p * 32 + (lane & 31);
       const int rb = wn * 128 + p * 32 + (lane & 31);
-      ad.a[kk][p] = AOFF + ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
+      if constexpr (ACH)
+        ad.a[kk][p] = AOFF + (ra >> 4) * 2048 + (c >> 2) * 1024 + (ra & 15) * 64 + (((c & 3) ^ swzc(ra & 15)) << 4);
+      else
+        ad.a[kk][p] = AOFF + ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
       ad.b[kk][p] = BOFF + rb * I::ROWB + ((c ^ I::swz(rb)) << 4);
     }
   return ad;
@@ -325,7 +359,8 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
 }
 
 // C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over the K stages s0 .. s0+nk-1 (k in [s0*BK, (s0+nk)*BK),
-// clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK.
+// clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK. ACH: A
+// is in the chunked layout (B never is).
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
 //                                              [wn*128 + nj*32 + lane%32].
 // Two 64 KiB LDS stages, four 16-wide K slices per stage; the fragments of slice kk+1 are read while slice kk is
@@ -334,7 +369,7 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF>
+template <bool KF, bool ACH = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4]) {
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
@@ -348,9 +383,9 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const Stream sa = make_stream(A, m0, wave, lane);
+  const Stream sa = ACH ? make_stream_chunked(A, m0, wave, lane) : make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
-  const FragAddr ad = make_frag_addr(wm, wn, lane);
+  const FragAddr ad = make_frag_addr<ACH>(wm, wn, lane);
   const int send = s0 + nk;
   // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
   issue_stage(sa, s0, send, lds, AOFF, wave);
@@ -686,7 +721,8 @@ __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__
 // and c = -wgt otherwise (cross-entropy and the mixture: go*wgt*(softmax - onehot)), written to both K-blocked
 // layouts:
 //   G   element (n, v) at G[(v/256)*Np*256 + n*256 + v%256]    (for dH, reduction over v)
-//   Gt  element (v, n) at Gt[(n/256)*Vp*256 + v*256 + n%256]   (for dW, reduction over n)
+//   Gt  element (v, n) at Gt[(n/256)*Vp*256 + ((v/16)*8 + (n%256)/32)*512 + (v%16)*32 + n%32]   (for dW,
+//       reduction over n; the chunked layout of Operand::chunked)
 // Each tile is one contiguous 128 KiB block of either buffer. The tile is staged in LDS as [256 n][256 v]
 // (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))):
 //   1. every lane writes go*wgt*exp(x - lse) for its 256 logits (8-byte writes);
@@ -814,8 +850,9 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 #pragma unroll
     for (int e = 0; e < 8; ++e) dbs[(wave * 32 + lane) * 8 + e] = db[e];
   }
-  // 4. Gt block of this tile ([256 v][256 n], contiguous). Task id -> (16 v from v16, 8 n from n8); 16-lane
-  //    group gi handles tasks gi, gi+16, ...; lane p of the group ends with (v16 + p, n8 .. n8+7).
+  // 4. Gt block of this tile (256 v x 256 n, contiguous, in 1 KiB [16 v][32 n] pieces). Task id -> (16 v from
+  //    v16, 8 n from n8); 16-lane group gi handles tasks gi, gi+16, ...; lane p of the group ends with (v16 + p,
+  //    n8 .. n8+7), and the four groups of a wave hold one whole piece, so every store instruction is contiguous.
   char* gtblk = reinterpret_cast<char*>(Gt + ((int64_t)tn * Vp + v0) * BLK);
   const int gi = t >> 4, p = t & 15;
 #pragma unroll 4
@@ -831,8 +868,10 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           (bf16x4 LDS_AS*)(lds + nl * 512 + ((vl * 2) ^ (gsw(nl) << 4))));
     }
     const bf16x8 o{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
+    // chunked layout: piece (v16/16, n8/32) is [16 v][32 n]; the wave's four groups fill one piece (1 KiB)
     __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o),
-                                reinterpret_cast<u32x4*>(gtblk + (int64_t)(v16 + p) * 512 + n8 * 2));
+                                reinterpret_cast<u32x4*>(gtblk + (int64_t)((v16 >> 4) * 8 + (n8 >> 5)) * 1024 +
+                                                         p * 64 + (n8 & 31) * 2));
   }
   if (dbias_part != nullptr) {
     __syncthreads();
@@ -897,7 +936,7 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16, bool KF>
+template <bool OUT_BF16, bool KF, bool ACH>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part) {
@@ -918,7 +957,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   tile_of(lin, tiles_m, tiles_n, group, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile<KF>(A, B, s0, nk, m0, n0, lds, acc);
+  gemm_tile<KF, ACH>(A, B, s0, nk, m0, n0, lds, acc);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   if (slot >= 0) {
@@ -1002,7 +1041,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
 }
 
 // Backward workspace (Np = N and Vp = V rounded up to 256):
-//   G   [Vp/256][Np][256] bf16, Gt [Np/256][Vp][256] bf16 (written by k_bwd_grad)
+//   G   [Vp/256][Np][256] bf16, Gt [Np/256][Vp/16][8][16][32] bf16 (chunked; written by k_bwd_grad)
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
 //   dbias_part [Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split tails)
 //   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), fix_col int32 / fix_val fp32 [Np][MAX_KC]
@@ -1065,12 +1104,23 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (R && P > TAIL_SLOTS / R) P = TAIL_SLOTS / R;
   const int full = (R && P >= 2) ? T - R : T;
   if (full == T) P = 1;
-  if (A.kext % BK == 0 && B.kext % BK == 0)
-    hipLaunchKernelGGL((k_gemm<OUT_BF16, true>), dim3(full + (T - full) * P), dim3(NTHREADS), 0, st, A, B, nk, M,
-                       Nc, tiles_m, tiles_n, group, full, P, C, ldc, part);
-  else
-    hipLaunchKernelGGL((k_gemm<OUT_BF16, false>), dim3(full + (T - full) * P), dim3(NTHREADS), 0, st, A, B, nk, M,
-                       Nc, tiles_m, tiles_n, group, full, P, C, ldc, part);
+  const bool kf = A.kext % BK == 0 && B.kext % BK == 0;
+  const dim3 grid(full + (T - full) * P);
+  if (A.chunked) {
+    if (kf)
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
+                         tiles_n, group, full, P, C, ldc, part);
+    else
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
+                         tiles_n, group, full, P, C, ldc, part);
+  } else {
+    if (kf)
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
+                         tiles_n, group, full, P, C, ldc, part);
+    else
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
+                         tiles_n, group, full, P, C, ldc, part);
+  }
   int rc = launch_status();
   if (rc || full == T) return rc;
   hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 16, T - full), dim3(BN), 0, st, part, P, full, tiles_m,
@@ -1318,8 +1368,8 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
                      ldh, N, K, w.Ht);
   if ((rc = launch_status())) return rc;
   // dW[v, k] = sum_n Gt(v, n) Ht(k, n), reduction over n < N
-  const Operand Aop{w.Gt, BLK, V, N, w.vp * BLK};
-  const Operand Bop{w.Ht, BLK, K, N, K * BLK};
+  const Operand Aop{w.Gt, BLK, V, N, w.vp * BLK, 1};
+  const Operand Bop{w.Ht, BLK, K, N, K * BLK, 0};
   return launch_gemm<false>(Aop, Bop, (int)cdiv(N, BK), V, K, 4, dW, lddw, w.part, st);
 }
 
