@@ -881,13 +881,20 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   }
 }
 
+// dBias[v] = sum over the tiles_n row-tile partials of column v. A block covers 64 columns with four threads per
+// column, each summing every fourth partial; the four sums are added in a fixed order, so the result is
+// deterministic.
 __global__ __launch_bounds__(256) void k_dbias_reduce(const float* __restrict__ part, int tiles_n, int64_t ldp,
                                                       int64_t V, float* __restrict__ dbias) {
-  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (v >= V) return;
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t v = (int64_t)blockIdx.x * 64 + c;
   float s = 0.f;
-  for (int i = 0; i < tiles_n; ++i) s += part[(int64_t)i * ldp + v];
-  dbias[v] = s;
+  if (v < V)
+    for (int i = g; i < tiles_n; i += 4) s += part[(int64_t)i * ldp + v];
+  red[g][c] = s;
+  __syncthreads();
+  if (g == 0 && v < V) dbias[v] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
 }
 
 __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, const float* __restrict__ go, int64_t N,
@@ -1233,7 +1240,7 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
                        dBias ? w.dbias_part : nullptr);
   if ((rc = launch_status())) return rc;
   if (dBias) {
-    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
+    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
                        dBias);
     if ((rc = launch_status())) return rc;
   }
