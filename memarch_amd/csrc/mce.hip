@@ -358,9 +358,40 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
   }
 }
 
+// Row offset (within the wave's 128 rows) held by accumulator register r of lane half lh in M-subtile mi.
+__device__ __forceinline__ constexpr int acc_row(int mi, int r, int lh) {
+  return mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+}
+
+// Bias + vocabulary mask of a tile's 256 vocabulary rows: tile_bias() reads bias[v0 + t] (one value per thread,
+// issued before the mainloop's first loads); stash_bias() stores bias or -inf (v >= V_real) into a 1 KiB LDS slot;
+// read_bias_mask() gives a lane the 64 values of its logit rows (v = v_lane + acc_row(mi, r, lh); r%4 = 0..3 are
+// consecutive, so 16 ds_read_b128). gemm_tile<.., BIAS> uses them to start the accumulators at the bias.
+__device__ __forceinline__ float tile_bias(const float* __restrict__ bias, int64_t v0, int64_t V) {
+  const int64_t v = v0 + threadIdx.x;
+  return (bias != nullptr && v < V) ? bias[v] : 0.f;
+}
+__device__ __forceinline__ void stash_bias(float* slot, float b, int64_t v0, int64_t Vreal) {
+  slot[threadIdx.x] = (v0 + threadIdx.x < Vreal) ? b : -INFINITY;
+}
+__device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* slot, int wm, int lh) {
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = *reinterpret_cast<const float4*>(slot + wm * 128 + acc_row(mi, 4 * q, lh));
+      bm[mi][4 * q + 0] = f.x;
+      bm[mi][4 * q + 1] = f.y;
+      bm[mi][4 * q + 2] = f.z;
+      bm[mi][4 * q + 3] = f.w;
+    }
+}
+
 // C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over the K stages s0 .. s0+nk-1 (k in [s0*BK, (s0+nk)*BK),
 // clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK. ACH: A
-// is in the chunked layout (B never is).
+// is in the chunked layout (B never is). BIAS: A's rows are vocabulary rows and every accumulator starts at its
+// row's bias, masked to -inf for rows >= Vreal (btile: this thread's bias value from tile_bias; bslot: 1 KiB of
+// LDS outside the operand ring), so the epilogue reads the biased, masked logits straight from the accumulators.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
 //                                              [wn*128 + nj*32 + lane%32].
 // Two 64 KiB LDS stages, four 16-wide K slices per stage; the fragments of slice kk+1 are read while slice kk is
@@ -369,19 +400,22 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool ACH = false>
+template <bool KF, bool ACH = false, bool BIAS = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
-                                          char* lds, f32x16 (&acc)[4][4]) {
+                                          char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
+                                          int64_t Vreal = 0) {
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
   const int wm = wave >> 1, wn = wave & 1;
+  if constexpr (!BIAS) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  }
 
   const Stream sa = ACH ? make_stream_chunked(A, m0, wave, lane) : make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
@@ -391,8 +425,20 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   issue_stage(sa, s0, send, lds, AOFF, wave);
   issue_stage(sb, s0, send, lds, BOFF, wave);
   issue_stage(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
+  if constexpr (BIAS) stash_bias(bslot, btile, m0, Vreal);
   wait_vmcnt<I::LPW>();
   __syncthreads();
+  if constexpr (BIAS) {
+    // the accumulators start at the row's bias (or -inf past V_real): x = b_v + sum_k w_vk h_nk
+    float bm[4][16];
+    read_bias_mask(bm, bslot, wm, lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = bm[i][r];
+  }
 
   bf16x8 fa[2][4], fb[2][4];
   read_frags<0, 0>(lds, ad, fa[0], fb[0]);
@@ -435,34 +481,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)a | ((uint32_t)b << 16);
 }
 
-// Row offset (within the wave's 128 rows) held by accumulator register r of lane half lh in M-subtile mi.
-__device__ __forceinline__ constexpr int acc_row(int mi, int r, int lh) {
-  return mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-}
-
-// Bias + vocabulary mask of a tile's 256 vocabulary rows, in two steps so that only one register per thread
-// is live across the mainloop: tile_bias() (before the mainloop) reads bias[v0 + t]; stash_bias() (after it)
-// stores bias or -inf (v >= V_real) into a 1 KiB LDS slot; read_bias_mask() gives a lane the 64 values of its
-// logit rows (v = v_lane + acc_row(mi, r, lh); r%4 = 0..3 are consecutive, so 16 ds_read_b128).
-__device__ __forceinline__ float tile_bias(const float* __restrict__ bias, int64_t v0, int64_t V) {
-  const int64_t v = v0 + threadIdx.x;
-  return (bias != nullptr && v < V) ? bias[v] : 0.f;
-}
-__device__ __forceinline__ void stash_bias(float* slot, float b, int64_t v0, int64_t Vreal) {
-  slot[threadIdx.x] = (v0 + threadIdx.x < Vreal) ? b : -INFINITY;
-}
-__device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* slot, int wm, int lh) {
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 f = *reinterpret_cast<const float4*>(slot + wm * 128 + acc_row(mi, 4 * q, lh));
-      bm[mi][4 * q + 0] = f.x;
-      bm[mi][4 * q + 1] = f.y;
-      bm[mi][4 * q + 2] = f.z;
-      bm[mi][4 * q + 3] = f.w;
-    }
-}
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
@@ -482,12 +500,9 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
   const int lr = lane & 31, lh = lane >> 5;
   const float btile = tile_bias(bias, v0, V);
   f32x16 acc[4][4];
-  gemm_tile<KF>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
-  float* bslot = reinterpret_cast<float*>(lds + LDS_BYTES);
-  stash_bias(bslot, btile, v0, Vreal);
-  __syncthreads();
-  float bm[4][16];
-  read_bias_mask(bm, bslot, wm, lh);
+  // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
+  gemm_tile<KF, false, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+                             reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
 
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
 #pragma unroll
@@ -496,7 +511,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r] + bm[mi][r]);
+      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r]);
     m = fmaxf(m, __shfl_xor(m, 32));
     float s = 0.f;
     if (m != -INFINITY) {
@@ -504,8 +519,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          s += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r] + bm[mi][r], LOG2E, -mb));
+        for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -mb));
     }
     s += __shfl_xor(s, 32);
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
@@ -772,7 +786,9 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           : 0.f;
 
   f32x16 acc[4][4];
-  gemm_tile<KF>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc);
+  // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
+  gemm_tile<KF, false, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+                             reinterpret_cast<float*>(lds + LDS_BYTES + 4 * 32 * 8 * 4), Vreal);
   // sparse fix-ups of row nf (nfix > 0 only with a sparse bias; the loads overlap the staging below)
   int scol[MAX_KC];
   float sval[MAX_KC];
@@ -784,12 +800,6 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
       sval[f] = ok ? fix_val[nf * MAX_KC + f] : 0.f;
     }
   }
-  float* bslot = reinterpret_cast<float*>(lds + LDS_BYTES + 4 * 32 * 8 * 4);
-  stash_bias(bslot, btile, v0, Vreal);
-  __syncthreads();
-  float bm[4][16];
-  read_bias_mask(bm, bslot, wm, lh);
-
   // 1. stage go*wgt*exp(x - lse) as bf16: lane holds 4 consecutive v (r%4) of one row n -> 8-byte LDS writes
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
@@ -803,8 +813,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
         float g4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          g4[e] = cn[nj] * __builtin_amdgcn_exp2f(
-                               __builtin_fmaf(acc[mi][nj][4 * q + e] + bm[mi][4 * q + e], LOG2E, -lb[nj]));
+          g4[e] = cn[nj] * __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][4 * q + e], LOG2E, -lb[nj]));
         const int vl = wm * 128 + acc_row(mi, 4 * q, lh);
         u32x2 pk;
         pk[0] = pack_bf16x2(g4[0], g4[1]);
