@@ -776,7 +776,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
     const bool ok = n < N;
     cn[nj] = ok ? gscale * wgt_rows[n] : 0.f;
-    lb[nj] = ok ? lse_rows[n] * LOG2E : 0.f;
+    lb[nj] = ok ? lse_rows[n] * LOG2E : INFINITY;  // rows past N: exp2(-inf) = 0 whatever the logit
   }
   const int64_t nf = n0 + t;  // the row this thread fixes up in step 2
   const int64_t yf = nf < N ? y[nf] : -1;

@@ -8,6 +8,7 @@ import pytest
 import torch
 
 from cases import GRAD_RTOL, LOSS_RTOL, assert_parity, gpu_run, oracle_of, random_case
+from oracle import mce_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -95,3 +96,27 @@ def test_skewed_targets():
     got = gpu_run(case)
     fwd, bwd = oracle_of(case)
     assert_parity(got, fwd, bwd, "skewed")
+
+
+def test_large_bias_with_partial_row_tile():
+    """Plain cross-entropy with a bias large enough that exp(b) overflows fp32 (b = 95 and 120 on a few ids) and
+    N = 300 rows, so the last 256-row tile is mostly padding: padded rows must contribute exact zeros to G and
+    dBias (no inf * 0), while the real rows' gradients (softmax mass on the large-bias id) are large."""
+    from memarch_amd import fused_ops
+    case = random_case(300, 128, 1000, None, True, seed=21)
+    case["bias"][[3, 500, 999]] = torch.tensor([95.0, 120.0, 110.0])
+    h = case["h"].cuda().bfloat16().requires_grad_()
+    w = case["w"].cuda().requires_grad_()
+    b = case["bias"].cuda().requires_grad_()
+    loss = fused_ops.linear_ce_mix_biased(h, w, b, case["y"].cuda(), None, None)
+    loss.backward()
+    torch.cuda.synchronize()
+    got = dict(loss=float(loss), dh=h.grad.float().cpu().numpy(), dw=w.grad.cpu().numpy(),
+               dbias=b.grad.cpu().numpy(), dgate=np.zeros(300))
+    assert np.isfinite(got["dbias"]).all() and np.isfinite(got["dw"]).all() and np.isfinite(got["dh"]).all()
+    hh = orc.bf16_round(case["h"].numpy())
+    ww = orc.bf16_round(case["w"].numpy())
+    fwd = orc.forward(hh, ww, case["y"].numpy(), None, None, case["bias"].numpy(), None, np.float64)
+    bwd = orc.backward(hh, ww, case["y"].numpy(), None, None, case["bias"].numpy(), None, 1.0, fwd, np.float64)
+    bwd = dict(bwd, dgate=np.zeros(300))
+    assert_parity(got, fwd, bwd, "large bias")
