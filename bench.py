@@ -5,7 +5,8 @@ inputs (default: config 2, N = 32768 tokens, d = 2048, V = 50304 (50257 real), b
 accumulation), with every input resident in HBM before the timed region. Prints one JSON line:
   value         tokens/s of the whole step: N*K / (wall time of K steps between two synchronisations)
   roofline      the dominant kernel of the step: its algorithmic FLOPs per launch (one N x V x d contraction,
-                2*N*V*d) over its average duration, timed with HIP events on the stream it is launched on;
+                2*N*V*d) over its average duration in the timed steps, from HIP events recorded around each C-ABI
+                stage on the stream it is launched on (torch's current stream);
                 `traffic` is its HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
                 profiles/ (null when that summary does not cover this kernel and configuration)
   op_roofline   the whole step against the bf16 MFMA peak on the op's 6*N*V*d algorithmic FLOPs (the
@@ -39,6 +40,8 @@ METRIC = "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA pea
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 
 # C-ABI stage -> the kernel that dominates it (the stage also runs small helpers: see stage_times)
+STAGE_OF_CALL = {"mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
+                 "mce_bwd_dweight": "dweight"}
 STAGE_KERNEL = {"fwd": "k_fwd_tiles<true>", "logits_grad": "k_bwd_grad<true>", "dhidden": "k_gemm<true, true>",
                 "dweight": "k_gemm<false, true>"}
 
@@ -50,7 +53,8 @@ def _args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--cpu-rows", type=int, default=16384, help="rows of the CPU baseline sample (0: skip)")
-    ap.add_argument("--stage-reps", type=int, default=5, help="timed repetitions of each kernel stage")
+    ap.add_argument("--stage-reps", type=int, default=0,
+                    help="extra isolated timed repetitions of each C-ABI stage after the timed steps (0: none)")
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
     ap.add_argument("--op", choices=("fused_ce", "swiglu"), default="fused_ce",
                     help="fused_ce: the north-star operator (default); swiglu: the SwiGLU gate kernels")
@@ -58,8 +62,8 @@ def _args():
 
 
 def stage_times(inp, reps):
-    """Average duration (ms) of each C-ABI stage, timed with torch events on the current stream (the stream
-    every stage is launched on). fwd = k_fwd_tiles + k_fwd_merge + k_sum; logits_grad = k_bwd_grad +
+    """Average duration (ms) of each C-ABI stage run in isolation `reps` times after the timed steps, timed with
+    torch events on the current stream (the stream every stage is launched on). fwd = k_fwd_tiles + k_fwd_merge + k_sum; logits_grad = k_bwd_grad +
     k_dbias_reduce + k_dgate; dhidden = k_transpose_blocked (W) + k_gemm<true>; dweight = k_transpose_blocked
     (H) + k_gemm<false>."""
     from memarch_amd import _lib
@@ -252,16 +256,34 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # HIP events around every C-ABI stage of the timed steps, on the stream the stages are launched on
+    from memarch_amd import _lib
+    marks = []
+
+    def hook(name, phase):
+        if name in STAGE_OF_CALL:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            marks.append((name, phase, ev))
+
     print("[bench] timed steps", file=sys.stderr, flush=True)
+    _lib.set_call_hook(hook)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
+    _lib.set_call_hook(None)
+    live = {}
+    for (name, ph0, e0), (name1, ph1, e1) in zip(marks[0::2], marks[1::2]):
+        assert name == name1 and ph0 == "begin" and ph1 == "end"
+        live.setdefault(STAGE_OF_CALL[name], []).append(e0.elapsed_time(e1))
+    stages = {k: sum(v) / len(v) for k, v in live.items()}
     tok_s = n / dt
     flops = 6.0 * n * v * d
-    print("[bench] stage timing", file=sys.stderr, flush=True)
-    stages = stage_times(inp, args.stage_reps)
+    if args.stage_reps > 0:
+        print("[bench] isolated stage timing", file=sys.stderr, flush=True)
+        isolated = stage_times(inp, args.stage_reps)
     dom = max(stages, key=stages.get)
     kflops = 2.0 * n * v * d   # every stage's kernel is one N x V x d contraction
     ach = kflops / (stages[dom] * 1e-3)
@@ -280,6 +302,8 @@ def main():
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
     }
+    if args.stage_reps > 0:
+        res["isolated_stages_ms"] = {k: round(x, 3) for k, x in isolated.items()}
     if args.cpu_rows > 0:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_rows, n))

@@ -45,6 +45,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_call_hook = None  # optional callable(name, phase) run around every C-ABI call, phase "begin" / "end"
 
 
 class MceError(RuntimeError):
@@ -74,5 +75,18 @@ def check(rc, what):
         raise MceError(f"{what} failed: {msg} (code {rc}, hipError {hip})")
 
 
+def set_call_hook(fn):
+    """Install fn(name, phase) to be called just before ("begin") and after ("end") every C-ABI call (e.g. to
+    record stream events around each stage); returns the previous hook. None removes it."""
+    global _call_hook
+    prev, _call_hook = _call_hook, fn
+    return prev
+
+
 def call(name, *args):
+    hook = _call_hook
+    if hook is not None:
+        hook(name, "begin")
     check(getattr(load(), name)(*args), name)
+    if hook is not None:
+        hook(name, "end")
