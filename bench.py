@@ -42,7 +42,7 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 # C-ABI stage -> the kernel that dominates it (the stage also runs small helpers: see stage_times)
 STAGE_OF_CALL = {"mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
                  "mce_bwd_dweight": "dweight"}
-STAGE_KERNEL = {"fwd": "k_fwd_tiles<true>", "logits_grad": "k_bwd_grad<true>", "dhidden": "k_gemm<true, true, false>",
+STAGE_KERNEL = {"fwd": "k_fwd_tiles<true>", "logits_grad": "k_bwd_grad<true>", "dhidden": "k_gemm<true, true, true>",
                 "dweight": "k_gemm<false, true, true>"}
 
 

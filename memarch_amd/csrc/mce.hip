@@ -10,18 +10,19 @@
 // staging registers); the next stage's loads are in flight while the current stage is multiplied.
 //
 // Every operand is a logical [M, K] matrix with K contiguous: element (m, k) at p[m*ld + k], or, in the
-// K-blocked layout of the internal buffers, at p[(k/256)*blk + m*256 + k%256] (256-wide K blocks, each a
-// contiguous [M][256] panel). The LDS image of one stage is [256 m][64 k] with 128-byte rows and the
-// 16-byte chunk index XOR-swizzled by the row, so fragment reads (ds_read_b128) are bank-conflict free.
-// Elements outside an operand's extent read as zero (out-of-range buffer offsets), so partial tiles need
-// no special path.
+// K-blocked layout of the transposed copies, at p[(k/256)*blk + m*256 + k%256] (256-wide K blocks, each a
+// contiguous [M][256] panel), or, for G and G^T, in tile-blocked 128-byte pieces (Operand::cm). The LDS image
+// of one stage is [256 m][64 k] with 128-byte rows and the 16-byte chunk index XOR-swizzled by the row (or in
+// piece order for a piece-layout operand), so fragment reads (ds_read_b128) are bank-conflict free. Elements
+// outside an operand's extent read as zero (out-of-range buffer offsets), so partial tiles need no special path.
 //
 //   forward     S^T = W H^T           -> per-half-tile row max / sum-exp; target logit by a dot product;
 //                                         merge -> lse, loss, wgt, dgr
-//   logits-grad S^T = W H^T recomputed -> G = go*wgt*(softmax - onehot) (bf16) written twice through LDS:
-//                                         G (v contiguous, for dH) and G^T (n contiguous, for dW); dBias partials
+//   logits-grad S^T = W H^T recomputed -> G = go*wgt*(softmax - onehot) (bf16) stored from registers as G
+//                                         (for dH) and, transposed by MFMAs, as G^T (for dW); dBias partials
 //   dhidden     dH  = G   . Wt  with Wt = W^T (K-blocked copy made by k_transpose_blocked)
 //   dweight     dW  = G^T . Ht  with Ht = H^T (K-blocked copy)
+// (the reduction index of G, G^T, Wt and Ht is stored in the kperm order)
 // The N x V logits never reach memory; G is the only N x V intermediate.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -29,7 +30,7 @@
 
 #include "../../include/mce.h"
 
-#define MCE_VERSION 310
+#define MCE_VERSION 320
 
 typedef int32_t mce_i32x4 __attribute__((ext_vector_type(4)));
 // The LLVM intrinsic behind `buffer_load_dword... lds`: (resource, LDS base, bytes per lane, per-lane offset,
@@ -65,12 +66,32 @@ static_assert(LDS_BYTES <= 160 * 1024, "operand ring exceeds the 160 KiB of LDS 
 
 struct Operand {
   const uint16_t* p;  // bf16 bits
-  int64_t ld;         // row stride in elements (256 in the K-blocked layout)
+  int64_t ld;         // row stride in elements (256 in the K-blocked layout); chunk-column stride when cm
   int64_t mext;       // valid extent along M
   int64_t kext;       // valid extent along K
   int64_t blk;        // 0, or the element distance between consecutive 256-wide K blocks
-  int chunked;        // 1: K-blocked and, within a block, [M/16][32-wide K chunk][16 m][32 k] (1 KiB pieces)
+  int cm;             // 1: tile-blocked chunk-major (below)
 };
+// Tile-blocked piece layout (Operand::cm) of an [M][K] operand with M and K padded to multiples of 256: every
+// 256 x 256 tile is one contiguous 128 KiB block of 128-byte pieces [8 m][8 k], [32 row groups][32 k chunks], and
+// the block of tile (m/256, k/256) starts at (k/256)*blk + (m/256)*65536:
+//   element (m, k) at p[(k/256)*blk + (m/256)*65536 + (((m%256)/8)*32 + (k%256)/8)*64 + (m%8)*8 + k%8],
+//   blk = 256 * Mpad.
+// The 8 rows x 64 k of one load instruction of a stage are then 1 KiB contiguous, and 32 consecutive m of one
+// 8-wide k chunk are four whole 128-byte pieces.
+constexpr int64_t CM_TILE = 256 * 256;
+// The reduction index of G, Gt and of the transposed copies Wt, Ht is stored permuted inside each 32-wide group:
+// index 8q + 4h + e (q < 4, h < 2, e < 4) at position 16h + 4q + e. A lane of the logits-grad epilogue holds, for
+// one row, the indices with one h, which are then 16 consecutive positions (two 16-byte stores). The dH and dW
+// contractions sum over positions, so the permutation cancels as long as both operands use it.
+__host__ __device__ constexpr int kperm(int k) {
+  return (k & ~31) | (((k >> 2) & 1) << 4) | (((k >> 3) & 3) << 2) | (k & 3);
+}
+// the index stored at position p
+__host__ __device__ constexpr int kperm_inv(int p) {
+  return (p & ~31) | (((p >> 2) & 3) << 3) | (((p >> 4) & 1) << 2) | (p & 3);
+}
+static_assert(kperm_inv(kperm(13)) == 13 && kperm_inv(kperm(58)) == 58 && kperm(kperm_inv(22)) == 22, "kperm");
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone). gfx9 encoding: vmcnt[3:0] and vmcnt[5:4] at bits 15:14.
 template <int N>
@@ -128,51 +149,38 @@ struct Stream {
   uint64_t base;   // bytes: element (m0, 0)
   int64_t blk;     // element distance between 256-wide K blocks (256 for a row-major operand)
   int64_t kext;
-  int kmul;        // bytes per k inside a 256-wide K block (2, or 32 for the chunked layout)
+  int kmul;        // bytes per k inside a 256-wide K block (2; 16 in the tile-blocked piece layout)
   int voff[I::LPW];
   int kloc[I::LPW];
   int vfull[I::LPW];
 };
 
+// Row-major / K-blocked: lane l of load instruction i reads row m = 8i + l/8, logical chunk c = (l%8) ^ swz(m), at
+// m*ld*2 + 16c bytes from the stage's base, and lands at l*16 in the instruction's 1 KiB of the swizzled [256][64]
+// image: the 8 lanes of a row read one 128-byte segment.
+// Tile-blocked pieces (Operand::cm, m0 a multiple of 256): lane l reads row m = 8i + l%8, chunk c = l/8, at
+// (m/8)*4096 + c*128 + (m%8)*16 = 4096i + 16l, so an instruction reads 1 KiB contiguously into the piece-order
+// image (make_frag_addr<true>); a k step inside a 256-wide K block is 16 bytes.
 __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
   Stream st;
   st.kext = op.kext;
-  st.blk = op.blk ? op.blk : BLK;  // row-major: K block b starts 256*b elements into the row
-  st.kmul = 2;
-  st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
-  const int rsub = lane / I::CH, pc = lane % I::CH;
-#pragma unroll
-  for (int j = 0; j < I::LPW; ++j) {
-    const int row = (wave * I::LPW + j) * I::RPI + rsub;
-    const int c = pc ^ I::swz(row);
-    const bool in = m0 + row < op.mext;
-    st.voff[j] = (int)(row * op.ld * 2) + c * 16;
-    st.kloc[j] = in ? c * 8 : OOB;
-    st.vfull[j] = in ? st.voff[j] : OOB;
+  if (op.cm) {
+    st.blk = op.blk;
+    st.kmul = 16;
+    st.base = reinterpret_cast<uint64_t>(op.p + (m0 / BM) * CM_TILE);
+  } else {
+    st.blk = op.blk ? op.blk : BLK;  // row-major: K block b starts 256*b elements into the row
+    st.kmul = 2;
+    st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
   }
-  return st;
-}
-
-// The chunked layout (Operand::chunked): inside each 256-wide K block, the 16 x 32 piece of rows 16a.. and k
-// 32b.. is 1 KiB contiguous, [16 m][32 k], at ((a*8 + b) * 512) elements from the block's row 0. A 64-wide stage
-// of a 256-row tile is then 32 such pieces, one per load instruction (instruction l = 2*(row block) + k half),
-// and its LDS image is the same pieces back to back, with the 16-byte chunks of a 64-byte piece row XOR-swizzled
-// by swzc(row % 16) so that fragment reads are bank-conflict free.
-__device__ __forceinline__ int swzc(int r16) { return (r16 >> 1) & 3; }
-
-__device__ __forceinline__ Stream make_stream_chunked(const Operand& op, int64_t m0, int wave, int lane) {
-  Stream st;
-  st.kext = op.kext;
-  st.blk = op.blk;
-  st.kmul = 32;  // a 64-wide stage advances two 1 KiB pieces
-  st.base = reinterpret_cast<uint64_t>(op.p + m0 * 256);
-  const int r16 = lane >> 2, c = (lane & 3) ^ swzc(lane >> 2);
 #pragma unroll
   for (int j = 0; j < I::LPW; ++j) {
-    const int l = wave * I::LPW + j, rb = l >> 1, h = l & 1;
-    const bool in = m0 + rb * 16 + r16 < op.mext;
-    st.voff[j] = (rb * 8 + h) * 1024 + r16 * 64 + c * 16;
-    st.kloc[j] = in ? h * 32 + c * 8 : OOB;
+    const int ins = wave * I::LPW + j;
+    const int row = op.cm ? ins * 8 + (lane & 7) : ins * I::RPI + lane / I::CH;
+    const int c = op.cm ? lane >> 3 : (lane % I::CH) ^ I::swz(row);
+    const bool in = m0 + row < op.mext;
+    st.voff[j] = op.cm ? ins * 4096 + lane * 16 : (int)(row * op.ld * 2) + c * 16;
+    st.kloc[j] = in ? c * 8 : OOB;
     st.vfull[j] = in ? st.voff[j] : OOB;
   }
   return st;
@@ -219,13 +227,14 @@ __device__ __forceinline__ void issue_stage(const Stream& st, int stage, int sen
 // (row0 + l%32, kk*16 + 8*(l/32) + 0..7) of a 32-row block), computed once per tile. Fragment i of slice kk is
 // at a[kk][i&1] + (i>>1)*64 rows: rows 64 apart share the XOR swizzle, so the rest is a compile-time offset,
 // as is the ring buffer (b*OPB). The mainloop then reads with immediates only.
+// APC: the A image is in piece order (an Operand::cm operand): the 16-byte chunk c of row r at
+// (r/8)*1024 + c*128 + (r%8)*16, so the 8 rows of a row group that one 8-lane group reads lie in 128 contiguous
+// bytes (no swizzle needed), and rows 64 apart are again 8 KiB apart.
 struct FragAddr {
   uint32_t a[4][2];  // [kk][i & 1], A image of buffer 0
   uint32_t b[4][2];  // [kk][j & 1], B image of buffer 0
 };
-// ACH: the A image holds the chunked layout, where row r, 8-wide k chunk c is at (r/16)*2048 + (c/4)*1024 +
-// (r%16)*64 + ((c%4) ^ swzc(r%16))*16; rows 64 apart are again 8 KiB apart, so the same immediates apply.
-template <bool ACH>
+template <bool APC>
 __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
   FragAddr ad;
 #pragma unroll
@@ -235,8 +244,8 @@ __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
       const int c = kk * 2 + (lane >> 5);
       const int ra = wm * 128 + p * 32 + (lane & 31);
       const int rb = wn * 128 + p * 32 + (lane & 31);
-      if constexpr (ACH)
-        ad.a[kk][p] = AOFF + (ra >> 4) * 2048 + (c >> 2) * 1024 + (ra & 15) * 64 + (((c & 3) ^ swzc(ra & 15)) << 4);
+      if constexpr (APC)
+        ad.a[kk][p] = AOFF + (ra >> 3) * 1024 + c * 128 + (ra & 7) * 16;
       else
         ad.a[kk][p] = AOFF + ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
       ad.b[kk][p] = BOFF + rb * I::ROWB + ((c ^ I::swz(rb)) << 4);
@@ -388,8 +397,9 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 }
 
 // C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over the K stages s0 .. s0+nk-1 (k in [s0*BK, (s0+nk)*BK),
-// clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK. ACH: A
-// is in the chunked layout (B never is). BIAS: A's rows are vocabulary rows and every accumulator starts at its
+// clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK. Either
+// operand may be row-major or K-blocked; A may instead be in the tile-blocked piece layout (Operand::cm), which
+// needs APC (its LDS image is in piece order). BIAS: A's rows are vocabulary rows and every accumulator starts at its
 // row's bias, masked to -inf for rows >= Vreal (btile: this thread's bias value from tile_bias; bslot: 1 KiB of
 // LDS outside the operand ring), so the epilogue reads the biased, masked logits straight from the accumulators.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
@@ -400,7 +410,7 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool ACH = false, bool BIAS = false>
+template <bool KF, bool BIAS = false, bool APC = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
                                           int64_t Vreal = 0) {
@@ -417,9 +427,9 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   }
 
-  const Stream sa = ACH ? make_stream_chunked(A, m0, wave, lane) : make_stream(A, m0, wave, lane);
+  const Stream sa = make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
-  const FragAddr ad = make_frag_addr<ACH>(wm, wn, lane);
+  const FragAddr ad = make_frag_addr<APC>(wm, wn, lane);
   const int send = s0 + nk;
   // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
   issue_stage(sa, s0, send, lds, AOFF, wave);
@@ -475,10 +485,12 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group,
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// two floats -> two bf16 (round to nearest even) in one 32-bit word, lo in the low half (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  const uint16_t a = __builtin_bit_cast(uint16_t, (__bf16)lo);
-  const uint16_t b = __builtin_bit_cast(uint16_t, (__bf16)hi);
-  return (uint32_t)a | ((uint32_t)b << 16);
+  const f32x2 v{lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 
@@ -501,8 +513,8 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
   const float btile = tile_bias(bias, v0, V);
   f32x16 acc[4][4];
   // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
-  gemm_tile<KF, false, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
-                             reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+  gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+                      reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
 
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
 #pragma unroll
@@ -730,177 +742,210 @@ __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Per-row inputs of the logits-grad tiles: the target of row n as an int32 id (-1 when y_n is outside
+// [0, V_real): no one-hot term) and the value of G at the target, go*(wgt*exp(x_y - lse) + c) with c = ycoef[n]
+// when given, else -wgt (computed in fp32 from the row's target logit xy, before any rounding).
+__global__ __launch_bounds__(256) void k_target_fix(const int64_t* __restrict__ y, const float* __restrict__ xy,
+                                                    const float* __restrict__ lse_rows,
+                                                    const float* __restrict__ wgt_rows,
+                                                    const float* __restrict__ ycoef, const float* __restrict__ go,
+                                                    int64_t N, int64_t Vreal, int* __restrict__ ty,
+                                                    float* __restrict__ tval) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const int64_t yn = y[n];
+  const bool ok = yn >= 0 && yn < Vreal;
+  const float gs = go != nullptr ? go[0] : 1.f;
+  ty[n] = ok ? (int)yn : -1;
+  tval[n] = ok ? gs * (wgt_rows[n] * expf(xy[n] - lse_rows[n]) + (ycoef != nullptr ? ycoef[n] : -wgt_rows[n])) : 0.f;
+}
+
 // Logits-grad tile: recompute S^T for the tile and form G = go*(wgt*exp(x - lse) + c*[v = y]) rounded to bf16,
 // with c = ycoef[n] when given (the (lse, x_y) gradient of chunk_ce: wgt = g_lse, c = g_ly, go = 1 when null)
-// and c = -wgt otherwise (cross-entropy and the mixture: go*wgt*(softmax - onehot)), written to both K-blocked
-// layouts:
-//   G   element (n, v) at G[(v/256)*Np*256 + n*256 + v%256]    (for dH, reduction over v)
-//   Gt  element (v, n) at Gt[(n/256)*Vp*256 + ((v/16)*8 + (n%256)/32)*512 + (v%16)*32 + n%32]   (for dW,
-//       reduction over n; the chunked layout of Operand::chunked)
-// Each tile is one contiguous 128 KiB block of either buffer. The tile is staged in LDS as [256 n][256 v]
-// (byte (n, v) at n*512 + ((2v) ^ (gsw(n) << 4))):
-//   1. every lane writes go*wgt*exp(x - lse) for its 256 logits (8-byte writes);
-//   2. one thread per row overwrites the target element with go*(wgt*exp(x_y - lse) + c), from the row's
-//      target logit (so the one-hot term is applied in fp32 before rounding, without searching registers),
-//      and, with a sparse bias, the row's candidate elements with their fix-up values (k_sparse_rows);
-//   3. G rows are copied out with ds_read_b128 (non-temporal stores: G is read back by another kernel, not
-//      by this one), and the same pass sums the bf16 G values of each column over
-//      the tile's rows (dBias partials, as the reference's dBias is the column sum of its bf16 G);
-//   4. Gt rows are assembled with ds_read_b64_tr_b16 (each 16-lane group turns a 4x16 [n][v] block into 16
-//      columns of 4 n).
-// gsw makes both read passes bank-conflict free and leaves the staging writes at most 2-way conflicted.
-__device__ __forceinline__ int gsw(int n) { return ((n & 3) << 1) | ((n >> 2) & 1); }
+// and c = -wgt otherwise (cross-entropy and the mixture: go*wgt*(softmax - onehot)), written to two buffers in
+// the tile-blocked piece layout (Operand::cm), so each tile is one contiguous 128 KiB block of either:
+//   G   [M = n][K = v]  (for dH, reduction over v): block (tm*Np/256 + tn), element (n, v) in piece
+//       (n%256/8, v%256/8)
+//   Gt  [M = v][K = n]  (for dW, reduction over n): block (tn*Vp/256 + tm), element (v, n) in piece
+//       (v%256/8, n%256/8)
+// Both are written from registers; the epilogue uses no LDS and no barrier. For each 32 x 32 block (mi, nj) of a
+// wave's accumulators a lane holds one row n (lane%32) and the 16 vocabulary rows 8q + 4(lane/32) + e (q, e =
+// 0..3), i.e. four runs of 4 consecutive v:
+//   * each run is an 8-byte store into G, and the 64 lanes of one store instruction fill four whole 128-byte
+//     pieces (32 rows n x 16 bytes of one 8-wide v chunk);
+//   * the block's bf16 values then go through two v_mfma_f32_32x32x16_bf16 as the A operand (rows n) against
+//     0/1 B operands (transpose_selectors) that send each (lane half, register) slot to its column v; the result
+//     has lane j holding column v = j and the rows n = 8q + 4(lane/32) + e: the transpose, exact because every
+//     product is x*1 or x*0 summed in fp32 (a non-finite G value would spread along its row of the block; G is
+//     finite for finite inputs). Each run of 4 n is again an 8-byte store, four whole pieces per instruction,
+//     into Gt;
+//   * the transposed block also gives the dBias column sums of the bf16 G values (the reference's dBias is the
+//     column sum of its bf16 G) over the wave's 128 rows n: one partial row per (row tile, wave column),
+//     dbias_part[(2*tn + wn)*Vp + v].
+// The target element takes its fp32 value from k_target_fix and, with a sparse bias, the row's candidate
+// elements take their fix-up values (k_sparse_rows); both are register selects. Rows past N use lse = +inf and
+// masked vocabulary rows have x = -inf, so every padding element is exactly zero.
 
-constexpr int GRAD_LDS_BYTES = LDS_BYTES + 4 * 32 * 8 * 4 + BM * 4;  // tile + [4][32][8] dBias sums + bias slot
+// B operands of the register transpose (lane l holds B[8(l/32) + t][l%32], t = 0..7): with A column
+// k = 8h + 4q + e holding (lane half h, run q, element e) of the runs 0-1 (A1) or 2-3 (A2), B1 has a one at
+// (k, 8q + 4h + e) and B2 at (k, 16 + 8q + 4h + e), so A1*B1 + A2*B2 puts vocabulary row 8q' + 4h + e of the
+// block (q' = 0..3) into output column 8q' + 4h + e.
+__device__ __forceinline__ void transpose_selectors(bf16x8& b1, bf16x8& b2, int lane) {
+  const int j = lane & 31, jj = j & 15;
+  const int t = 4 * (jj >> 3) + (jj & 3);
+  const bool mine = ((jj >> 2) & 1) == (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    b1[i] = (__bf16)((mine && j < 16 && i == t) ? 1.f : 0.f);
+    b2[i] = (__bf16)((mine && j >= 16 && i == t) ? 1.f : 0.f);
+  }
+}
+
+__device__ __forceinline__ void store_b128_nt(uint16_t* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+constexpr int GRAD_LDS_BYTES = LDS_BYTES + BM * 4;  // operand ring + bias slot
 
 template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
-void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int64_t* __restrict__ y,
-                const float* __restrict__ lse_rows, const float* __restrict__ wgt_rows, const float* __restrict__ xy,
-                const int* __restrict__ fix_col, const float* __restrict__ fix_val, int nfix,
-                const float* __restrict__ ycoef, const float* __restrict__ go, int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal,
-                int tiles_v, int tiles_n, uint16_t* __restrict__ G, uint16_t* __restrict__ Gt,
-                float* __restrict__ dbias_part) {
+void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int* __restrict__ ty,
+                const float* __restrict__ tval, const float* __restrict__ lse_rows,
+                const float* __restrict__ wgt_rows, const int* __restrict__ fix_col,
+                const float* __restrict__ fix_val, int nfix, const float* __restrict__ go, int64_t N, int64_t Np,
+                int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n, uint16_t* __restrict__ G,
+                uint16_t* __restrict__ Gt, float* __restrict__ dbias_part) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, 8, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  // everything the epilogue needs from memory is loaded before the mainloop
+  const int64_t vw = v0 + wm * 128;  // first vocabulary row of this wave
+  // everything the epilogue needs from memory is loaded before the mainloop: per row n of the lane (one per nj)
+  // go*wgt, lse, the target's local index (-1: none) and the target's G value
   const float btile = tile_bias(bias, v0, V);
   const float gscale = go != nullptr ? go[0] : 1.f;
-  float cn[4], lb[4];
+  float cn[4], lb[4], fv[4];
+  int yl[4];
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
     const bool ok = n < N;
     cn[nj] = ok ? gscale * wgt_rows[n] : 0.f;
     lb[nj] = ok ? lse_rows[n] * LOG2E : INFINITY;  // rows past N: exp2(-inf) = 0 whatever the logit
+    yl[nj] = ok ? ty[n] : -1;
+    fv[nj] = ok ? tval[n] : 0.f;
   }
-  const int64_t nf = n0 + t;  // the row this thread fixes up in step 2
-  const int64_t yf = nf < N ? y[nf] : -1;
-  const bool fix = yf >= v0 && yf < v0 + BM && yf < Vreal;
-  const float fval =
-      fix ? gscale * (wgt_rows[nf] * expf(xy[nf] - lse_rows[nf]) + (ycoef != nullptr ? ycoef[nf] : -wgt_rows[nf]))
-          : 0.f;
 
   f32x16 acc[4][4];
   // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
-  gemm_tile<KF, false, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
-                             reinterpret_cast<float*>(lds + LDS_BYTES + 4 * 32 * 8 * 4), Vreal);
-  // sparse fix-ups of row nf (nfix > 0 only with a sparse bias; the loads overlap the staging below)
-  int scol[MAX_KC];
-  float sval[MAX_KC];
-  if (nfix > 0) {
-#pragma unroll
-    for (int f = 0; f < MAX_KC; ++f) {
-      const bool ok = f < nfix && nf < N;
-      scol[f] = ok ? fix_col[nf * MAX_KC + f] : -1;
-      sval[f] = ok ? fix_val[nf * MAX_KC + f] : 0.f;
-    }
-  }
-  // 1. stage go*wgt*exp(x - lse) as bf16: lane holds 4 consecutive v (r%4) of one row n -> 8-byte LDS writes
+  gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+                      reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+  // element (mi, r) of a block is vocabulary row vw + mi*32 + 8*(r/4) + 4*lh + r%4: the local index
+  // mi*32 + 8*(r/4) + r%4 is compared with (v - vw - 4*lh), which never matches when v belongs to the other half
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
-    const int nl = wn * 128 + nj * 32 + lr;
-    char* row = lds + nl * 512;
-    const int sw = gsw(nl) << 4;
+    const int64_t d = (int64_t)yl[nj] - vw - 4 * lh;
+    yl[nj] = (yl[nj] >= 0 && d >= 0 && d < 128) ? (int)d : -1;
+  }
+  bf16x8 b1, b2;
+  transpose_selectors(b1, b2, lane);
+  // this tile's 128 KiB blocks of G and Gt: element (row m, chunk c, e) at ((m/8)*32 + c)*64 + (m%8)*8 + e
+  uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
+  uint16_t* tblk = Gt + ((int64_t)tn * (Vp / BM) + tm) * CM_TILE;
+  float db[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+  for (int nj = 0; nj < 4; ++nj) {
+    const int64_t nb = n0 + wn * 128 + nj * 32;  // first row n of the block
+    // sparse fix-ups of row nb + lr (nfix > 0 only with a sparse bias), as local indices like yl
+    int scol[MAX_KC];
+    float sval[MAX_KC];
+    if (nfix > 0) {
+      const int64_t n = nb + lr;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float g4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          g4[e] = cn[nj] * __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][4 * q + e], LOG2E, -lb[nj]));
-        const int vl = wm * 128 + acc_row(mi, 4 * q, lh);
-        u32x2 pk;
-        pk[0] = pack_bf16x2(g4[0], g4[1]);
-        pk[1] = pack_bf16x2(g4[2], g4[3]);
-        *reinterpret_cast<u32x2*>(row + ((vl * 2) ^ sw)) = pk;
+      for (int f = 0; f < MAX_KC; ++f) {
+        const bool ok = f < nfix && n < N;
+        const int c = ok ? fix_col[n * MAX_KC + f] : -1;
+        const int64_t d = (int64_t)c - vw - 4 * lh;
+        scol[f] = (c >= 0 && d >= 0 && d < 128) ? (int)d : -1;
+        sval[f] = ok ? fix_val[n * MAX_KC + f] : 0.f;
       }
-  }
-  __syncthreads();
-  // 2. one-hot term of row t
-  if (fix) {
-    const int vl = (int)(yf - v0);
-    *reinterpret_cast<__bf16*>(lds + t * 512 + ((vl * 2) ^ (gsw(t) << 4))) = (__bf16)fval;
-  }
-  if (nfix > 0) {
-#pragma unroll
-    for (int f = 0; f < MAX_KC; ++f) {
-      const int64_t vl = (int64_t)scol[f] - v0;
-      if (scol[f] >= 0 && vl >= 0 && vl < BM)
-        *reinterpret_cast<__bf16*>(lds + t * 512 + ((int)(vl * 2) ^ (gsw(t) << 4))) = (__bf16)sval[f];
     }
-  }
-  __syncthreads();
-  // 3. G block of this tile ([256 n][256 v], contiguous): thread t copies 16-byte chunks t, t+256, ...; its
-  //    chunk column c = t % 32 is fixed, so it also sums the 8 columns of that chunk over its 32 rows
-  char* gblk = reinterpret_cast<char*>(G + ((int64_t)tm * Np + n0) * BLK);
-  float db[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-  for (int i = 0; i < 32; ++i) {
-    const int id = i * 256 + t;
-    const int nl = id >> 5, c = id & 31;
-    const u32x4 val = *reinterpret_cast<const u32x4*>(lds + nl * 512 + ((c ^ gsw(nl)) << 4));
-    __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(gblk + (int64_t)id * 16));
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      db[2 * e] += __uint_as_float(val[e] << 16);
-      db[2 * e + 1] += __uint_as_float(val[e] & 0xFFFF0000u);
+    for (int mi = 0; mi < 4; ++mi) {
+      float g[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        g[r] = cn[nj] * __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -lb[nj]));
+      // the selects run only when some lane of the wave has its target (or a candidate) in this block
+      if (__builtin_amdgcn_ballot_w64((yl[nj] >> 5) == mi) != 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = mi * 32 + 8 * (r >> 2) + (r & 3);
+          g[r] = c == yl[nj] ? fv[nj] : g[r];
+        }
+      }
+      if (nfix > 0) {
+#pragma unroll
+        for (int f = 0; f < MAX_KC; ++f)
+          if (__builtin_amdgcn_ballot_w64((scol[f] >> 5) == mi) != 0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int c = mi * 32 + 8 * (r >> 2) + (r & 3);
+              g[r] = c == scol[f] ? sval[f] : g[r];
+            }
+          }
+      }
+      uint32_t pk[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pk[i] = pack_bf16x2(g[2 * i], g[2 * i + 1]);
+      // G: registers r of row n = nb + lr hold v = vw + mi*32 + 8(r/4) + 4lh + r%4, stored at kperm position
+      // mi*32 + 16lh + r: chunks wm*16 + mi*4 + 2lh + s (s = 0, 1) of the block, 16 bytes each
+      const int nl = wn * 128 + nj * 32 + lr, vl = wm * 128 + mi * 32 + lr;
+#pragma unroll
+      for (int sc = 0; sc < 2; ++sc)
+        store_b128_nt(gblk + ((nl >> 3) * 32 + wm * 16 + mi * 4 + 2 * lh + sc) * 64 + (nl & 7) * 8,
+                      u32x4{pk[4 * sc], pk[4 * sc + 1], pk[4 * sc + 2], pk[4 * sc + 3]});
+      // transpose: lane lr now holds column v = vw + mi*32 + lr, rows n = nb + 8q + 4lh + 0..3
+      const u32x4 a1{pk[0], pk[1], pk[2], pk[3]}, a2{pk[4], pk[5], pk[6], pk[7]};
+      f32x16 tr = {};
+      tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), b1, tr, 0, 0, 0);
+      tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a2), b2, tr, 0, 0, 0);
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += tr[r];
+      db[mi] += s;
+      // Gt: register r of row v = vw + mi*32 + lr holds n = nb + 8(r/4) + 4lh + r%4, kperm position
+      // nj*32 + 16lh + r: chunks wn*16 + nj*4 + 2lh + s of the block
+#pragma unroll
+      for (int sc = 0; sc < 2; ++sc)
+        store_b128_nt(tblk + ((vl >> 3) * 32 + wn * 16 + nj * 4 + 2 * lh + sc) * 64 + (vl & 7) * 8,
+                      u32x4{pack_bf16x2(tr[8 * sc], tr[8 * sc + 1]), pack_bf16x2(tr[8 * sc + 2], tr[8 * sc + 3]),
+                            pack_bf16x2(tr[8 * sc + 4], tr[8 * sc + 5]), pack_bf16x2(tr[8 * sc + 6], tr[8 * sc + 7])});
     }
-  }
-  float* dbs = reinterpret_cast<float*>(lds + LDS_BYTES);  // [4 waves][32 chunks][8]
-#pragma unroll
-  for (int e = 0; e < 8; ++e) db[e] += __shfl_xor(db[e], 32);
-  if (lane < 32) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) dbs[(wave * 32 + lane) * 8 + e] = db[e];
-  }
-  // 4. Gt block of this tile (256 v x 256 n, contiguous, in 1 KiB [16 v][32 n] pieces). Task id -> (16 v from
-  //    v16, 8 n from n8); 16-lane group gi handles tasks gi, gi+16, ...; lane p of the group ends with (v16 + p,
-  //    n8 .. n8+7), and the four groups of a wave hold one whole piece, so every store instruction is contiguous.
-  char* gtblk = reinterpret_cast<char*>(Gt + ((int64_t)tn * Vp + v0) * BLK);
-  const int gi = t >> 4, p = t & 15;
-#pragma unroll 4
-  for (int i = 0; i < 32; ++i) {
-    const int id = i * 16 + gi;
-    const int n8 = (id & 31) * 8, v16 = (id >> 5) * 16;
-    bf16x4 h[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int nl = n8 + 4 * q + (p >> 2);
-      const int vl = v16 + 4 * (p & 3);
-      h[q] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-          (bf16x4 LDS_AS*)(lds + nl * 512 + ((vl * 2) ^ (gsw(nl) << 4))));
-    }
-    const bf16x8 o{h[0][0], h[0][1], h[0][2], h[0][3], h[1][0], h[1][1], h[1][2], h[1][3]};
-    // chunked layout: piece (v16/16, n8/32) is [16 v][32 n]; the wave's four groups fill one piece (1 KiB)
-    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o),
-                                reinterpret_cast<u32x4*>(gtblk + (int64_t)((v16 >> 4) * 8 + (n8 >> 5)) * 1024 +
-                                                         p * 64 + (n8 & 31) * 2));
   }
   if (dbias_part != nullptr) {
-    __syncthreads();
-    const int c = t >> 3, e = t & 7;  // column v0 + t = chunk c, element e
-    dbias_part[(int64_t)tn * Vp + v0 + t] =
-        dbs[(0 * 32 + c) * 8 + e] + dbs[(1 * 32 + c) * 8 + e] + dbs[(2 * 32 + c) * 8 + e] + dbs[(3 * 32 + c) * 8 + e];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) db[mi] += __shfl_xor(db[mi], 32);
+    if (lh == 0) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) dbias_part[(int64_t)(2 * tn + wn) * Vp + vw + mi * 32 + lr] = db[mi];
+    }
   }
 }
 
-// dBias[v] = sum over the tiles_n row-tile partials of column v. A block covers 64 columns with four threads per
-// column, each summing every fourth partial; the four sums are added in a fixed order, so the result is
-// deterministic.
-__global__ __launch_bounds__(256) void k_dbias_reduce(const float* __restrict__ part, int tiles_n, int64_t ldp,
+// dBias[v] = sum over the `rows` partial rows of column v (two per row tile: one per wave column). A block
+// covers 64 columns with four threads per column, each summing every fourth partial; the four sums are added in
+// a fixed order, so the result is deterministic.
+__global__ __launch_bounds__(256) void k_dbias_reduce(const float* __restrict__ part, int rows, int64_t ldp,
                                                       int64_t V, float* __restrict__ dbias) {
   __shared__ float red[4][64];
   const int c = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t v = (int64_t)blockIdx.x * 64 + c;
   float s = 0.f;
   if (v < V)
-    for (int i = g; i < tiles_n; i += 4) s += part[(int64_t)i * ldp + v];
+    for (int i = g; i < rows; i += 4) s += part[(int64_t)i * ldp + v];
   red[g][c] = s;
   __syncthreads();
   if (g == 0 && v < V) dbias[v] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
@@ -913,8 +958,10 @@ __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, co
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// K-blocked transpose: dst element (c, r) at dst[(r/256)*C*256 + c*256 + r%256] = src[r*ld + c] for r < R,
-// 0 for R <= r < (grid rows); c < C (C % 8 == 0). One workgroup per 64 x 64 tile, staged through LDS.
+// K-blocked transpose: dst element (c, r) at dst[(r/256)*C*256 + c*256 + kperm(r%256)] = src[r*ld + c] for r < R,
+// 0 for R <= r < (grid rows); c < C (C % 8 == 0). One workgroup per 64 x 64 tile, staged through LDS. The
+// reduction index r is stored in the permuted order kperm that G and Gt use (their 16-byte stores), so the
+// products of the dH and dW contractions pair up.
 __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __restrict__ src, int64_t ld, int64_t R,
                                                            int64_t C, uint16_t* __restrict__ dst) {
   __shared__ uint16_t tile[64][66];
@@ -937,9 +984,10 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
     const int cl = id & 63, rq = id >> 6;
     const int64_t c = c0 + cl;
     if (c < C) {
+      // output positions r0 + 8rq .. +7 (kperm order) hold the rows kperm_inv(8rq + e)
       u16x8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = tile[rq * 8 + e][cl];
+      for (int e = 0; e < 8; ++e) v[e] = tile[kperm_inv(rq * 8 + e)][cl];
       const int64_t r = r0 + rq * 8;
       *reinterpret_cast<u16x8*>(dst + (r >> 8) * C * BLK + c * BLK + (r & (BLK - 1))) = v;
     }
@@ -952,7 +1000,7 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16, bool KF, bool ACH>
+template <bool OUT_BF16, bool KF, bool APC>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part) {
@@ -973,7 +1021,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   tile_of(lin, tiles_m, tiles_n, group, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile<KF, ACH>(A, B, s0, nk, m0, n0, lds, acc);
+  gemm_tile<KF, false, APC>(A, B, s0, nk, m0, n0, lds, acc);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   if (slot >= 0) {
@@ -1057,15 +1105,17 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
 }
 
 // Backward workspace (Np = N and Vp = V rounded up to 256):
-//   G   [Vp/256][Np][256] bf16, Gt [Np/256][Vp/16][8][16][32] bf16 (chunked; written by k_bwd_grad)
+//   G   [Vp/256][Np/256][32][32][8][8] bf16, Gt [Np/256][Vp/256][32][32][8][8] bf16 (tile-blocked pieces;
+//       written by k_bwd_grad)
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
-//   dbias_part [Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split tails)
+//   dbias_part [2*Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split
+//   tails), ty int32 / tval fp32 [Np] (k_target_fix)
 //   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), fix_col int32 / fix_val fp32 [Np][MAX_KC]
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
   uint16_t *G, *Gt, *Wt, *Ht;
-  float *dbias_part, *xy, *part, *xc, *fix_val;
-  int* fix_col;
+  float *dbias_part, *xy, *part, *xc, *fix_val, *tval;
+  int *fix_col, *ty;
   int64_t np, vp;
   size_t bytes;
 };
@@ -1078,8 +1128,11 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.Gt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * w.np);
   w.Wt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * K);
   w.Ht = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.np * K);
-  w.dbias_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.vp * (w.np / BLK));
+  w.dbias_part = reinterpret_cast<float*>(base + off);
+  off = align256(off + sizeof(float) * w.vp * (2 * w.np / BLK));
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
+  w.ty = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * w.np);
+  w.tval = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
   w.part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * TAIL_SLOTS * BM * BN);
   w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
   w.fix_col = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * w.np * MAX_KC);
@@ -1122,7 +1175,8 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (full == T) P = 1;
   const bool kf = A.kext % BK == 0 && B.kext % BK == 0;
   const dim3 grid(full + (T - full) * P);
-  if (A.chunked) {
+  if (B.cm) return MCE_EINVAL;  // only the A operand may be in the piece layout
+  if (A.cm) {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
                          tiles_n, group, full, P, C, ldc, part);
@@ -1234,22 +1288,25 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
                      kc, N, K, V_real, w.xy, w.xc);
   if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_target_fix, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, y, w.xy, lse_rows, wgt_rows, ycoef,
+                     go, N, V_real, w.ty, w.tval);
+  if ((rc = launch_status())) return rc;
   if (kc > 0) {
     hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, y, cand, cval, kc, w.xy, w.xc,
                        lse_rows, wgt_rows, go, N, V_real, w.fix_col, w.fix_val, dCval);
     if ((rc = launch_status())) return rc;
   }
   if (K % BK == 0)
-    hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows,
-                       w.xy, w.fix_col, w.fix_val, kc, ycoef, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+    hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
+                       lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
                        dBias ? w.dbias_part : nullptr);
   else
-    hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, y, lse_rows, wgt_rows,
-                       w.xy, w.fix_col, w.fix_val, kc, ycoef, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+    hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
+                       lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
                        dBias ? w.dbias_part : nullptr);
   if ((rc = launch_status())) return rc;
   if (dBias) {
-    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, tn, w.vp, V,
+    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, 2 * tn, w.vp, V,
                        dBias);
     if ((rc = launch_status())) return rc;
   }
@@ -1359,7 +1416,7 @@ int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_
                      ldw, V, K, w.Wt);
   if ((rc = launch_status())) return rc;
   // dH[n, k] = sum_v G(n, v) Wt(k, v); G's and Wt's columns V..Vp-1 are zero
-  const Operand Aop{w.G, BLK, N, w.vp, w.np * BLK};
+  const Operand Aop{w.G, 0, N, w.vp, w.np * BLK, 1};
   const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
   const int nk = (int)(w.vp / BK);
   return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st)
@@ -1383,10 +1440,11 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
   hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, H,
                      ldh, N, K, w.Ht);
   if ((rc = launch_status())) return rc;
-  // dW[v, k] = sum_n Gt(v, n) Ht(k, n), reduction over n < N
-  const Operand Aop{w.Gt, BLK, V, N, w.vp * BLK, 1};
-  const Operand Bop{w.Ht, BLK, K, N, K * BLK, 0};
-  return launch_gemm<false>(Aop, Bop, (int)cdiv(N, BK), V, K, 4, dW, lddw, w.part, st);
+  // dW[v, k] = sum_n Gt(v, n) Ht(k, n), reduction over the padded n < Np: the kperm order moves indices across
+  // 32-wide groups' halves, and Gt's and Ht's columns N..Np-1 are zero
+  const Operand Aop{w.Gt, 0, V, w.np, w.vp * BLK, 1};
+  const Operand Bop{w.Ht, BLK, K, w.np, K * BLK, 0};
+  return launch_gemm<false>(Aop, Bop, (int)(w.np / BK), V, K, 4, dW, lddw, w.part, st);
 }
 
 int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
