@@ -621,7 +621,25 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
   const int64_t n = (int64_t)blockIdx.x * 32 + r;
   float m = -INFINITY, s = 0.f;
   if (n < N) {
-    for (int tb = sl; tb < T; tb += 8) {
+    int tb = sl;
+    // four partials per step (independent loads), folded into (m, s) against their common maximum; a partial
+    // with max -inf has sum 0 and contributes 0 * exp(-inf) = 0
+    for (; tb + 24 < T; tb += 32) {
+      float mm[4], ss[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        mm[q] = part_m[(int64_t)(tb + 8 * q) * N + n];
+        ss[q] = part_s[(int64_t)(tb + 8 * q) * N + n];
+      }
+      const float M4 = fmaxf(fmaxf(m, fmaxf(mm[0], mm[1])), fmaxf(mm[2], mm[3]));
+      if (M4 == -INFINITY) continue;
+      float acc = m == -INFINITY ? 0.f : s * expf(m - M4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc += ss[q] * expf(mm[q] - M4);
+      s = acc;
+      m = M4;
+    }
+    for (; tb < T; tb += 8) {
       const float mm = part_m[(int64_t)tb * N + n];
       if (mm == -INFINITY) continue;
       const float ss = part_s[(int64_t)tb * N + n];
@@ -935,20 +953,36 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   }
 }
 
-// dBias[v] = sum over the `rows` partial rows of column v (two per row tile: one per wave column). A block
-// covers 64 columns with four threads per column, each summing every fourth partial; the four sums are added in
-// a fixed order, so the result is deterministic.
+// dBias[v] = sum over the `rows` partial rows of column v (two per row tile: one per wave column; ldp, the row
+// stride, is a multiple of 64). A block covers 64 columns: thread t sums columns 4*(t%16) .. +3 over the rows
+// t/16, t/16 + 16, ... with 16-byte loads, and the 16 row-group sums are added in a fixed order, so the result is
+// deterministic.
 __global__ __launch_bounds__(256) void k_dbias_reduce(const float* __restrict__ part, int rows, int64_t ldp,
                                                       int64_t V, float* __restrict__ dbias) {
-  __shared__ float red[4][64];
-  const int c = threadIdx.x & 63, g = threadIdx.x >> 6;
-  const int64_t v = (int64_t)blockIdx.x * 64 + c;
-  float s = 0.f;
-  if (v < V)
-    for (int i = g; i < rows; i += 4) s += part[(int64_t)i * ldp + v];
-  red[g][c] = s;
+  __shared__ float4 red[16][16];
+  const int c4 = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int64_t v = (int64_t)blockIdx.x * 64 + c4 * 4;
+  float4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int i = g; i < rows; i += 16) {
+    const float4 x = *reinterpret_cast<const float4*>(part + (int64_t)i * ldp + v);
+    s.x += x.x;
+    s.y += x.y;
+    s.z += x.z;
+    s.w += x.w;
+  }
+  red[g][c4] = s;
   __syncthreads();
-  if (g == 0 && v < V) dbias[v] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+  if (threadIdx.x < 64) {
+    const int cc = threadIdx.x >> 2, e = threadIdx.x & 3;
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4 x = red[i][cc];
+      tot += e == 0 ? x.x : e == 1 ? x.y : e == 2 ? x.z : x.w;
+    }
+    const int64_t vo = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (vo < V) dbias[vo] = tot;
+  }
 }
 
 __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, const float* __restrict__ go, int64_t N,
@@ -1054,7 +1088,8 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   }
 }
 
-// Sum of the P K-slices of each split tail tile into C (fixed order p = 0..P-1). Block (row block of 16, tile r).
+// Sum of the P K-slices of each split tail tile into C (fixed order p = 0..P-1). Block (group of 4 rows, tile r);
+// thread t sums columns 4*(t%64) .. +3 of row 4*blockIdx.x + t/64 with 16-byte loads.
 template <bool OUT_BF16>
 __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ part, int P, int full, int tiles_m,
                                                      int tiles_n, int group, int64_t M, int64_t Nc,
@@ -1062,17 +1097,26 @@ __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ p
   const int r = (int)blockIdx.y;
   int tm, tn;
   tile_of(full + r, tiles_m, tiles_n, group, tm, tn);
-  const int jl = threadIdx.x;
-#pragma unroll 4
-  for (int il = (int)blockIdx.x * 16; il < (int)blockIdx.x * 16 + 16; ++il) {
-    float s = 0.f;
-    for (int p = 0; p < P; ++p) s += part[((int64_t)(r * P + p) * BM + il) * BN + jl];
-    const int64_t i = (int64_t)tm * BM + il, j = (int64_t)tn * BN + jl;
-    if (i < M && j < Nc) {
+  const int il = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6), jl = ((int)threadIdx.x & 63) * 4;
+  float4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < P; ++p) {
+    const float4 v = *reinterpret_cast<const float4*>(part + ((int64_t)(r * P + p) * BM + il) * BN + jl);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  const int64_t i = (int64_t)tm * BM + il;
+  if (i >= M) return;
+  const float o[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t j = (int64_t)tn * BN + jl + e;
+    if (j < Nc) {
       if constexpr (OUT_BF16)
-        reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)s;
+        reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)o[e];
       else
-        reinterpret_cast<float*>(C)[i * ldc + j] = s;
+        reinterpret_cast<float*>(C)[i * ldc + j] = o[e];
     }
   }
 }
@@ -1193,7 +1237,7 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   }
   int rc = launch_status();
   if (rc || full == T) return rc;
-  hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 16, T - full), dim3(BN), 0, st, part, P, full, tiles_m,
+  hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 4, T - full), dim3(256), 0, st, part, P, full, tiles_m,
                      tiles_n, group, M, Nc, C, ldc);
   return launch_status();
 }
