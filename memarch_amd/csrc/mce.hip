@@ -158,9 +158,10 @@ struct Stream {
 // Row-major / K-blocked: lane l of load instruction i reads row m = 8i + l/8, logical chunk c = (l%8) ^ swz(m), at
 // m*ld*2 + 16c bytes from the stage's base, and lands at l*16 in the instruction's 1 KiB of the swizzled [256][64]
 // image: the 8 lanes of a row read one 128-byte segment.
-// Tile-blocked pieces (Operand::cm, m0 a multiple of 256): lane l reads row m = 8i + l%8, chunk c = l/8, at
-// (m/8)*4096 + c*128 + (m%8)*16 = 4096i + 16l, so an instruction reads 1 KiB contiguously into the piece-order
-// image (make_frag_addr<true>); a k step inside a 256-wide K block is 16 bytes.
+// Tile-blocked pieces (Operand::cm, m0 a multiple of 256): lane l reads row m = 8i + l%8, chunk
+// c = (l/8) ^ (i & 1), at (m/8)*4096 + c*128 + (m%8)*16, so an instruction reads 1 KiB contiguously (whole
+// 128-byte pieces, swapped in pairs for odd i) into the piece-order image (make_frag_addr<true>); a k step inside
+// a 256-wide K block is 16 bytes.
 __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
   Stream st;
   st.kext = op.kext;
@@ -177,9 +178,9 @@ __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int
   for (int j = 0; j < I::LPW; ++j) {
     const int ins = wave * I::LPW + j;
     const int row = op.cm ? ins * 8 + (lane & 7) : ins * I::RPI + lane / I::CH;
-    const int c = op.cm ? lane >> 3 : (lane % I::CH) ^ I::swz(row);
+    const int c = op.cm ? (lane >> 3) ^ (ins & 1) : (lane % I::CH) ^ I::swz(row);
     const bool in = m0 + row < op.mext;
-    st.voff[j] = op.cm ? ins * 4096 + lane * 16 : (int)(row * op.ld * 2) + c * 16;
+    st.voff[j] = op.cm ? ins * 4096 + c * 128 + (lane & 7) * 16 : (int)(row * op.ld * 2) + c * 16;
     st.kloc[j] = in ? c * 8 : OOB;
     st.vfull[j] = in ? st.voff[j] : OOB;
   }
@@ -228,8 +229,9 @@ __device__ __forceinline__ void issue_stage(const Stream& st, int stage, int sen
 // at a[kk][i&1] + (i>>1)*64 rows: rows 64 apart share the XOR swizzle, so the rest is a compile-time offset,
 // as is the ring buffer (b*OPB). The mainloop then reads with immediates only.
 // APC: the A image is in piece order (an Operand::cm operand): the 16-byte chunk c of row r at
-// (r/8)*1024 + c*128 + (r%8)*16, so the 8 rows of a row group that one 8-lane group reads lie in 128 contiguous
-// bytes (no swizzle needed), and rows 64 apart are again 8 KiB apart.
+// (r/8)*1024 + (c ^ ((r/8) & 1))*128 + (r%8)*16. A ds_read_b128 serves 16 lanes (256 bytes) per cycle: those are
+// 16 consecutive rows at one chunk, i.e. two row groups, whose 128-byte runs the parity swizzle puts 1024 +- 128
+// bytes apart, in different bank halves, so the reads are conflict free; rows 64 apart are again 8 KiB apart.
 struct FragAddr {
   uint32_t a[4][2];  // [kk][i & 1], A image of buffer 0
   uint32_t b[4][2];  // [kk][j & 1], B image of buffer 0
@@ -245,7 +247,7 @@ __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
       const int ra = wm * 128 + p * 32 + (lane & 31);
       const int rb = wn * 128 + p * 32 + (lane & 31);
       if constexpr (APC)
-        ad.a[kk][p] = AOFF + (ra >> 3) * 1024 + c * 128 + (ra & 7) * 16;
+        ad.a[kk][p] = AOFF + (ra >> 3) * 1024 + ((c ^ ((ra >> 3) & 1)) << 7) + (ra & 7) * 16;
       else
         ad.a[kk][p] = AOFF + ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
       ad.b[kk][p] = BOFF + rb * I::ROWB + ((c ^ I::swz(rb)) << 4);
