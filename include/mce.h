@@ -92,10 +92,10 @@ MCE_API int mce_fwd_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, in
                    int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* ws,
                    size_t ws_bytes, void* stream);
 
-/* Workspace bytes needed by the backward entry points for this shape: the bf16 gradient of the logits in two
- * K-blocked layouts (G, v contiguous, and G^T, n contiguous; each N x V rounded up to 256 x 256), the K-blocked
- * transposed copies W^T and H^T, and the dBias partial sums. Replaces the bf16 logits chunk that
- * fused_ops.py:150,134 overwrites with the gradient. */
+/* Workspace bytes needed by the backward entry points for this shape: the bf16 gradient of the logits twice, in
+ * tile-blocked layouts (G with the vocabulary as its reduction index, for dH, and G^T with the rows, for dW; each
+ * N x V rounded up to 256 x 256), the K-blocked transposed copies W^T and H^T, and the dBias partial sums.
+ * Replaces the bf16 logits chunk that fused_ops.py:150,134 overwrites with the gradient. */
 MCE_API size_t mce_bwd_ws_bytes(int64_t N, int64_t K, int64_t V);
 
 /*

@@ -66,7 +66,7 @@ static_assert(LDS_BYTES <= 160 * 1024, "operand ring exceeds the 160 KiB of LDS 
 
 struct Operand {
   const uint16_t* p;  // bf16 bits
-  int64_t ld;         // row stride in elements (256 in the K-blocked layout); chunk-column stride when cm
+  int64_t ld;         // row stride in elements (256 in the K-blocked layout; unused when cm)
   int64_t mext;       // valid extent along M
   int64_t kext;       // valid extent along K
   int64_t blk;        // 0, or the element distance between consecutive 256-wide K blocks
