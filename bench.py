@@ -1,7 +1,7 @@
 """Benchmark of the fused output-projection + cross-entropy + pointer-mixture op (fwd+bwd) on one MI355X.
 
-A step is one forward + backward of `linear_ce_mix_biased` over one batch of the configuration's synthetic
-inputs (default: config 2, N = 32768 tokens, d = 2048, V = 50304 (50257 real), bf16 operands, fp32
+A step is one forward + backward of `linear_ce_mix_biased` (the one-pass training path unless --path recompute)
+over one batch of the configuration's synthetic inputs (default: config 2, N = 32768 tokens, d = 2048, V = 50304 (50257 real), bf16 operands, fp32
 accumulation), with every input resident in HBM before the timed region. Prints one JSON line:
   value         tokens/s of the whole step: N*K / (wall time of K steps between two synchronisations)
   roofline      the dominant kernel of the step: its algorithmic FLOPs per launch (one N x V x d contraction,
@@ -39,11 +39,16 @@ PEAK_HBM = 8.0e12      # MI355X HBM3E, B/s
 METRIC = "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA peak"
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 
-# C-ABI stage -> the kernel that dominates it (the stage also runs small helpers: see stage_times)
-STAGE_OF_CALL = {"mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
-                 "mce_bwd_dweight": "dweight"}
-STAGE_KERNEL = {"fwd": "k_fwd_tiles<true>", "logits_grad": "k_bwd_grad<true>", "dhidden": "k_gemm<true, true, true>",
-                "dweight": "k_gemm<false, true, true>"}
+# C-ABI call -> (stage, the kernel that dominates it); the stages also run small helper kernels. One-pass path
+# (default): mce_fwd_train, mce_bwd_train_dhidden, mce_bwd_train_dweight; recompute path: mce_fwd,
+# mce_bwd_logits_grad, mce_bwd_dhidden, mce_bwd_dweight.
+STAGE_OF_CALL = {"mce_fwd_train": ("fwd", "k_fwd_train<true>"),
+                 "mce_bwd_train_dhidden": ("dhidden", "k_gemm<true, true, true>"),
+                 "mce_bwd_train_dweight": ("dweight", "k_gemm<false, true, true>"),
+                 "mce_fwd": ("fwd", "k_fwd_tiles<true>"),
+                 "mce_bwd_logits_grad": ("logits_grad", "k_bwd_grad<true>"),
+                 "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true>"),
+                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true>")}
 
 
 def _args():
@@ -58,6 +63,11 @@ def _args():
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
     ap.add_argument("--op", choices=("fused_ce", "swiglu"), default="fused_ce",
                     help="fused_ce: the north-star operator (default); swiglu: the SwiGLU gate kernels")
+    ap.add_argument("--path", choices=("one-pass", "recompute"), default="one-pass",
+                    help="one-pass: the logits gradient formed in the forward (default); recompute: the backward "
+                         "recomputes the logits")
+    ap.add_argument("--other-path-steps", type=int, default=3,
+                    help="timed steps of the other path, reported beside the line (0: skip)")
     return ap.parse_args()
 
 
@@ -252,7 +262,18 @@ def main():
         (loss / n).backward()
         return loss
 
-    print("[bench] warmup", file=sys.stderr, flush=True)
+    def time_path(recompute, steps):
+        fused_ops.RECOMPUTE = recompute
+        step()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / steps
+
+    fused_ops.RECOMPUTE = args.path == "recompute"
+    print(f"[bench] warmup ({args.path} path)", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -274,10 +295,12 @@ def main():
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
     _lib.set_call_hook(None)
-    live = {}
+    live, kernel_of = {}, {}
     for (name, ph0, e0), (name1, ph1, e1) in zip(marks[0::2], marks[1::2]):
         assert name == name1 and ph0 == "begin" and ph1 == "end"
-        live.setdefault(STAGE_OF_CALL[name], []).append(e0.elapsed_time(e1))
+        stage, kern = STAGE_OF_CALL[name]
+        live.setdefault(stage, []).append(e0.elapsed_time(e1))
+        kernel_of[stage] = kern
     stages = {k: sum(v) / len(v) for k, v in live.items()}
     tok_s = n / dt
     flops = 6.0 * n * v * d
@@ -287,7 +310,7 @@ def main():
     dom = max(stages, key=stages.get)
     kflops = 2.0 * n * v * d   # every stage's kernel is one N x V x d contraction
     ach = kflops / (stages[dom] * 1e-3)
-    traffic = traffic_bytes(STAGE_KERNEL[dom], cfg.index)
+    traffic = traffic_bytes(kernel_of[dom], cfg.index)
     res = {
         "metric": METRIC,
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -295,13 +318,20 @@ def main():
         "dtype": "bf16", "data": f"synthetic (seeded config {cfg.index} distributions, random-init weights)",
         "config": {"workload": f"config {cfg.index}: fused linear+CE+pointer fwd+bwd, one batch per step",
                    "N": n, "d": d, "V": v, "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
-        "roofline": {"bound": "mfma", "kernel": STAGE_KERNEL[dom], "stage": dom, "achieved": round(ach / 1e12, 2),
+        "roofline": {"bound": "mfma", "kernel": kernel_of[dom], "stage": dom, "achieved": round(ach / 1e12, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16, 4),
                      "flops_per_launch": kflops, "traffic": traffic},
         "op_roofline": {"achieved": round(flops / dt / 1e12, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
     }
+    res["path"] = args.path
+    if args.other_path_steps > 0:
+        other = "recompute" if args.path == "one-pass" else "one-pass"
+        print(f"[bench] {other} path for comparison", file=sys.stderr, flush=True)
+        res["other_path"] = {"path": other,
+                             "ms_per_step": round(time_path(other == "recompute", args.other_path_steps) * 1e3, 3)}
+        fused_ops.RECOMPUTE = args.path == "recompute"
     if args.stage_reps > 0:
         res["isolated_stages_ms"] = {k: round(x, 3) for k, x in isolated.items()}
     if args.cpu_rows > 0:

@@ -166,6 +166,63 @@ MCE_API int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
             int64_t K, int64_t V, int64_t V_real, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
             float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream);
 
+/*
+ * One-pass training path (mixture or plain cross-entropy, no sparse bias). The reference computes its
+ * gradients during the forward (fused_ops.py:148-155); so does this path, without materialising logits and
+ * without a second pass over them:
+ *   mce_fwd_train writes, besides the per-row outputs of mce_fwd, the logits gradient into the workspace as
+ *   E'[n, v] = G[n, v] / (go a_n), a_n = wgt_n exp(e_n - lse_n), where e_n <= lse_n is the logsumexp of the first
+ *   vocabulary tile and the target logit; rows whose logits exceed e_n by too much for the exponent range are
+ *   detected on the device and written exactly by a fallback pass (with a_n = wgt_n). The backward then applies
+ *   go a_n in the epilogue of dH = go a . (E' W), in the row-scaled H^T copy of dW = E'^T (go a . H) and in
+ *   dBias = E'^T (go a).
+ * The workspace (mce_train_ws_bytes) must be kept unchanged between mce_fwd_train and the backward calls.
+ */
+MCE_API size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V);
+
+/*
+ * Forward of the training path. Outputs as mce_fwd (loss_rows, lse_rows, wgt_rows, dgr_rows fp32 [N], loss_sum
+ * fp32 [1]) plus E' and a in ws. Replaces `_LinearCEMix.forward` (fused_ops.py:138-157): the logits GEMM
+ * (fused_ops.py:150) and `_ce_mix_kernel` (fused_ops.py:104-134); gate = hit = NULL replaces
+ * `_LinearCE.forward` (fused_ops.py:44-58) and `_ce_grad_kernel` (fused_ops.py:10-36).
+ */
+MCE_API int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                          const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
+                          int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
+                          float* loss_sum, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * dH = G W of the training path (W^T is written into ws here; `go` is the fp32 upstream gradient on the
+ * device). dH as for mce_bwd_dhidden. Replaces `gh[i] = logits @ wd` (fused_ops.py:153) and the `gh * go` of
+ * `_LinearCEMix.backward` (fused_ops.py:161).
+ */
+MCE_API int mce_bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V,
+                                  void* dH, int dh_bf16, int64_t lddh, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * dW = G^T H (fp32 [V, K], row stride lddw, overwritten; may be NULL) and dBias = sum_n G[n, :] (fp32 [V]; may be
+ * NULL) of the training path (the row-scaled H^T is written into ws here). Replaces `gw += (logits.T @
+ * hc).float()` (fused_ops.py:154) and the `gw * go` of `_LinearCEMix.backward` (fused_ops.py:161); dBias replaces
+ * the bias column of `gw` in the folded layout (full2.py:1842-1851).
+ */
+MCE_API int mce_bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N, int64_t K, int64_t V,
+                                  float* dW, int64_t lddw, float* dBias, void* ws, size_t ws_bytes, void* stream);
+
+/* The training-path backward in one call: dH, dW / dBias, and dGate = go * dgr_rows (each may be NULL). */
+MCE_API int mce_bwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* go,
+                          const float* dgr_rows, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16, int64_t lddh,
+                          float* dW, int64_t lddw, float* dBias, float* dGate, void* ws, size_t ws_bytes,
+                          void* stream);
+
+/* Copies the number of rows the last mce_fwd_train on this workspace wrote by the exact fallback pass into
+ * *out (a device int), on `stream`. No counterpart in the reference (diagnostics and tests). */
+MCE_API int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int* out, void* stream);
+
+/* Test hook: the bound on a row's sum of E over one half tile (128 vocabulary rows) above which the row takes
+ * the exact fallback pass; s_max <= 0 restores the default 2^64. Process-wide; affects later mce_fwd_train
+ * calls. No counterpart in the reference. */
+MCE_API void mce_train_set_threshold(float s_max);
+
 #ifdef __cplusplus
 }
 #endif

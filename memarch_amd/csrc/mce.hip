@@ -30,7 +30,7 @@
 
 #include "../../include/mce.h"
 
-#define MCE_VERSION 320
+#define MCE_VERSION 400
 
 typedef int32_t mce_i32x4 __attribute__((ext_vector_type(4)));
 // The LLVM intrinsic behind `buffer_load_dword... lds`: (resource, LDS base, bytes per lane, per-lane offset,
@@ -825,6 +825,33 @@ __device__ __forceinline__ void store_b128_nt(uint16_t* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// One 32 x 32 block (mi, nj) of a wave's bf16 logits-grad values into both tile-blocked buffers. pk: lane (row
+// n = nb + lr) holds the 16 vocabulary rows vw + mi*32 + 8(r/4) + 4lh + r%4 (r = 0..15, two per word).
+//   G:  those sit at kperm positions mi*32 + 16lh + r: chunks wm*16 + mi*4 + 2lh + s (s = 0, 1) of the block,
+//       16 bytes each;
+//   Gt: the two selector MFMAs transpose the block, so lane lr holds column v = vw + mi*32 + lr and the rows
+//       n = nb + 8(r/4) + 4lh + r%4, at kperm positions nj*32 + 16lh + r: chunks wn*16 + nj*4 + 2lh + s.
+// Returns the transposed block (fp32 copies of the bf16 values) for column sums.
+__device__ __forceinline__ f32x16 store_g_block(uint16_t* gblk, uint16_t* tblk, const uint32_t (&pk)[8],
+                                                const bf16x8& b1, const bf16x8& b2, int wm, int wn, int mi, int nj,
+                                                int lr, int lh) {
+  const int nl = wn * 128 + nj * 32 + lr, vl = wm * 128 + mi * 32 + lr;
+#pragma unroll
+  for (int sc = 0; sc < 2; ++sc)
+    store_b128_nt(gblk + ((nl >> 3) * 32 + wm * 16 + mi * 4 + 2 * lh + sc) * 64 + (nl & 7) * 8,
+                  u32x4{pk[4 * sc], pk[4 * sc + 1], pk[4 * sc + 2], pk[4 * sc + 3]});
+  const u32x4 a1{pk[0], pk[1], pk[2], pk[3]}, a2{pk[4], pk[5], pk[6], pk[7]};
+  f32x16 tr = {};
+  tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), b1, tr, 0, 0, 0);
+  tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a2), b2, tr, 0, 0, 0);
+#pragma unroll
+  for (int sc = 0; sc < 2; ++sc)
+    store_b128_nt(tblk + ((vl >> 3) * 32 + wn * 16 + nj * 4 + 2 * lh + sc) * 64 + (vl & 7) * 8,
+                  u32x4{pack_bf16x2(tr[8 * sc], tr[8 * sc + 1]), pack_bf16x2(tr[8 * sc + 2], tr[8 * sc + 3]),
+                        pack_bf16x2(tr[8 * sc + 4], tr[8 * sc + 5]), pack_bf16x2(tr[8 * sc + 6], tr[8 * sc + 7])});
+  return tr;
+}
+
 constexpr int GRAD_LDS_BYTES = LDS_BYTES + BM * 4;  // operand ring + bias slot
 
 template <bool KF>
@@ -920,29 +947,11 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
       uint32_t pk[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) pk[i] = pack_bf16x2(g[2 * i], g[2 * i + 1]);
-      // G: registers r of row n = nb + lr hold v = vw + mi*32 + 8(r/4) + 4lh + r%4, stored at kperm position
-      // mi*32 + 16lh + r: chunks wm*16 + mi*4 + 2lh + s (s = 0, 1) of the block, 16 bytes each
-      const int nl = wn * 128 + nj * 32 + lr, vl = wm * 128 + mi * 32 + lr;
-#pragma unroll
-      for (int sc = 0; sc < 2; ++sc)
-        store_b128_nt(gblk + ((nl >> 3) * 32 + wm * 16 + mi * 4 + 2 * lh + sc) * 64 + (nl & 7) * 8,
-                      u32x4{pk[4 * sc], pk[4 * sc + 1], pk[4 * sc + 2], pk[4 * sc + 3]});
-      // transpose: lane lr now holds column v = vw + mi*32 + lr, rows n = nb + 8q + 4lh + 0..3
-      const u32x4 a1{pk[0], pk[1], pk[2], pk[3]}, a2{pk[4], pk[5], pk[6], pk[7]};
-      f32x16 tr = {};
-      tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), b1, tr, 0, 0, 0);
-      tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a2), b2, tr, 0, 0, 0);
+      const f32x16 tr = store_g_block(gblk, tblk, pk, b1, b2, wm, wn, mi, nj, lr, lh);
       float s = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s += tr[r];
       db[mi] += s;
-      // Gt: register r of row v = vw + mi*32 + lr holds n = nb + 8(r/4) + 4lh + r%4, kperm position
-      // nj*32 + 16lh + r: chunks wn*16 + nj*4 + 2lh + s of the block
-#pragma unroll
-      for (int sc = 0; sc < 2; ++sc)
-        store_b128_nt(tblk + ((vl >> 3) * 32 + wn * 16 + nj * 4 + 2 * lh + sc) * 64 + (vl & 7) * 8,
-                      u32x4{pack_bf16x2(tr[8 * sc], tr[8 * sc + 1]), pack_bf16x2(tr[8 * sc + 2], tr[8 * sc + 3]),
-                            pack_bf16x2(tr[8 * sc + 4], tr[8 * sc + 5]), pack_bf16x2(tr[8 * sc + 6], tr[8 * sc + 7])});
     }
   }
   if (dbias_part != nullptr) {
@@ -994,12 +1003,285 @@ __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, co
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// One-pass training path. The logits gradient is written once, by the forward tiles, instead of being recomputed
+// by a backward pass over the logits:
+//   G[n, v] = go * wgt_n * (exp(x_v - lse_n) - [v = y_n]) = go * a_n * E'[n, v],
+//   E[n, v] = exp(x_v - e_n),  a_n = wgt_n * exp(e_n - lse_n),  E'[n, y_n] = (exp(x_y - lse_n) - 1) exp(lse_n - e_n)
+// with e_n a lower bound of lse_n that is known before the tiles run: the logsumexp of the first vocabulary tile
+// and of the target logit (k_lse_est). E' (= E except at the target) goes into the G / Gt buffers in the
+// tile-blocked layout; the per-row factor a_n, which needs the final lse, is applied by the backward
+// (dH = go a . (E' W) in the GEMM epilogue, dW = E'^T (go a . H) through a row-scaled H^T copy, dBias = E'^T (go a)).
+// Because e_n <= lse_n, E underflows only where the softmax is below e^-87 anyway. It could overflow only where a
+// logit exceeds e_n by more than ~88: a row whose sum of E over a half tile exceeds the bound s_max (or is not
+// finite) is flagged instead; its partials are then the usual (max, sum of exp(x - max)), so the merged lse is
+// exact, and k_repair rewrites its E' row exactly from a fresh dot-product pass with a_n = wgt_n.
+
+// Largest accepted sum of E over one half tile (128 vocabulary rows): 2^64. With it every stored E' and every
+// sum over V of E' W stays far inside the fp32 / bf16 range. A test hook may lower it (mce_train_set_threshold).
+constexpr float TRAIN_S_MAX = 18446744073709551616.f;
+
+// Element (m, k) of a tile-blocked [Mp][.] operand (Operand::cm) with Mp rows: the index formula of the layout,
+// with the reduction index k in kperm order.
+__device__ __forceinline__ int64_t cm_index(int64_t m, int64_t k, int64_t Mp) {
+  const int kp = kperm((int)(k & 255));
+  return (k >> 8) * 256 * Mp + (m >> 8) * CM_TILE + ((((m & 255) >> 3) * 32 + (kp >> 3)) * 64) + (m & 7) * 8 +
+         (kp & 7);
+}
+__device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xFFFFu); }
+
+// e_n per row from the two half-tile partials of vocabulary tile 0 (part_m / part_s rows 0 and 1) and the target
+// logit when the target lies outside tile 0; also clears the flags and the flagged-row counter.
+__global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_m, const float* __restrict__ part_s,
+                                                 const float* __restrict__ xy, const int64_t* __restrict__ y,
+                                                 int64_t N, int64_t Np, float* __restrict__ lse_est,
+                                                 int* __restrict__ flag, int* __restrict__ flag_count) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n == 0) *flag_count = 0;
+  if (n >= Np) return;
+  flag[n] = 0;
+  if (n >= N) {
+    lse_est[n] = INFINITY;
+    return;
+  }
+  const float m0 = part_m[n], m1 = part_m[N + n];
+  const float m = fmaxf(m0, m1);
+  float l = -INFINITY;
+  if (m != -INFINITY) {
+    float s = 0.f;
+    if (m0 != -INFINITY) s += part_s[n] * expf(m0 - m);
+    if (m1 != -INFINITY) s += part_s[N + n] * expf(m1 - m);
+    l = m + logf(s);
+  }
+  const float x = xy[n];
+  if (y[n] >= BM && x != -INFINITY) {
+    const float mm = fmaxf(l, x);
+    l = mm + logf(expf(l - mm) + expf(x - mm));
+  }
+  lse_est[n] = l;
+}
+
+// Forward tile of the training path: the logits tile as in k_fwd_tiles, then E = exp(x - e_n) for its 256 x 256
+// elements, rounded to bf16 and stored into G and Gt exactly as k_bwd_grad stores G (store_g_block). The
+// half-tile partials are (e_n, sum of E) -- or, for a flagged row, (max, sum of exp(x - max)) -- in the part_m /
+// part_s format k_fwd_merge reads. Rows past N use e = +inf, so their E is exactly zero.
+template <bool KF>
+__global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
+void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const float* __restrict__ lse_est,
+                 int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n, float s_max,
+                 uint16_t* __restrict__ G, uint16_t* __restrict__ Gt, float* __restrict__ part_m,
+                 float* __restrict__ part_s, int* __restrict__ flag) {
+  __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
+  int tm, tn;
+  tile_coords(tiles_v, tiles_n, 8, tm, tn);
+  const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  const float btile = tile_bias(bias, v0, V);
+  float le[4], lb[4];
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) {
+    const int64_t n = n0 + wn * 128 + nj * 32 + lr;
+    le[nj] = n < N ? lse_est[n] : INFINITY;
+    lb[nj] = le[nj] * LOG2E;
+  }
+
+  f32x16 acc[4][4];
+  gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+                      reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+  bf16x8 b1, b2;
+  transpose_selectors(b1, b2, lane);
+  uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
+  uint16_t* tblk = Gt + ((int64_t)tn * (Vp / BM) + tm) * CM_TILE;
+  const int64_t prow = (int64_t)(2 * tm + wm) * N;
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) {
+    float s = 0.f;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      float e[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -lb[nj]));
+        s += e[r];
+      }
+      uint32_t pk[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pk[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
+      (void)store_g_block(gblk, tblk, pk, b1, b2, wm, wn, mi, nj, lr, lh);
+    }
+    s += __shfl_xor(s, 32);
+    const int64_t n = n0 + wn * 128 + nj * 32 + lr;
+    const bool ok = n < N;
+    const bool robust = ok && !(s <= s_max && le[nj] < INFINITY);
+    float mo = le[nj], so = s;
+    if (__builtin_amdgcn_ballot_w64(robust) != 0) {  // rare: the exact partial from the logits themselves
+      float m = -INFINITY;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r]);
+      m = fmaxf(m, __shfl_xor(m, 32));
+      float ss = 0.f;
+      if (m != -INFINITY) {
+        const float mb = m * LOG2E;
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ss += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -mb));
+      }
+      ss += __shfl_xor(ss, 32);
+      if (robust) {
+        mo = m;
+        so = ss;
+      }
+    }
+    if (lh == 0 && ok) {
+      part_m[prow + n] = mo;
+      part_s[prow + n] = so;
+      if (robust) flag[n] = 1;
+    }
+  }
+}
+
+// After the merge: a_n = wgt_n exp(e_n - lse_n), and the target element of E' (both buffers) for unflagged rows;
+// flagged rows get a_n = wgt_n and are appended to flag_list for k_repair. Rows N .. Np-1 get a_n = 0.
+__global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ y, const float* __restrict__ xy,
+                                                    const float* __restrict__ lse_est,
+                                                    const float* __restrict__ lse_rows,
+                                                    const float* __restrict__ wgt_rows, const int* __restrict__ flag,
+                                                    int64_t N, int64_t Np, int64_t Vp, int64_t Vreal,
+                                                    float* __restrict__ arow, int* __restrict__ flag_count,
+                                                    int* __restrict__ flag_list, uint16_t* __restrict__ G,
+                                                    uint16_t* __restrict__ Gt) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= Np) return;
+  if (n >= N) {
+    arow[n] = 0.f;
+    return;
+  }
+  const float w = wgt_rows[n];
+  if (flag[n]) {
+    arow[n] = w;
+    flag_list[atomicAdd(flag_count, 1)] = (int)n;
+    return;
+  }
+  const float e = lse_est[n], l = lse_rows[n];
+  arow[n] = w * expf(e - l);
+  const int64_t yn = y[n];
+  if (yn >= 0 && yn < Vreal) {
+    const uint16_t b = to_bf16((expf(xy[n] - l) - 1.f) * expf(l - e));
+    G[cm_index(n, yn, Np)] = b;
+    Gt[cm_index(yn, n, Vp)] = b;
+  }
+}
+
+// Exact E' rows of the flagged rows (a grid-stride loop over flag_list, one row per workgroup at a time):
+// x_v = b_v + h_n . w_v (fp32 sums of the bf16 products; -inf for v >= V_real) for every v < Vp, then
+// E'[n, v] = exp(x_v - lse_n) - [v = y_n] into G and Gt. h_n is staged in LDS 16384 values at a time; thread t
+// takes v = v0 + t. This is the fallback for rows whose logits exceed e_n by about 44 or more, which the bound
+// from the first vocabulary tile and the target makes rare; it reads all of W once per flagged row.
+constexpr int REPAIR_KC = 16384;
+__global__ __launch_bounds__(256) void k_repair(const uint16_t* __restrict__ H, int64_t ldh,
+                                                const uint16_t* __restrict__ W, int64_t ldw,
+                                                const float* __restrict__ bias, const int64_t* __restrict__ y,
+                                                const float* __restrict__ lse_rows, int64_t K, int64_t V, int64_t Vp,
+                                                int64_t Vreal, int64_t Np, const int* __restrict__ flag_count,
+                                                const int* __restrict__ flag_list, uint16_t* __restrict__ G,
+                                                uint16_t* __restrict__ Gt) {
+  __shared__ __attribute__((aligned(16))) uint16_t hs[REPAIR_KC];
+  const int cnt = *flag_count;
+  const int t = threadIdx.x;
+  const int nkc = (int)((K + REPAIR_KC - 1) / REPAIR_KC);
+  for (int i = blockIdx.x; i < cnt; i += gridDim.x) {
+    const int64_t n = flag_list[i];
+    const float l = lse_rows[n];
+    const int64_t yn = y[n];
+    for (int64_t v0 = 0; v0 < Vp; v0 += 256) {
+      const int64_t v = v0 + t;
+      float x = 0.f;
+      for (int kc = 0; kc < nkc; ++kc) {
+        const int64_t k0 = (int64_t)kc * REPAIR_KC;
+        const int kn = (int)((K - k0) < REPAIR_KC ? (K - k0) : REPAIR_KC);
+        if (v0 == 0 || nkc > 1) {
+          __syncthreads();
+          for (int k = t * 8; k < kn; k += 256 * 8)
+            *reinterpret_cast<u16x8*>(hs + k) = *reinterpret_cast<const u16x8*>(H + n * ldh + k0 + k);
+          __syncthreads();
+        }
+        if (v < V) {
+          const uint16_t* wr = W + v * ldw + k0;
+          for (int k = 0; k < kn; k += 8) {
+            const u16x8 a = *reinterpret_cast<const u16x8*>(hs + k);
+            const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[e]), x);
+          }
+        }
+      }
+      float g = 0.f;
+      if (v < Vreal) g = expf(x + (bias != nullptr ? bias[v] : 0.f) - l);
+      if (v == yn) g -= 1.f;
+      const uint16_t b = to_bf16(g);
+      G[cm_index(n, v, Np)] = b;
+      Gt[cm_index(v, n, Vp)] = b;
+    }
+  }
+}
+
+// dBias partials of the training path: part[s][v] = go * sum over the row tiles of split s of
+// sum_n a_n E'[n, v], read from Gt (block (n/256, v/256), one 128 KiB block per row tile). Block (v tile, split s);
+// thread t owns the vocabulary rows 8i + t%8 (i = 0..31) of the tile and the 8-wide chunk t/8 of reduction
+// positions (kperm order), so each 16-byte load is one piece row; the 32 chunk sums of a row are added in a fixed
+// order through LDS.
+__global__ __launch_bounds__(256) void k_dbias_gemv(const uint16_t* __restrict__ Gt, const float* __restrict__ arow,
+                                                    const float* __restrict__ go, int64_t Np, int64_t Vp,
+                                                    int per_split, float* __restrict__ part) {
+  __shared__ float red[32][257];
+  const int t = threadIdx.x, c = t >> 3;
+  const int64_t tv = blockIdx.x;
+  const int s = (int)blockIdx.y;
+  const int nt = (int)(Np / BM);
+  const int j0 = s * per_split, j1 = min(nt, j0 + per_split);
+  float acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  // positions 8c .. 8c+7 hold the rows kperm_inv(8c + e): two runs of 4 consecutive n
+  const int r0 = kperm_inv(8 * c), r1 = kperm_inv(8 * c + 4);
+  for (int j = j0; j < j1; ++j) {
+    const float4 a0 = *reinterpret_cast<const float4*>(arow + (int64_t)j * BM + r0);
+    const float4 a1 = *reinterpret_cast<const float4*>(arow + (int64_t)j * BM + r1);
+    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const uint16_t* blk = Gt + ((int64_t)j * (Vp / BM) + tv) * CM_TILE;
+#pragma unroll 8
+    for (int i = 0; i < 32; ++i) {
+      const u16x8 g = *reinterpret_cast<const u16x8*>(blk + ((int64_t)i * 256 + t) * 8);
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = __builtin_fmaf(bf16_to_f32(g[e]), av[e], d);
+      acc[i] += d;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) red[i][t] = acc[i];
+  __syncthreads();
+  // vocabulary row 8i + r of the tile (thread t: i = t/8, r = t%8) = sum over the 32 chunks c of red[i][8c + r]
+  const int i = t >> 3, r = t & 7;
+  float sum = 0.f;
+#pragma unroll
+  for (int cc = 0; cc < 32; ++cc) sum += red[i][cc * 8 + r];
+  part[(int64_t)s * Vp + tv * BM + t] = (go != nullptr ? go[0] : 1.f) * sum;
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // K-blocked transpose: dst element (c, r) at dst[(r/256)*C*256 + c*256 + kperm(r%256)] = src[r*ld + c] for r < R,
-// 0 for R <= r < (grid rows); c < C (C % 8 == 0). One workgroup per 64 x 64 tile, staged through LDS. The
+// 0 for R <= r < (grid rows); c < C (C % 8 == 0). With rscale, source row r is first multiplied by
+// go[0] * rscale[r] (fp32) and rounded to bf16. One workgroup per 64 x 64 tile, staged through LDS. The
 // reduction index r is stored in the permuted order kperm that G and Gt use (their 16-byte stores), so the
 // products of the dH and dW contractions pair up.
 __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __restrict__ src, int64_t ld, int64_t R,
-                                                           int64_t C, uint16_t* __restrict__ dst) {
+                                                           int64_t C, uint16_t* __restrict__ dst,
+                                                           const float* __restrict__ rscale = nullptr,
+                                                           const float* __restrict__ go = nullptr) {
   __shared__ uint16_t tile[64][66];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
@@ -1008,7 +1290,14 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
     const int rl = (t >> 3) + 32 * h, cl = (t & 7) * 8;
     const int64_t r = r0 + rl, c = c0 + cl;
     u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < R && c < C) v = *reinterpret_cast<const u16x8*>(src + r * ld + c);
+    if (r < R && c < C) {
+      v = *reinterpret_cast<const u16x8*>(src + r * ld + c);
+      if (rscale != nullptr) {  // row r scaled by go * rscale[r], rounded back to bf16
+        const float f = (go != nullptr ? go[0] : 1.f) * rscale[r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = to_bf16(f * bf16_to_f32(v[e]));
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) tile[rl][cl + e] = v[e];
   }
@@ -1032,14 +1321,15 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 
 // ---------------------------------------------------------------------------------------------------------
 // Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
-// nk_total K stages. The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
+// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
 template <bool OUT_BF16, bool KF, bool APC>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
-            int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part) {
+            int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part,
+            const float* __restrict__ rscale, const float* __restrict__ go) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
   const int b = (int)blockIdx.x;
   int lin, s0 = 0, nk = nk_total, slot = -1;
@@ -1071,23 +1361,26 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
           pt[(wm * 128 + acc_row(mi, r, lh)) * BN + wn * 128 + nj * 32 + lr] = acc[mi][nj][r];
     return;
   }
+  const float gs = go != nullptr ? go[0] : 1.f;
 #pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
-    const int64_t j = n0 + wn * 128 + nj * 32 + lr;
-    if (j >= Nc) continue;
+  for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int r = 0; r < 16; ++r) {
+      const int64_t i = m0 + wm * 128 + acc_row(mi, r, lh);
+      if (i >= M) continue;
+      const float sc = rscale != nullptr ? gs * rscale[i] : 1.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t i = m0 + wm * 128 + acc_row(mi, r, lh);
-        if (i < M) {
+      for (int nj = 0; nj < 4; ++nj) {
+        const int64_t j = n0 + wn * 128 + nj * 32 + lr;
+        if (j < Nc) {
+          const float o = rscale != nullptr ? sc * acc[mi][nj][r] : acc[mi][nj][r];
           if constexpr (OUT_BF16)
-            reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)acc[mi][nj][r];
+            reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)o;
           else
-            reinterpret_cast<float*>(C)[i * ldc + j] = acc[mi][nj][r];
+            reinterpret_cast<float*>(C)[i * ldc + j] = o;
         }
       }
-  }
+    }
 }
 
 // Sum of the P K-slices of each split tail tile into C (fixed order p = 0..P-1). Block (group of 4 rows, tile r);
@@ -1095,7 +1388,8 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
 template <bool OUT_BF16>
 __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ part, int P, int full, int tiles_m,
                                                      int tiles_n, int group, int64_t M, int64_t Nc,
-                                                     void* __restrict__ C, int64_t ldc) {
+                                                     void* __restrict__ C, int64_t ldc,
+                                                     const float* __restrict__ rscale, const float* __restrict__ go) {
   const int r = (int)blockIdx.y;
   int tm, tn;
   tile_of(full + r, tiles_m, tiles_n, group, tm, tn);
@@ -1110,7 +1404,8 @@ __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ p
   }
   const int64_t i = (int64_t)tm * BM + il;
   if (i >= M) return;
-  const float o[4] = {s.x, s.y, s.z, s.w};
+  const float sc = rscale != nullptr ? (go != nullptr ? go[0] : 1.f) * rscale[i] : 1.f;
+  const float o[4] = {sc * s.x, sc * s.y, sc * s.z, sc * s.w};
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t j = (int64_t)tn * BN + jl + e;
@@ -1207,7 +1502,7 @@ int check_bias(const float* bias) { return (bias != nullptr && (reinterpret_cast
 int launch_status();
 template <bool OUT_BF16>
 int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t Nc, int group, void* C, int64_t ldc,
-                float* part, hipStream_t st) {
+                float* part, hipStream_t st, const float* rscale = nullptr, const float* go = nullptr) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nc, BN), T = tiles_m * tiles_n;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -1225,22 +1520,22 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (A.cm) {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part);
+                         tiles_n, group, full, P, C, ldc, part, rscale, go);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part);
+                         tiles_n, group, full, P, C, ldc, part, rscale, go);
   } else {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part);
+                         tiles_n, group, full, P, C, ldc, part, rscale, go);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part);
+                         tiles_n, group, full, P, C, ldc, part, rscale, go);
   }
   int rc = launch_status();
   if (rc || full == T) return rc;
   hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 4, T - full), dim3(256), 0, st, part, P, full, tiles_m,
-                     tiles_n, group, M, Nc, C, ldc);
+                     tiles_n, group, M, Nc, C, ldc, rscale, go);
   return launch_status();
 }
 
@@ -1358,6 +1653,149 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
   }
   if (dGate) {
     hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
+    if ((rc = launch_status())) return rc;
+  }
+  return MCE_OK;
+}
+
+// Training-path workspace: the backward workspace (G and Gt hold E', the transposed copies, partials), the
+// forward workspace after it, then e_n, a_n, the flags and the flagged-row list, all [Np], and the counter.
+struct TrainWs {
+  BwdWs b;
+  FwdWs f;
+  float *lse_est, *arow;
+  int *flag, *flag_list, *flag_count;
+  size_t bytes;
+};
+TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
+  TrainWs w{};
+  w.b = bwd_ws_layout(base, N, K, V);
+  size_t off = align256(w.b.bytes);
+  w.f = fwd_ws_layout(base == nullptr ? nullptr : base + off, N, V);
+  off = align256(off + w.f.bytes);
+  const int64_t np = w.b.np;
+  w.lse_est = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
+  w.arow = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
+  w.flag = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
+  w.flag_list = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
+  w.flag_count = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
+  w.bytes = off;
+  return w;
+}
+
+float g_train_s_max = TRAIN_S_MAX;
+constexpr int REPAIR_BLOCKS = 256;
+
+// Forward of the one-pass training path (mixture or plain cross-entropy, no sparse bias): the per-row outputs of
+// fwd_impl plus E' in the workspace's G / Gt and a_n.
+int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                   const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
+                   int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
+                   float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
+  if (rc) return rc;
+  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr)) return MCE_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N == 0) {
+    (void)hipMemsetAsync(loss_sum, 0, sizeof(float), st);
+    return launch_status();
+  }
+  if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
+  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
+  const bool kf = K % BK == 0;
+  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, nullptr,
+                     nullptr, 0, N, K, V_real, w.f.xy, w.f.xc);
+  if ((rc = launch_status())) return rc;
+  // e_n: the first vocabulary tile (one tile row of k_fwd_tiles) and the target logit
+  if (kf)
+    hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
+                       w.f.part_m, w.f.part_s);
+  else
+    hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
+                       w.f.part_m, w.f.part_s);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, w.f.part_m, w.f.part_s, w.f.xy,
+                     y, N, w.b.np, w.lse_est, w.flag, w.flag_count);
+  if ((rc = launch_status())) return rc;
+  if (kf)
+    hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est, N,
+                       w.b.np, V, w.b.vp, V_real, tv, tn, g_train_s_max, w.b.G, w.b.Gt, w.f.part_m, w.f.part_s,
+                       w.flag);
+  else
+    hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est, N,
+                       w.b.np, V, w.b.vp, V_real, tv, tn, g_train_s_max, w.b.G, w.b.Gt, w.f.part_m, w.f.part_s,
+                       w.flag);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.f.part_m, w.f.part_s, w.f.xy,
+                     nullptr, nullptr, nullptr, 0, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows,
+                     dgr_rows, w.f.loss_part);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_train_rows, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, y, w.f.xy, w.lse_est,
+                     lse_rows, wgt_rows, w.flag, N, w.b.np, w.b.vp, V_real, w.arow, w.flag_count, w.flag_list, w.b.G,
+                     w.b.Gt);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, y, lse_rows, K, V,
+                     w.b.vp, V_real, w.b.np, w.flag_count, w.flag_list, w.b.G, w.b.Gt);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.f.loss_part, (int64_t)cdiv(N, 32), loss_sum);
+  return launch_status();
+}
+
+// dH = go a . (E' W) of the training path.
+int bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V, void* dH,
+                      int dh_bf16, int64_t lddh, void* ws, size_t ws_bytes, hipStream_t st) {
+  int rc = check_common(W, ldw, W, ldw, N, K, V, V);
+  if (rc) return rc;
+  if (N == 0) return MCE_OK;
+  if (!dH || !ws || !go || lddh < K) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.b.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
+                     ldw, V, K, w.b.Wt, nullptr, nullptr);
+  if ((rc = launch_status())) return rc;
+  const Operand Aop{w.b.G, 0, N, w.b.vp, w.b.np * BLK, 1};
+  const Operand Bop{w.b.Wt, BLK, K, w.b.vp, K * BLK};
+  const int nk = (int)(w.b.vp / BK);
+  return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.b.part, st, w.arow, go)
+                 : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.b.part, st, w.arow, go);
+}
+
+// dW = E'^T (go a . H) and dBias = E'^T (go a) of the training path (either output may be null).
+constexpr int DBIAS_SPLITS = 8;
+int bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N, int64_t K, int64_t V, float* dW,
+                      int64_t lddw, float* dBias, void* ws, size_t ws_bytes, hipStream_t st) {
+  int rc = check_common(H, ldh, H, ldh, N, K, V, V);
+  if (rc) return rc;
+  if (dW && lddw < K) return MCE_EINVAL;
+  if (N == 0) {
+    if (dW) (void)hipMemset2DAsync(dW, sizeof(float) * lddw, 0, sizeof(float) * K, V, st);
+    if (dBias) (void)hipMemsetAsync(dBias, 0, sizeof(float) * V, st);
+    return launch_status();
+  }
+  if (!ws || !go) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  if (dW) {
+    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.b.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st,
+                       H, ldh, N, K, w.b.Ht, w.arow, go);
+    if ((rc = launch_status())) return rc;
+    const Operand Aop{w.b.Gt, 0, V, w.b.np, w.b.vp * BLK, 1};
+    const Operand Bop{w.b.Ht, BLK, K, w.b.np, K * BLK, 0};
+    if ((rc = launch_gemm<false>(Aop, Bop, (int)(w.b.np / BK), V, K, 4, dW, lddw, w.b.part, st))) return rc;
+  }
+  if (dBias) {
+    const int nt = (int)(w.b.np / BM);
+    const int per = (int)cdiv(nt, DBIAS_SPLITS);
+    const int splits = (int)cdiv(nt, per);
+    hipLaunchKernelGGL(k_dbias_gemv, dim3((unsigned)(w.b.vp / BM), (unsigned)splits), dim3(256), 0, st, w.b.Gt,
+                       w.arow, go, w.b.np, w.b.vp, per, w.b.dbias_part);
+    if ((rc = launch_status())) return rc;
+    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.b.dbias_part, splits, w.b.vp,
+                       V, dBias);
     if ((rc = launch_status())) return rc;
   }
   return MCE_OK;
@@ -1504,5 +1942,53 @@ int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
   if (dW && (rc = mce_bwd_dweight(H, ldh, N, K, V, dW, lddw, ws, ws_bytes, stream))) return rc;
   return MCE_OK;
 }
+
+size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V) {
+  if (N < 0 || V <= 0 || K <= 0) return 0;
+  return train_ws_layout(nullptr, N, K, V).bytes;
+}
+
+int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                  const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
+                  int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
+                  float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
+  return fwd_train_impl(H, ldh, W, ldw, bias, y, gate, hit, N, K, V, V_real, loss_rows, lse_rows, wgt_rows, dgr_rows,
+                        loss_sum, ws, ws_bytes, stream);
+}
+
+int mce_bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V, void* dH,
+                          int dh_bf16, int64_t lddh, void* ws, size_t ws_bytes, void* stream) {
+  return bwd_train_dhidden(W, ldw, go, N, K, V, dH, dh_bf16, lddh, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mce_bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N, int64_t K, int64_t V, float* dW,
+                          int64_t lddw, float* dBias, void* ws, size_t ws_bytes, void* stream) {
+  return bwd_train_dweight(H, ldh, go, N, K, V, dW, lddw, dBias, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mce_bwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* go,
+                  const float* dgr_rows, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16, int64_t lddh,
+                  float* dW, int64_t lddw, float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  if (dH && (rc = bwd_train_dhidden(W, ldw, go, N, K, V, dH, dh_bf16, lddh, ws, ws_bytes, st))) return rc;
+  if ((dW || dBias) && (rc = bwd_train_dweight(H, ldh, go, N, K, V, dW, lddw, dBias, ws, ws_bytes, st))) return rc;
+  if (dGate && N > 0) {
+    if (!dgr_rows || !go) return MCE_EINVAL;
+    hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
+    return launch_status();
+  }
+  return MCE_OK;
+}
+
+int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int* out, void* stream) {
+  if (ws == nullptr || out == nullptr || N <= 0 || K <= 0 || V <= 0) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(const_cast<void*>(ws)), N, K, V);
+  (void)hipMemcpyAsync(out, w.flag_count, sizeof(int), hipMemcpyDeviceToDevice,
+                       reinterpret_cast<hipStream_t>(stream));
+  return launch_status();
+}
+
+void mce_train_set_threshold(float s_max) { g_train_s_max = s_max > 0.f ? s_max : TRAIN_S_MAX; }
 
 }  // extern "C"

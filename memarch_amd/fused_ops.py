@@ -6,17 +6,24 @@ call signatures, same return value (the fp32 loss SUM over rows) and the same gr
 w, gate and the sparse values b in their own dtypes; None for y, hit, cand and chunk). All device work runs in libmce.so (HIP, gfx950) on torch's
 current stream; there is no other code path, and a tensor that is not on a GPU raises.
 
-Differences from the reference that autograd cannot observe: gradients are computed in `backward` by
-recomputing the logits (the reference computes them during `forward`, fused_ops.py:148-155), and `chunk` is
-accepted and ignored (tiling is internal). Logits are fp32 in both passes (never rounded to bf16), and rows
-with P below the 1e-30 clamp get zero gradient, as the reference's eager formula does (full2.py:1925-1929).
+When any input needs a gradient (and there is no sparse bias), the forward runs the one-pass training path
+(mce_fwd_train): like the reference (fused_ops.py:148-155) it forms the logits gradient during the forward, as a
+bf16 N x V buffer of exp(x - e_n) with one per-row factor left to the backward, and never stores the logits; the
+backward then runs only the dH and dW contractions. Otherwise -- no gradient needed, a sparse bias, or
+RECOMPUTE set (environment MEMARCH_AMD_RECOMPUTE=1) -- the forward computes only the per-row statistics and the
+backward recomputes the logits tile by tile to form the gradient. `chunk` is accepted and ignored (tiling is
+internal). Logits are fp32 in both paths (never rounded to bf16), and rows with P below the 1e-30 clamp get zero
+gradient, as the reference's eager formula does (full2.py:1925-1929).
 """
+import os
+
 import torch
 
 from . import _lib
 
 _BF16 = torch.bfloat16
 MAX_KC = 8   # sparse candidates per row of linear_ce_sparse (the library's limit)
+RECOMPUTE = os.environ.get("MEMARCH_AMD_RECOMPUTE", "0") == "1"   # True: the two-pass (recompute) backward
 
 
 def _stream(dev):
@@ -67,9 +74,10 @@ def _check_sparse(cand, cval, n, gate):
     return kc
 
 
-def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
+def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=False):
     """Validates the inputs, prepares the bf16 operands and runs mce_fwd (or mce_fwd_sparse when a sparse bias
-    cand/cval [N, k] is given) on the current stream. Returns (operands, per-row outputs, loss_sum, meta)."""
+    cand/cval [N, k] is given, or mce_fwd_train for train=True) on the current stream. Returns (operands, per-row
+    outputs, loss_sum, meta, training workspace or None)."""
     if h.dim() != 2 or w.dim() != 2 or h.shape[1] != w.shape[1]:
         raise ValueError(f"h {tuple(h.shape)} and w {tuple(w.shape)} must be [N, K] and [V, K]")
     n, k = h.shape
@@ -98,6 +106,14 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
     loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
     loss_sum = torch.empty((), **f32)
     lib = _lib.load()
+    if train and kc == 0:
+        ws_bytes = lib.mce_train_ws_bytes(n, kp, v)
+        tws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
+                  _ptr(hf), n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum),
+                  _ptr(tws), ws_bytes, _stream(dev))
+        rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
+        return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real), tws
     ws_bytes = lib.mce_fwd_ws_bytes(n, kp, v)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     if cand64 is not None:
@@ -110,12 +126,15 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
                   _ptr(hf), n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum),
                   _ptr(ws), ws_bytes, _stream(dev))
     rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
-    return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real)
+    return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real), None
 
 
 def _forward(ctx, h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
-    (hd, wd, bf, y64, c64, cv32), rows, loss_sum, meta = _fwd_launch(h, w, bias, y, gate, hit, v_real, cand, cval)
+    train = ctx is not None and any(ctx.needs_input_grad) and cand is None and not RECOMPUTE
+    (hd, wd, bf, y64, c64, cv32), rows, loss_sum, meta, tws = _fwd_launch(h, w, bias, y, gate, hit, v_real, cand,
+                                                                          cval, train)
     ctx.save_for_backward(hd, wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"], c64, cv32)
+    ctx.train_ws = tws   # the one-pass path's E' and row factors, read by the backward (None: recompute)
     ctx.meta = meta
     ctx.dtypes = (h.dtype, w.dtype, None if gate is None else gate.dtype, None if bias is None else bias.dtype,
                   None if cval is None else cval.dtype)
@@ -135,8 +154,8 @@ def forward_rows(h, w, y, gate, hit, bias=None, v_real=None, cand=None, cval=Non
     """The forward pass without autograd: dict of the fp32 loss sum and the per-row loss, lse (logsumexp of the
     row's logits), wgt = (1-g)py/P and dgr = (py-hit)/P (both 0 for rows under the 1e-30 clamp). gate = hit =
     None is plain cross-entropy (wgt = 1, dgr = 0), optionally with a sparse bias cand/cval [..., k]."""
-    _, rows, loss_sum, _ = _fwd_launch(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), _flat(gate), _flat(hit),
-                                       v_real, _flat_k(cand), _flat_k(cval))
+    _, rows, loss_sum, _, _ = _fwd_launch(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), _flat(gate),
+                                          _flat(hit), v_real, _flat_k(cand), _flat_k(cval))
     return dict(loss_sum=loss_sum, **rows)
 
 
@@ -152,7 +171,26 @@ def _backward(ctx, go, need_h, need_w, need_b, need_g, need_c=False):
     dbias = torch.empty(v, **f32) if (need_b and bf is not None) else None
     dcval = torch.empty(c64.shape, **f32) if (need_c and c64 is not None) else None
     dh = dw = None
-    if need_h or need_w or need_g or dbias is not None or dcval is not None:
+    tws = getattr(ctx, "train_ws", None)
+    if tws is not None:
+        st = _stream(dev)
+        nb = tws.numel()
+        if need_h:
+            out_bf16 = hdt == _BF16
+            dh = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev)
+            _lib.call("mce_bwd_train_dhidden", _ptr(wd), wd.stride(0), _ptr(go32), n, kp, v, _ptr(dh), int(out_bf16),
+                      dh.stride(0), _ptr(tws), nb, st)
+            dh = dh[:, :k].to(hdt)
+        if need_w or dbias is not None:
+            dwf = torch.empty(v, kp, **f32) if need_w else None
+            _lib.call("mce_bwd_train_dweight", _ptr(hd), hd.stride(0), _ptr(go32), n, kp, v, _ptr(dwf),
+                      kp if dwf is None else dwf.stride(0), _ptr(dbias), _ptr(tws), nb, st)
+            if need_w:
+                dw = dwf[:, :k].to(wdt)
+        if dgate is not None:
+            _lib.call("mce_bwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(go32), _ptr(dgr), n, kp,
+                      v, None, 0, kp, None, kp, None, _ptr(dgate), _ptr(tws), nb, st)
+    elif need_h or need_w or need_g or dbias is not None or dcval is not None:
         lib = _lib.load()
         ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)

@@ -83,3 +83,48 @@ def assert_parity(got, fwd, bwd, what=""):
         if k in errs:
             assert errs[k] <= GRAD_RTOL, (what, k, errs)
     return errs
+
+
+def capi_train(case, go=1.0, s_max=None, dev="cuda"):
+    """The one-pass training path through the C ABI directly (mce_fwd_train, mce_bwd_train) on bf16 copies of the
+    case's operands; s_max sets the fallback bound (mce_train_set_threshold) for this call only. Returns numpy
+    results and the number of rows written by the exact fallback pass."""
+    from memarch_amd import _lib
+    lib = _lib.load()
+    n, k = case["h"].shape
+    v = case["w"].shape[0]
+    h = case["h"].to(dev, torch.bfloat16).contiguous()
+    w = case["w"].to(dev, torch.bfloat16).contiguous()
+    b = None if case["bias"] is None else case["bias"].to(dev, torch.float32).contiguous()
+    y = case["y"].to(dev, torch.int64).contiguous()
+    gate = case["gate"].to(dev, torch.float32).contiguous()
+    hit = case["hit"].to(dev, torch.float32).contiguous()
+    f32 = dict(dtype=torch.float32, device=dev)
+    loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
+    loss_sum = torch.empty((), **f32)
+    nb = lib.mce_train_ws_bytes(n, k, v)
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    if s_max is not None:
+        lib.mce_train_set_threshold(float(s_max))
+    try:
+        _lib.call("mce_fwd_train", p(h), k, p(w), k, p(b), p(y), p(gate), p(hit), n, k, v, case["v_real"],
+                  p(loss_rows), p(lse), p(wgt), p(dgr), p(loss_sum), p(ws), nb, st)
+    finally:
+        if s_max is not None:
+            lib.mce_train_set_threshold(0.0)
+    flagged = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("mce_train_flagged", p(ws), n, k, v, p(flagged), st)
+    go_t = torch.full((), go, **f32)
+    dh = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    dw = torch.empty(v, k, **f32)
+    dbias = torch.empty(v, **f32) if b is not None else None
+    dgate = torch.empty(n, **f32)
+    _lib.call("mce_bwd_train", p(h), k, p(w), k, p(go_t), p(dgr), n, k, v, p(dh), 1, k, p(dw), k, p(dbias),
+              p(dgate), p(ws), nb, st)
+    torch.cuda.synchronize()
+    out = dict(loss=float(loss_sum) * go, dh=dh.float().cpu().numpy(), dw=dw.cpu().numpy(),
+               dgate=dgate.cpu().numpy(), dbias=None if dbias is None else dbias.cpu().numpy(),
+               lse=lse.cpu().double().numpy(), flagged=int(flagged.item()))
+    return out
