@@ -47,6 +47,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef mce_i32x4 i32x4;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #define LDS_AS __attribute__((address_space(3)))
 
 constexpr int BM = 256;              // tile rows (A operand rows)
@@ -101,7 +102,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int SG_MFMA = 0x8, SG_DS_READ = 0x100;
+constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DS_READ = 0x100;
 
 // ---------------------------------------------------------------------------------------------------------
 // Direct global -> LDS loads through a buffer resource (buffer_load_lds, declared above): lane l of one
@@ -294,6 +295,60 @@ __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4],
     for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
 
+// Dot products of the A fragments with a vector over the reduction index (gemm_tile<.., DB>): sum_k A(m, k) u(k)
+// for the wave's 128 rows m, accumulated per lane over its half of each slice's K positions (lane/32 selects
+// 8 of the 16), with v_dot2c_f32_bf16 beside the MFMAs. u arrives through LDS: 64 bf16 values per stage (the
+// slot of ring buffer b at APOFF + 1024 b, written by one load instruction of wave 0).
+constexpr int APOFF = LDS_BYTES;
+struct DotState {
+  i32x4 rsrc;       // u, bf16
+  uint32_t addr;    // this lane's LDS byte offset within a slot: 16 * (lane / 32)
+  bf16x8 cur, next; // u values of the slice being multiplied / of the slice whose fragments are being read
+  float acc[4];     // per A fragment i (rows 32 i .. 32 i + 31 of the wave)
+};
+template <int BUF, int KK>
+__device__ __forceinline__ bf16x8 ap_read(const char* lds, uint32_t addr) {
+  return frag_at<APOFF + BUF * 1024 + KK * 32>(lds, addr);
+}
+// c + a[2q] u[2q] + a[2q+1] u[2q+1] (the pairs taken with shufflevector: a bit_cast of one 32-bit element of a
+// vector loses the element index in this compiler)
+template <int Q>
+__device__ __forceinline__ float dot2_pair(const bf16x8& a, const bf16x8& u, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2 * Q, 2 * Q + 1),
+                                         __builtin_shufflevector(u, u, 2 * Q, 2 * Q + 1), c, false);
+}
+__device__ __forceinline__ float dot2_word(const bf16x8& a, const bf16x8& u, int q, float c) {
+  switch (q) {
+    case 0: return dot2_pair<0>(a, u, c);
+    case 1: return dot2_pair<1>(a, u, c);
+    case 2: return dot2_pair<2>(a, u, c);
+    default: return dot2_pair<3>(a, u, c);
+  }
+}
+__device__ __forceinline__ float dot8(const bf16x8& a, const bf16x8& u, float c) {
+  return dot2_pair<3>(a, u, dot2_pair<2>(a, u, dot2_pair<1>(a, u, dot2_pair<0>(a, u, c))));
+}
+// Keeps a dot-product accumulator's update inside the slice that issues it: without this the compiler sinks a
+// stage's dot products to the end of the loop body, keeping all its fragments alive.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+// Wave 0's load of u[stage*64 .. +63] into the slot of ring buffer `slot` (lanes 8..63 write zeros).
+__device__ __forceinline__ void issue_ap(const DotState& dp, int stage, int send, char* lds, int slot) {
+  const int lane = threadIdx.x & 63;
+  const int off = (stage < send && lane < 8) ? stage * 128 + lane * 16 : OOB;
+  buffer_load_lds(dp.rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
+}
+// sched_slice with the dot products: one LDS read, then MFMA, two VALU, MFMA; the extra LDS read of u first.
+__device__ __forceinline__ void sched_slice_db() {
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_VALU, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+  }
+}
+
 // Interleave the current scheduling region: one LDS read between two MFMAs.
 __device__ __forceinline__ void sched_slice() {
 #pragma unroll
@@ -305,23 +360,36 @@ __device__ __forceinline__ void sched_slice() {
 
 // A slice without loads: reads of slice RK of buffer RBUF into (da, db), the 16 MFMAs of (ua, ub), interleaved by
 // the compiler one read per two MFMAs.
-template <int RBUF, int RK>
+template <int RBUF, int RK, bool DB = false>
 __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
-                                            const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4]) {
-  read_frags<RBUF, RK>(lds, ad, da, db);
-  mma16(acc, ua, ub);
-  sched_slice();
+                                            const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
+                                            DotState* dp = nullptr) {
+  if constexpr (DB) {
+    dp->next = ap_read<RBUF, RK>(lds, dp->addr);
+    read_frags<RBUF, RK>(lds, ad, da, db);
+    mma16(acc, ua, ub);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dp->acc[i] = dot8(ua[i], dp->cur, dp->acc[i]);
+    sched_slice_db();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pin(dp->acc[i]);
+  } else {
+    read_frags<RBUF, RK>(lds, ad, da, db);
+    mma16(acc, ua, ub);
+    sched_slice();
+  }
   __builtin_amdgcn_sched_barrier(0);
 }
 
 // A slice with loads, in a fixed order (a scheduling barrier after every MFMA): the 16 MFMAs of (ua, ub); the 8
 // fragment reads of slice RK of buffer RBUF into (da, db), one before every even MFMA; and this wave's 8 load
 // instructions of one operand of a stage into that operand's image of buffer LBUF, one after every odd MFMA.
-template <int RBUF, int RK, bool OPB_, int LBUF, bool KF>
+template <int RBUF, int RK, bool OPB_, int LBUF, bool KF, bool DB = false>
 __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
-                                            const Stream& st, const StageSrc& g, int wave) {
+                                            const Stream& st, const StageSrc& g, int wave, DotState* dp = nullptr) {
   constexpr int IMG = (OPB_ ? BOFF : AOFF) + LBUF * I::OPB;
+  if constexpr (DB) dp->next = ap_read<RBUF, RK>(lds, dp->addr);
 #pragma unroll
   for (int idx = 0; idx < 16; ++idx) {
     if ((idx & 1) == 0) {
@@ -336,6 +404,10 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
     }
     acc[idx >> 2][idx & 3] =
         __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua[idx >> 2], ub[idx & 3], acc[idx >> 2][idx & 3], 0, 0, 0);
+    if constexpr (DB) {
+      dp->acc[idx >> 2] = dot2_word(ua[idx >> 2], dp->cur, idx & 3, dp->acc[idx >> 2]);
+      pin(dp->acc[idx >> 2]);
+    }
     if (idx & 1) {
       const int j = idx >> 1;
       issue_one<KF>(st, g, j, lds, IMG + (wave * I::LPW + j) * 1024);
@@ -350,22 +422,29 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
 //   wait for this wave's loads of stage kt+1, barrier: every wave has read all of stage kt and stage kt+1 landed;
 //   slice 3: MFMAs on slice 3, reads of slice 0 of stage kt+1 (NB), loads of stage kt+2's A operand into CB.
 // A stage's loads are thus split in two halves, one load per two MFMAs, landing over three slices of MFMAs.
-template <int CB, bool KF>
+template <int CB, bool KF, bool DB = false>
 __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4][4], bf16x8 (&fa)[2][4],
                                            bf16x8 (&fb)[2][4], char* lds, const FragAddr& ad, const Stream& sa,
-                                           const Stream& sb, int wave) {
+                                           const Stream& sb, int wave, DotState* dp = nullptr) {
   constexpr int NB = CB ^ 1;
   {
     const StageSrc gb = stage_src(sb, stage + 1, send);
-    slice_loads<CB, 1, true, NB, KF>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave);
+    slice_loads<CB, 1, true, NB, KF, DB>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave, dp);
   }
-  slice_plain<CB, 2>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0]);
-  slice_plain<CB, 3>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1]);
+  if constexpr (DB) dp->cur = dp->next;
+  slice_plain<CB, 2, DB>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], dp);
+  if constexpr (DB) dp->cur = dp->next;
+  slice_plain<CB, 3, DB>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], dp);
+  if constexpr (DB) dp->cur = dp->next;
   wait_vmcnt<0>();
   __syncthreads();
   {
     const StageSrc ga = stage_src(sa, stage + 2, send);
-    slice_loads<NB, 0, false, CB, KF>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
+    slice_loads<NB, 0, false, CB, KF, DB>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave, dp);
+  }
+  if constexpr (DB) {
+    dp->cur = dp->next;
+    if (wave == 0) issue_ap(*dp, stage + 2, send, lds, CB);
   }
 }
 
@@ -412,10 +491,10 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool BIAS = false, bool APC = false>
+template <bool KF, bool BIAS = false, bool APC = false, bool DB = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
-                                          int64_t Vreal = 0) {
+                                          int64_t Vreal = 0, DotState* dp = nullptr) {
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
@@ -436,9 +515,19 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
   issue_stage(sa, s0, send, lds, AOFF, wave);
   issue_stage(sb, s0, send, lds, BOFF, wave);
+  if constexpr (DB) {
+    // u of stage s0 before the A loads of stage s0+1, so the wait below covers it
+    dp->addr = 16 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dp->acc[i] = 0.f;
+    if (wave == 0) issue_ap(*dp, s0, send, lds, 0);
+  }
   issue_stage(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
+  if constexpr (DB) {
+    if (wave == 0) issue_ap(*dp, s0 + 1, send, lds, 1);
+  }
   if constexpr (BIAS) stash_bias(bslot, btile, m0, Vreal);
-  wait_vmcnt<I::LPW>();
+  wait_vmcnt<I::LPW>();  // with DB, wave 0's u of stage s0 precedes its last 8 loads
   __syncthreads();
   if constexpr (BIAS) {
     // the accumulators start at the row's bias (or -inf past V_real): x = b_v + sum_k w_vk h_nk
@@ -454,12 +543,13 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 
   bf16x8 fa[2][4], fb[2][4];
   read_frags<0, 0>(lds, ad, fa[0], fb[0]);
+  if constexpr (DB) dp->cur = ap_read<0, 0>(lds, dp->addr);
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    gemm_stage<0, KF>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave);
-    gemm_stage<1, KF>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave);
+    gemm_stage<0, KF, DB>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+    gemm_stage<1, KF, DB>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   }
-  if (kt < nk) gemm_stage<0, KF>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave);
+  if (kt < nk) gemm_stage<0, KF, DB>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   wait_vmcnt<0>();
   __syncthreads();
 }
@@ -487,7 +577,6 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group,
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 // two floats -> two bf16 (round to nearest even) in one 32-bit word, lo in the low half (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -1275,16 +1364,23 @@ __global__ __launch_bounds__(256) void k_dbias_gemv(const uint16_t* __restrict__
 // ---------------------------------------------------------------------------------------------------------
 // K-blocked transpose: dst element (c, r) at dst[(r/256)*C*256 + c*256 + kperm(r%256)] = src[r*ld + c] for r < R,
 // 0 for R <= r < (grid rows); c < C (C % 8 == 0). With rscale, source row r is first multiplied by
-// go[0] * rscale[r] (fp32) and rounded to bf16. One workgroup per 64 x 64 tile, staged through LDS. The
+// go[0] * rscale[r] (fp32) and rounded to bf16; uperm (needs rscale) then also receives those factors as bf16 in
+// the same kperm order, uperm[p] for every p < grid rows (0 past R). One workgroup per 64 x 64 tile, staged through LDS. The
 // reduction index r is stored in the permuted order kperm that G and Gt use (their 16-byte stores), so the
 // products of the dH and dW contractions pair up.
 __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __restrict__ src, int64_t ld, int64_t R,
                                                            int64_t C, uint16_t* __restrict__ dst,
                                                            const float* __restrict__ rscale = nullptr,
-                                                           const float* __restrict__ go = nullptr) {
+                                                           const float* __restrict__ go = nullptr,
+                                                           uint16_t* __restrict__ uperm = nullptr) {
   __shared__ uint16_t tile[64][66];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  if (uperm != nullptr && blockIdx.y == 0 && t < 64) {
+    // the row scales themselves, bf16, in the same kperm order: uperm[r0 + p] = go * rscale[r0 + kperm_inv(p)]
+    const int64_t r = r0 + kperm_inv(t);
+    uperm[r0 + t] = r < R ? to_bf16((go != nullptr ? go[0] : 1.f) * rscale[r]) : (uint16_t)0;
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int rl = (t >> 3) + 32 * h, cl = (t & 7) * 8;
@@ -1321,16 +1417,19 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 
 // ---------------------------------------------------------------------------------------------------------
 // Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
-// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
+// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB: the tiles of the
+// first tile column also write upart[p * ldu + m] = sum_k A(m, k) u(k) (u bf16 over the K positions) for their
+// K slice p (0 .. P-1; 0 for whole tiles, which zero rows 1 .. P-1). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16, bool KF, bool APC>
+template <bool OUT_BF16, bool KF, bool APC, bool DB>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part,
-            const float* __restrict__ rscale, const float* __restrict__ go) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+            const float* __restrict__ rscale, const float* __restrict__ go, const uint16_t* __restrict__ u,
+            float* __restrict__ upart, int64_t ldu) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (DB ? 2048 : 0)];
   const int b = (int)blockIdx.x;
   int lin, s0 = 0, nk = nk_total, slot = -1;
   if (b < full) {
@@ -1347,9 +1446,31 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   tile_of(lin, tiles_m, tiles_n, group, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   f32x16 acc[4][4];
-  gemm_tile<KF, false, APC>(A, B, s0, nk, m0, n0, lds, acc);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
+  if (DB && tn == 0) {
+    // the tiles of the first column also form upart[p][m] = sum_k A(m, k) u(k) over their K range, p = the K
+    // slice (0 for a whole tile, whose other P-1 rows are zeroed)
+    DotState dp;
+    dp.rsrc = make_rsrc(reinterpret_cast<uint64_t>(u));
+    gemm_tile<KF, false, APC, DB>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp);
+    if (wn == 0) {
+      float d[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = dp.acc[i] + __shfl_xor(dp.acc[i], 32);
+      if (lh == 0) {
+        const int p = slot >= 0 ? (b - full) % P : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) upart[(int64_t)p * ldu + m0 + wm * 128 + i * 32 + lr] = d[i];
+        if (slot < 0)
+          for (int q = 1; q < P; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) upart[(int64_t)q * ldu + m0 + wm * 128 + i * 32 + lr] = 0.f;
+      }
+    }
+  } else {
+    gemm_tile<KF, false, APC>(A, B, s0, nk, m0, n0, lds, acc);
+  }
   if (slot >= 0) {
     float* pt = part + (int64_t)slot * BM * BN;
 #pragma unroll
@@ -1502,7 +1623,8 @@ int check_bias(const float* bias) { return (bias != nullptr && (reinterpret_cast
 int launch_status();
 template <bool OUT_BF16>
 int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t Nc, int group, void* C, int64_t ldc,
-                float* part, hipStream_t st, const float* rscale = nullptr, const float* go = nullptr) {
+                float* part, hipStream_t st, const float* rscale = nullptr, const float* go = nullptr,
+                const uint16_t* u = nullptr, float* upart = nullptr, int64_t ldu = 0, int* p_out = nullptr) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nc, BN), T = tiles_m * tiles_n;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -1517,20 +1639,30 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   const bool kf = A.kext % BK == 0 && B.kext % BK == 0;
   const dim3 grid(full + (T - full) * P);
   if (B.cm) return MCE_EINVAL;  // only the A operand may be in the piece layout
-  if (A.cm) {
+  if (p_out) *p_out = P;
+  if (u != nullptr) {
+    // dot products with u: only for an A operand in the piece layout (G^T), fp32 output
+    if (!A.cm || OUT_BF16 || upart == nullptr) return MCE_EINVAL;
     if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part, rscale, go);
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
+                         tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart, ldu);
     else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part, rscale, go);
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart, ldu);
+  } else if (A.cm) {
+    if (kf)
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
+    else
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
   } else {
     if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part, rscale, go);
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
     else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part, rscale, go);
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
   }
   int rc = launch_status();
   if (rc || full == T) return rc;
@@ -1659,11 +1791,13 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
 }
 
 // Training-path workspace: the backward workspace (G and Gt hold E', the transposed copies, partials), the
-// forward workspace after it, then e_n, a_n, the flags and the flagged-row list, all [Np], and the counter.
+// forward workspace after it, then e_n, a_n, go*a_n in bf16 (kperm order), the flags and the flagged-row list,
+// all [Np], and the counter.
 struct TrainWs {
   BwdWs b;
   FwdWs f;
   float *lse_est, *arow;
+  uint16_t* uperm;
   int *flag, *flag_list, *flag_count;
   size_t bytes;
 };
@@ -1676,6 +1810,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   const int64_t np = w.b.np;
   w.lse_est = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
   w.arow = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
+  w.uperm = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * np);
   w.flag = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
   w.flag_list = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
   w.flag_count = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
@@ -1780,14 +1915,25 @@ int bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N
   const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   if (dW) {
+    // H^T scaled by go*a (and, for dBias, go*a itself in bf16); dW = E'^T (go a . H), and the first tile column
+    // also forms dBias partials sum_n E'[n, v] go a_n (one row per K slice of the split tail tiles)
     hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.b.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st,
-                       H, ldh, N, K, w.b.Ht, w.arow, go);
+                       H, ldh, N, K, w.b.Ht, w.arow, go, dBias ? w.uperm : nullptr);
     if ((rc = launch_status())) return rc;
     const Operand Aop{w.b.Gt, 0, V, w.b.np, w.b.vp * BLK, 1};
     const Operand Bop{w.b.Ht, BLK, K, w.b.np, K * BLK, 0};
-    if ((rc = launch_gemm<false>(Aop, Bop, (int)(w.b.np / BK), V, K, 4, dW, lddw, w.b.part, st))) return rc;
+    int P = 1;
+    if ((rc = launch_gemm<false>(Aop, Bop, (int)(w.b.np / BK), V, K, 4, dW, lddw, w.b.part, st, nullptr, nullptr,
+                                 dBias ? w.uperm : nullptr, w.b.dbias_part, w.b.vp, &P)))
+      return rc;
+    if (dBias) {
+      hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.b.dbias_part, P, w.b.vp,
+                         V, dBias);
+      return launch_status();
+    }
+    return MCE_OK;
   }
-  if (dBias) {
+  if (dBias) {  // dBias without dW: a pass over G^T
     const int nt = (int)(w.b.np / BM);
     const int per = (int)cdiv(nt, DBIAS_SPLITS);
     const int splits = (int)cdiv(nt, per);
