@@ -295,60 +295,6 @@ __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4],
     for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
 
-// Dot products of the A fragments with a vector over the reduction index (gemm_tile<.., DB>): sum_k A(m, k) u(k)
-// for the wave's 128 rows m, accumulated per lane over its half of each slice's K positions (lane/32 selects
-// 8 of the 16), with v_dot2c_f32_bf16 beside the MFMAs. u arrives through LDS: 64 bf16 values per stage (the
-// slot of ring buffer b at APOFF + 1024 b, written by one load instruction of wave 0).
-constexpr int APOFF = LDS_BYTES;
-struct DotState {
-  i32x4 rsrc;       // u, bf16
-  uint32_t addr;    // this lane's LDS byte offset within a slot: 16 * (lane / 32)
-  bf16x8 cur, next; // u values of the slice being multiplied / of the slice whose fragments are being read
-  float acc[4];     // per A fragment i (rows 32 i .. 32 i + 31 of the wave)
-};
-template <int BUF, int KK>
-__device__ __forceinline__ bf16x8 ap_read(const char* lds, uint32_t addr) {
-  return frag_at<APOFF + BUF * 1024 + KK * 32>(lds, addr);
-}
-// c + a[2q] u[2q] + a[2q+1] u[2q+1] (the pairs taken with shufflevector: a bit_cast of one 32-bit element of a
-// vector loses the element index in this compiler)
-template <int Q>
-__device__ __forceinline__ float dot2_pair(const bf16x8& a, const bf16x8& u, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2 * Q, 2 * Q + 1),
-                                         __builtin_shufflevector(u, u, 2 * Q, 2 * Q + 1), c, false);
-}
-__device__ __forceinline__ float dot2_word(const bf16x8& a, const bf16x8& u, int q, float c) {
-  switch (q) {
-    case 0: return dot2_pair<0>(a, u, c);
-    case 1: return dot2_pair<1>(a, u, c);
-    case 2: return dot2_pair<2>(a, u, c);
-    default: return dot2_pair<3>(a, u, c);
-  }
-}
-__device__ __forceinline__ float dot8(const bf16x8& a, const bf16x8& u, float c) {
-  return dot2_pair<3>(a, u, dot2_pair<2>(a, u, dot2_pair<1>(a, u, dot2_pair<0>(a, u, c))));
-}
-// Keeps a dot-product accumulator's update inside the slice that issues it: without this the compiler sinks a
-// stage's dot products to the end of the loop body, keeping all its fragments alive.
-__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
-// Wave 0's load of u[stage*64 .. +63] into the slot of ring buffer `slot` (lanes 8..63 write zeros).
-__device__ __forceinline__ void issue_ap(const DotState& dp, int stage, int send, char* lds, int slot) {
-  const int lane = threadIdx.x & 63;
-  const int off = (stage < send && lane < 8) ? stage * 128 + lane * 16 : OOB;
-  buffer_load_lds(dp.rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
-}
-// sched_slice with the dot products: one LDS read, then MFMA, two VALU, MFMA; the extra LDS read of u first.
-__device__ __forceinline__ void sched_slice_db() {
-  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_VALU, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-  }
-}
-
 // Interleave the current scheduling region: one LDS read between two MFMAs.
 __device__ __forceinline__ void sched_slice() {
 #pragma unroll
@@ -358,21 +304,74 @@ __device__ __forceinline__ void sched_slice() {
   }
 }
 
+// Dot products of one 32-row group of the A operand with a vector u over the reduction index (gemm_tile<.., DB>):
+// sum_k A(m, k) u(k) for the rows m of group `rg` of the tile. In every stage, wave w takes slice w (16 K
+// positions) of that group: one extra A fragment read and one read of the slice's u values (the lane's 8 of
+// them), then four v_dot2c_f32_bf16; every wave and tile runs the same instructions, so the work adds a small,
+// even cost to every stage. u arrives through LDS: 64 bf16 values per stage (the slot of ring buffer b at
+// APOFF + 1024 b, written by one load instruction of wave 0).
+constexpr int APOFF = LDS_BYTES;
+struct DotState {
+  i32x4 rsrc;       // u, bf16
+  uint32_t faddr;   // LDS byte offset of this lane's fragment (group rg, slice = wave) in the A image of buffer 0
+  uint32_t uaddr;   // LDS byte offset of this lane's 8 u values (slice = wave) in the slot of buffer 0
+  bf16x8 x, u;      // the fragment and u values read for this stage
+  float acc;        // row rg*32 + lane%32, K positions of lane half lane/32 of slice `wave` of every stage
+};
+// c + a[2q] u[2q] + a[2q+1] u[2q+1] (the pairs taken with shufflevector: a bit_cast of one 32-bit element of a
+// vector loses the element index in this compiler)
+template <int Q>
+__device__ __forceinline__ float dot2_pair(const bf16x8& a, const bf16x8& u, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2 * Q, 2 * Q + 1),
+                                         __builtin_shufflevector(u, u, 2 * Q, 2 * Q + 1), c, false);
+}
+__device__ __forceinline__ float dot8(const bf16x8& a, const bf16x8& u, float c) {
+  return dot2_pair<3>(a, u, dot2_pair<2>(a, u, dot2_pair<1>(a, u, dot2_pair<0>(a, u, c))));
+}
+// Keeps the dot-product accumulator's update inside the slice that issues it (the compiler would otherwise sink
+// it to the end of the loop body).
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+// Wave 0's load of u[stage*64 .. +63] into the slot of ring buffer `slot` (lanes 8..63 write zeros).
+__device__ __forceinline__ void issue_ap(const DotState& dp, int stage, int send, char* lds, int slot) {
+  const int lane = threadIdx.x & 63;
+  const int off = (stage < send && lane < 8) ? stage * 128 + lane * 16 : OOB;
+  buffer_load_lds(dp.rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
+}
+// Slice 1 with the two extra reads first; slice 2 with the four dot products between its first MFMAs.
+__device__ __forceinline__ void sched_slice_rd2() {
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+  sched_slice();
+}
+__device__ __forceinline__ void sched_slice_dot() {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    if (i < 4) __builtin_amdgcn_sched_group_barrier(SG_VALU, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+  }
+}
+
 // A slice without loads: reads of slice RK of buffer RBUF into (da, db), the 16 MFMAs of (ua, ub), interleaved by
 // the compiler one read per two MFMAs.
 template <int RBUF, int RK, bool DB = false>
 __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
                                             DotState* dp = nullptr) {
-  if constexpr (DB) {
-    dp->next = ap_read<RBUF, RK>(lds, dp->addr);
+  if constexpr (DB && RK == 2) {
+    // slice 1 of the stage (reads slice 2): this wave's extra fragment and u values of the stage's buffer
+    dp->x = frag_at<AOFF + RBUF * I::OPB>(lds, dp->faddr);
+    dp->u = frag_at<APOFF + RBUF * 1024>(lds, dp->uaddr);
     read_frags<RBUF, RK>(lds, ad, da, db);
     mma16(acc, ua, ub);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dp->acc[i] = dot8(ua[i], dp->cur, dp->acc[i]);
-    sched_slice_db();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pin(dp->acc[i]);
+    sched_slice_rd2();
+  } else if constexpr (DB && RK == 3) {
+    // slice 2 of the stage (reads slice 3): the dot products of the fragment read in slice 1
+    read_frags<RBUF, RK>(lds, ad, da, db);
+    mma16(acc, ua, ub);
+    dp->acc = dot8(dp->x, dp->u, dp->acc);
+    sched_slice_dot();
+    pin(dp->acc);
   } else {
     read_frags<RBUF, RK>(lds, ad, da, db);
     mma16(acc, ua, ub);
@@ -384,12 +383,11 @@ __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&
 // A slice with loads, in a fixed order (a scheduling barrier after every MFMA): the 16 MFMAs of (ua, ub); the 8
 // fragment reads of slice RK of buffer RBUF into (da, db), one before every even MFMA; and this wave's 8 load
 // instructions of one operand of a stage into that operand's image of buffer LBUF, one after every odd MFMA.
-template <int RBUF, int RK, bool OPB_, int LBUF, bool KF, bool DB = false>
+template <int RBUF, int RK, bool OPB_, int LBUF, bool KF>
 __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
-                                            const Stream& st, const StageSrc& g, int wave, DotState* dp = nullptr) {
+                                            const Stream& st, const StageSrc& g, int wave) {
   constexpr int IMG = (OPB_ ? BOFF : AOFF) + LBUF * I::OPB;
-  if constexpr (DB) dp->next = ap_read<RBUF, RK>(lds, dp->addr);
 #pragma unroll
   for (int idx = 0; idx < 16; ++idx) {
     if ((idx & 1) == 0) {
@@ -404,10 +402,6 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
     }
     acc[idx >> 2][idx & 3] =
         __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua[idx >> 2], ub[idx & 3], acc[idx >> 2][idx & 3], 0, 0, 0);
-    if constexpr (DB) {
-      dp->acc[idx >> 2] = dot2_word(ua[idx >> 2], dp->cur, idx & 3, dp->acc[idx >> 2]);
-      pin(dp->acc[idx >> 2]);
-    }
     if (idx & 1) {
       const int j = idx >> 1;
       issue_one<KF>(st, g, j, lds, IMG + (wave * I::LPW + j) * 1024);
@@ -429,21 +423,17 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
   constexpr int NB = CB ^ 1;
   {
     const StageSrc gb = stage_src(sb, stage + 1, send);
-    slice_loads<CB, 1, true, NB, KF, DB>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave, dp);
+    slice_loads<CB, 1, true, NB, KF>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave);
   }
-  if constexpr (DB) dp->cur = dp->next;
   slice_plain<CB, 2, DB>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], dp);
-  if constexpr (DB) dp->cur = dp->next;
   slice_plain<CB, 3, DB>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], dp);
-  if constexpr (DB) dp->cur = dp->next;
   wait_vmcnt<0>();
   __syncthreads();
   {
     const StageSrc ga = stage_src(sa, stage + 2, send);
-    slice_loads<NB, 0, false, CB, KF, DB>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave, dp);
+    slice_loads<NB, 0, false, CB, KF>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
   }
   if constexpr (DB) {
-    dp->cur = dp->next;
     if (wave == 0) issue_ap(*dp, stage + 2, send, lds, CB);
   }
 }
@@ -494,7 +484,7 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 template <bool KF, bool BIAS = false, bool APC = false, bool DB = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
-                                          int64_t Vreal = 0, DotState* dp = nullptr) {
+                                          int64_t Vreal = 0, DotState* dp = nullptr, int rg = 0) {
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
@@ -516,10 +506,15 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   issue_stage(sa, s0, send, lds, AOFF, wave);
   issue_stage(sb, s0, send, lds, BOFF, wave);
   if constexpr (DB) {
+    // this lane's extra fragment: row rg*32 + lane%32, 16-byte chunk 2*wave + lane/32 of the stage (slice = wave)
+    const int ra = rg * 32 + (lane & 31), c = 2 * wave + (lane >> 5);
+    if constexpr (APC)
+      dp->faddr = (ra >> 3) * 1024 + ((c ^ ((ra >> 3) & 1)) << 7) + (ra & 7) * 16;
+    else
+      dp->faddr = ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
+    dp->uaddr = 32 * wave + 16 * (lane >> 5);
+    dp->acc = 0.f;
     // u of stage s0 before the A loads of stage s0+1, so the wait below covers it
-    dp->addr = 16 * (lane >> 5);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dp->acc[i] = 0.f;
     if (wave == 0) issue_ap(*dp, s0, send, lds, 0);
   }
   issue_stage(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
@@ -543,7 +538,6 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 
   bf16x8 fa[2][4], fb[2][4];
   read_frags<0, 0>(lds, ad, fa[0], fb[0]);
-  if constexpr (DB) dp->cur = ap_read<0, 0>(lds, dp->addr);
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
     gemm_stage<0, KF, DB>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
@@ -1417,9 +1411,9 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 
 // ---------------------------------------------------------------------------------------------------------
 // Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
-// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB: the tiles of the
-// first tile column also write upart[p * ldu + m] = sum_k A(m, k) u(k) (u bf16 over the K positions) for their
-// K slice p (0 .. P-1; 0 for whole tiles, which zero rows 1 .. P-1). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
+// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB (tiles_n >= 8): block
+// of tile (tm, tn < 8) also forms sum_k A(m, k) u(k) (u bf16 over the K positions) for the rows m of its 32-row
+// group tn, over its K range: one 32-value partial per block (k_dbias_tiles adds them up). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
@@ -1428,7 +1422,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgp
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part,
             const float* __restrict__ rscale, const float* __restrict__ go, const uint16_t* __restrict__ u,
-            float* __restrict__ upart, int64_t ldu) {
+            float* __restrict__ upart) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (DB ? 2048 : 0)];
   const int b = (int)blockIdx.x;
   int lin, s0 = 0, nk = nk_total, slot = -1;
@@ -1448,25 +1442,22 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   f32x16 acc[4][4];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  if (DB && tn == 0) {
-    // the tiles of the first column also form upart[p][m] = sum_k A(m, k) u(k) over their K range, p = the K
-    // slice (0 for a whole tile, whose other P-1 rows are zeroed)
+  if constexpr (DB) {
+    // the tile also forms sum_k A(m, k) u(k) for its row group tn (rows tn*32 .. +31; requires tiles_n >= 8, so
+    // the row groups of a tile row are covered by its first 8 tiles), over its K range: written to
+    // upart[lin * 32 ..] for a whole tile, upart[(tiles_m * tiles_n + q) * 32 ..] for K slice q of the split tail
     DotState dp;
     dp.rsrc = make_rsrc(reinterpret_cast<uint64_t>(u));
-    gemm_tile<KF, false, APC, DB>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp);
-    if (wn == 0) {
-      float d[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = dp.acc[i] + __shfl_xor(dp.acc[i], 32);
-      if (lh == 0) {
-        const int p = slot >= 0 ? (b - full) % P : 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) upart[(int64_t)p * ldu + m0 + wm * 128 + i * 32 + lr] = d[i];
-        if (slot < 0)
-          for (int q = 1; q < P; ++q)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) upart[(int64_t)q * ldu + m0 + wm * 128 + i * 32 + lr] = 0.f;
-      }
+    const int rg = tn < 8 ? tn : 0;
+    gemm_tile<KF, false, APC, true>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, rg);
+    // lanes l and l+32 hold the two K halves of row rg*32 + l%32; the four waves hold the four slices
+    float d = dp.acc + __shfl_xor(dp.acc, 32);
+    float* red = reinterpret_cast<float*>(lds);
+    if (lh == 0) red[wave * 32 + lr] = d;
+    __syncthreads();
+    if (t < 32 && tn < 8) {
+      const int64_t row = slot >= 0 ? (int64_t)tiles_m * tiles_n + slot : lin;
+      upart[row * 32 + t] = (red[t] + red[32 + t]) + (red[64 + t] + red[96 + t]);
     }
   } else {
     gemm_tile<KF, false, APC>(A, B, s0, nk, m0, n0, lds, acc);
@@ -1537,6 +1528,29 @@ __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ p
         reinterpret_cast<float*>(C)[i * ldc + j] = o[e];
     }
   }
+}
+
+// dBias of the training path from the dW blocks' dot-product partials (k_gemm<.., DB>): dbias[v] = the partial of
+// tile (v/256, tn = (v%256)/32) at row v%32 -- or, for a tile of the split tail, the sum of its P K-slice partials
+// in a fixed order. One thread per v.
+__device__ __forceinline__ int lin_of(int tm, int tn, int tiles_m, int tiles_n, int group) {
+  const int g = tm / group, first = g * group, gsize = min(tiles_m - first, group);
+  return g * group * tiles_n + tn * gsize + (tm - first);
+}
+__global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ upart, int tiles_m, int tiles_n,
+                                                     int group, int full, int P, int64_t V, float* __restrict__ dbias) {
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= V) return;
+  const int tm = (int)(v / BM), tn = (int)((v % BM) / 32), m = (int)(v % 32);
+  const int64_t T = (int64_t)tiles_m * tiles_n;
+  const int lin = lin_of(tm, tn, tiles_m, tiles_n, group);
+  float s = 0.f;
+  if (lin < full) {
+    s = upart[(int64_t)lin * 32 + m];
+  } else {
+    for (int p = 0; p < P; ++p) s += upart[(T + (int64_t)(lin - full) * P + p) * 32 + m];
+  }
+  dbias[v] = s;
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1624,7 +1638,7 @@ int launch_status();
 template <bool OUT_BF16>
 int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t Nc, int group, void* C, int64_t ldc,
                 float* part, hipStream_t st, const float* rscale = nullptr, const float* go = nullptr,
-                const uint16_t* u = nullptr, float* upart = nullptr, int64_t ldu = 0, int* p_out = nullptr) {
+                const uint16_t* u = nullptr, float* upart = nullptr, int* p_out = nullptr, int* full_out = nullptr) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nc, BN), T = tiles_m * tiles_n;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
@@ -1640,29 +1654,30 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   const dim3 grid(full + (T - full) * P);
   if (B.cm) return MCE_EINVAL;  // only the A operand may be in the piece layout
   if (p_out) *p_out = P;
+  if (full_out) *full_out = full;
   if (u != nullptr) {
     // dot products with u: only for an A operand in the piece layout (G^T), fp32 output
     if (!A.cm || OUT_BF16 || upart == nullptr) return MCE_EINVAL;
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart, ldu);
+                         tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart, ldu);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart);
   } else if (A.cm) {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
   } else {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr, 0);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
   }
   int rc = launch_status();
   if (rc || full == T) return rc;
@@ -1791,12 +1806,12 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
 }
 
 // Training-path workspace: the backward workspace (G and Gt hold E', the transposed copies, partials), the
-// forward workspace after it, then e_n, a_n, go*a_n in bf16 (kperm order), the flags and the flagged-row list,
-// all [Np], and the counter.
+// forward workspace after it, then e_n, a_n, go*a_n in bf16 (kperm order) (all [Np]), the dW blocks' dBias
+// partials, the flags and the flagged-row list ([Np]), and the counter.
 struct TrainWs {
   BwdWs b;
   FwdWs f;
-  float *lse_est, *arow;
+  float *lse_est, *arow, *upart;
   uint16_t* uperm;
   int *flag, *flag_list, *flag_count;
   size_t bytes;
@@ -1811,6 +1826,9 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.lse_est = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
   w.arow = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
   w.uperm = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * np);
+  // dW blocks' dBias partials: 32 values per tile of the dW grid and per tail K slice
+  w.upart = reinterpret_cast<float*>(base + off);
+  off = align256(off + sizeof(float) * 32 * ((w.b.vp / BM) * cdiv(K, BN) + TAIL_SLOTS));
   w.flag = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
   w.flag_list = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
   w.flag_count = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
@@ -1915,25 +1933,25 @@ int bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N
   const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   if (dW) {
-    // H^T scaled by go*a (and, for dBias, go*a itself in bf16); dW = E'^T (go a . H), and the first tile column
-    // also forms dBias partials sum_n E'[n, v] go a_n (one row per K slice of the split tail tiles)
+    // H^T scaled by go*a (and, for dBias, go*a itself in bf16); dW = E'^T (go a . H), and the blocks also form
+    // the dBias partials sum_n E'[n, v] go a_n, each over its share of the K stages (k_dbias_tiles adds them)
     hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.b.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st,
                        H, ldh, N, K, w.b.Ht, w.arow, go, dBias ? w.uperm : nullptr);
     if ((rc = launch_status())) return rc;
     const Operand Aop{w.b.Gt, 0, V, w.b.np, w.b.vp * BLK, 1};
     const Operand Bop{w.b.Ht, BLK, K, w.b.np, K * BLK, 0};
-    int P = 1;
+    int P = 1, full = 0;
+    const bool fold = dBias != nullptr && cdiv(K, BN) >= 8;  // the dW tiles form dBias (8 row groups per tile row)
     if ((rc = launch_gemm<false>(Aop, Bop, (int)(w.b.np / BK), V, K, 4, dW, lddw, w.b.part, st, nullptr, nullptr,
-                                 dBias ? w.uperm : nullptr, w.b.dbias_part, w.b.vp, &P)))
+                                 fold ? w.uperm : nullptr, w.upart, &P, &full)))
       return rc;
-    if (dBias) {
-      hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.b.dbias_part, P, w.b.vp,
-                         V, dBias);
+    if (fold) {
+      hipLaunchKernelGGL(k_dbias_tiles, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.upart, (int)cdiv(V, BM),
+                         (int)cdiv(K, BN), 4, full, P, V, dBias);
       return launch_status();
     }
-    return MCE_OK;
   }
-  if (dBias) {  // dBias without dW: a pass over G^T
+  if (dBias) {  // dBias without dW, or K < 1793: a pass over G^T
     const int nt = (int)(w.b.np / BM);
     const int per = (int)cdiv(nt, DBIAS_SPLITS);
     const int splits = (int)cdiv(nt, per);

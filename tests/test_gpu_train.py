@@ -27,6 +27,8 @@ SHAPES = [
     (1, 64, 300, 257, True),
     (777, 520, 2051, 2000, True),
     (64, 2064, 1024, None, False),
+    (300, 2048, 1300, 1290, True),     # K >= 1793: dBias formed inside the dW GEMM
+    (300, 2048, 9000, 8990, True),     # ... with a K-split tail in the dW grid (36 x 8 tiles)
 ]
 
 
