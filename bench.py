@@ -43,12 +43,12 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 # (default): mce_fwd_train, mce_bwd_train_dhidden, mce_bwd_train_dweight; recompute path: mce_fwd,
 # mce_bwd_logits_grad, mce_bwd_dhidden, mce_bwd_dweight.
 STAGE_OF_CALL = {"mce_fwd_train": ("fwd", "k_fwd_train<true>"),
-                 "mce_bwd_train_dhidden": ("dhidden", "k_gemm<true, true, true>"),
-                 "mce_bwd_train_dweight": ("dweight", "k_gemm<false, true, true>"),
+                 "mce_bwd_train_dhidden": ("dhidden", "k_gemm<true, true, true, false>"),
+                 "mce_bwd_train_dweight": ("dweight", "k_gemm<false, true, true, true>"),
                  "mce_fwd": ("fwd", "k_fwd_tiles<true>"),
                  "mce_bwd_logits_grad": ("logits_grad", "k_bwd_grad<true>"),
-                 "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true>"),
-                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true>")}
+                 "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true, false>"),
+                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, false>")}
 
 
 def _args():
