@@ -1258,56 +1258,62 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   }
 }
 
-// Exact E' rows of the flagged rows (a grid-stride loop over flag_list, one row per workgroup at a time):
-// x_v = b_v + h_n . w_v (fp32 sums of the bf16 products; -inf for v >= V_real) for every v < Vp, then
-// E'[n, v] = exp(x_v - lse_n) - [v = y_n] into G and Gt. h_n is staged in LDS 16384 values at a time; thread t
-// takes v = v0 + t. This is the fallback for rows whose logits exceed e_n by about 44 or more, which the bound
-// from the first vocabulary tile and the target makes rare; it reads all of W once per flagged row.
+// Exact E' rows of the flagged rows: work item i = (flagged row flag_list[i / tiles_v], vocabulary tile
+// i % tiles_v), a grid-stride loop over the items, so even one flagged row is spread over many workgroups. For
+// the item's 256 vocabulary rows v (thread t: v = v0 + t): x_v = b_v + h_n . w_v (fp32 sums of the bf16 products;
+// -inf for v >= V_real), E'[n, v] = exp(x_v - lse_n) - [v = y_n] into G and Gt. h_n is staged in LDS 16384 values
+// at a time. This is the fallback for rows whose logits exceed e_n by about 44 or more, which the bound from the
+// first vocabulary tile and the target makes rare; it reads all of W once per flagged row.
 constexpr int REPAIR_KC = 16384;
 __global__ __launch_bounds__(256) void k_repair(const uint16_t* __restrict__ H, int64_t ldh,
                                                 const uint16_t* __restrict__ W, int64_t ldw,
                                                 const float* __restrict__ bias, const int64_t* __restrict__ y,
-                                                const float* __restrict__ lse_rows, int64_t K, int64_t V, int64_t Vp,
+                                                const float* __restrict__ lse_rows,
+                                                const float* __restrict__ wgt_rows, int64_t K, int64_t V, int64_t Vp,
                                                 int64_t Vreal, int64_t Np, const int* __restrict__ flag_count,
                                                 const int* __restrict__ flag_list, uint16_t* __restrict__ G,
                                                 uint16_t* __restrict__ Gt) {
   __shared__ __attribute__((aligned(16))) uint16_t hs[REPAIR_KC];
-  const int cnt = *flag_count;
+  const int tiles_v = (int)(Vp / BM);
+  const int64_t items = (int64_t)(*flag_count) * tiles_v;
   const int t = threadIdx.x;
   const int nkc = (int)((K + REPAIR_KC - 1) / REPAIR_KC);
-  for (int i = blockIdx.x; i < cnt; i += gridDim.x) {
-    const int64_t n = flag_list[i];
+  for (int64_t i = blockIdx.x; i < items; i += gridDim.x) {
+    const int64_t n = flag_list[i / tiles_v];
+    const int64_t v = (i % tiles_v) * BM + t;
     const float l = lse_rows[n];
     const int64_t yn = y[n];
-    for (int64_t v0 = 0; v0 < Vp; v0 += 256) {
-      const int64_t v = v0 + t;
-      float x = 0.f;
-      for (int kc = 0; kc < nkc; ++kc) {
-        const int64_t k0 = (int64_t)kc * REPAIR_KC;
-        const int kn = (int)((K - k0) < REPAIR_KC ? (K - k0) : REPAIR_KC);
-        if (v0 == 0 || nkc > 1) {
-          __syncthreads();
-          for (int k = t * 8; k < kn; k += 256 * 8)
-            *reinterpret_cast<u16x8*>(hs + k) = *reinterpret_cast<const u16x8*>(H + n * ldh + k0 + k);
-          __syncthreads();
-        }
-        if (v < V) {
-          const uint16_t* wr = W + v * ldw + k0;
-          for (int k = 0; k < kn; k += 8) {
-            const u16x8 a = *reinterpret_cast<const u16x8*>(hs + k);
-            const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
+    // a row with wgt = 0 (under the clamp, or all its probability on the pointer) has a zero gradient: its E'
+    // row only has to be finite, so it is zeroed without the dot products
+    if (!(wgt_rows[n] != 0.f)) {
+      G[cm_index(n, v, Np)] = 0;
+      Gt[cm_index(v, n, Vp)] = 0;
+      continue;
+    }
+    float x = 0.f;
+    for (int kc = 0; kc < nkc; ++kc) {
+      const int64_t k0 = (int64_t)kc * REPAIR_KC;
+      const int kn = (int)((K - k0) < REPAIR_KC ? (K - k0) : REPAIR_KC);
+      __syncthreads();
+      for (int k = t * 8; k < kn; k += 256 * 8)
+        *reinterpret_cast<u16x8*>(hs + k) = *reinterpret_cast<const u16x8*>(H + n * ldh + k0 + k);
+      __syncthreads();
+      if (v < V) {
+        const uint16_t* wr = W + v * ldw + k0;
+        for (int k = 0; k < kn; k += 8) {
+          const u16x8 a = *reinterpret_cast<const u16x8*>(hs + k);
+          const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[e]), x);
-          }
+          for (int e = 0; e < 8; ++e) x = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[e]), x);
         }
       }
-      float g = 0.f;
-      if (v < Vreal) g = expf(x + (bias != nullptr ? bias[v] : 0.f) - l);
-      if (v == yn) g -= 1.f;
-      const uint16_t b = to_bf16(g);
-      G[cm_index(n, v, Np)] = b;
-      Gt[cm_index(v, n, Vp)] = b;
     }
+    float g = 0.f;
+    if (v < Vreal) g = expf(x + (bias != nullptr ? bias[v] : 0.f) - l);
+    if (v == yn) g -= 1.f;
+    const uint16_t b = to_bf16(g);
+    G[cm_index(n, v, Np)] = b;
+    Gt[cm_index(v, n, Vp)] = b;
   }
 }
 
@@ -1837,7 +1843,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
 }
 
 float g_train_s_max = TRAIN_S_MAX;
-constexpr int REPAIR_BLOCKS = 256;
+constexpr int REPAIR_BLOCKS = 1024;
 
 // Forward of the one-pass training path (mixture or plain cross-entropy, no sparse bias): the per-row outputs of
 // fwd_impl plus E' in the workspace's G / Gt and a_n.
@@ -1891,8 +1897,8 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
                      lse_rows, wgt_rows, w.flag, N, w.b.np, w.b.vp, V_real, w.arow, w.flag_count, w.flag_list, w.b.G,
                      w.b.Gt);
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, y, lse_rows, K, V,
-                     w.b.vp, V_real, w.b.np, w.flag_count, w.flag_list, w.b.G, w.b.Gt);
+  hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, y, lse_rows, wgt_rows, K,
+                     V, w.b.vp, V_real, w.b.np, w.flag_count, w.flag_list, w.b.G, w.b.Gt);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.f.loss_part, (int64_t)cdiv(N, 32), loss_sum);
   return launch_status();

@@ -56,6 +56,17 @@ def test_forced_fallback_every_row(shape):
     assert_parity(got, fwd, bwd, f"forced fallback {shape}")
 
 
+def test_forced_fallback_with_clamped_rows():
+    """Every row flagged on a case with rows under the 1e-30 clamp (wgt = 0): those rows' E' is zeroed without the
+    dot-product pass, the others recomputed exactly."""
+    case = random_case(64, 64, 512, None, False, seed=9, w_scale=3.0, gate_mode="zero")
+    got = capi_train(case, s_max=1e-30)
+    fwd, bwd = oracle_of(case)
+    assert got["flagged"] == 64
+    assert (~(fwd["P"] >= 1e-30)).sum() > 0, "case must contain clamped rows"
+    assert_parity(got, fwd, bwd, "forced fallback, clamped rows")
+
+
 def _peaked_case(n=600, k=128, v=1500, rows=(3, 4, 100, 255, 256, 599), seed=17):
     """Rows `rows` carry h[:, 0] = 150 against vocabulary rows 1000 and 1001, the only ones with a nonzero first
     coordinate (0.5 and 2/15): their logits ~75 and ~20. The target is 1001 and the gate 0, so py ~ e^-55 stays
