@@ -548,6 +548,11 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   __syncthreads();
 }
 
+// Tile-rows per group of the logits tile kernels (k_fwd_tiles, k_bwd_grad, k_fwd_train): an XCD's 32 resident tiles
+// are then 4 vocabulary tiles x 8 row tiles, whose 4 W panels stay the same for many consecutive waves (measured:
+// 0.14 ms faster per pass than 8 x 4 at config 2).
+constexpr int FWD_GROUP = 4;
+
 // Block id -> (tile_m, tile_n). Workgroups are dispatched round-robin over the 8 XCDs (block b on XCD b%8);
 // the remap gives each XCD a contiguous range of logical tiles, and the logical order walks groups of
 // `group` tile-rows column by column, so the tiles resident on one XCD share A and B panels in its L2.
@@ -591,7 +596,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
                  int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + BM * 4];
   int tm, tn;
-  tile_coords(tiles_v, tiles_n, 8, tm, tn);
+  tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
@@ -947,7 +952,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
                 uint16_t* __restrict__ Gt, float* __restrict__ dbias_part) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   int tm, tn;
-  tile_coords(tiles_v, tiles_n, 8, tm, tn);
+  tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
@@ -1155,7 +1160,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
                  float* __restrict__ part_s, int* __restrict__ flag) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   int tm, tn;
-  tile_coords(tiles_v, tiles_n, 8, tm, tn);
+  tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
