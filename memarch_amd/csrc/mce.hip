@@ -304,19 +304,20 @@ __device__ __forceinline__ void sched_slice() {
   }
 }
 
-// Dot products of one 32-row group of the A operand with a vector u over the reduction index (gemm_tile<.., DB>):
-// sum_k A(m, k) u(k) for the rows m of group `rg` of the tile. In every stage, wave w takes slice w (16 K
-// positions) of that group: one extra A fragment read and one read of the slice's u values (the lane's 8 of
-// them), then four v_dot2c_f32_bf16; every wave and tile runs the same instructions, so the work adds a small,
+// Dot products of NR 32-row groups of the A operand with a vector u over the reduction index (gemm_tile<.., DB = NR>):
+// sum_k A(m, k) u(k) for the rows m of groups rg_0 .. rg_{NR-1} of the tile. In every stage, wave w takes slice w
+// (16 K positions) of each group: NR extra A fragment reads and one read of the slice's u values (the lane's 8 of
+// them), then 4 NR v_dot2c_f32_bf16; every wave and tile runs the same instructions, so the work adds a small,
 // even cost to every stage. u arrives through LDS: 64 bf16 values per stage (the slot of ring buffer b at
 // APOFF + 1024 b, written by one load instruction of wave 0).
 constexpr int APOFF = LDS_BYTES;
+template <int NR>
 struct DotState {
-  i32x4 rsrc;       // u, bf16
-  uint32_t faddr;   // LDS byte offset of this lane's fragment (group rg, slice = wave) in the A image of buffer 0
-  uint32_t uaddr;   // LDS byte offset of this lane's 8 u values (slice = wave) in the slot of buffer 0
-  bf16x8 x, u;      // the fragment and u values read for this stage
-  float acc;        // row rg*32 + lane%32, K positions of lane half lane/32 of slice `wave` of every stage
+  i32x4 rsrc;         // u, bf16
+  uint32_t faddr[NR]; // LDS byte offsets of this lane's fragments (group rg_j, slice = wave), A image of buffer 0
+  uint32_t uaddr;     // LDS byte offset of this lane's 8 u values (slice = wave) in the slot of buffer 0
+  bf16x8 x[NR], u;    // the fragments and u values read for this stage
+  float acc[NR];      // row rg_j*32 + lane%32, K positions of lane half lane/32 of slice `wave` of every stage
 };
 // c + a[2q] u[2q] + a[2q+1] u[2q+1] (the pairs taken with shufflevector: a bit_cast of one 32-bit element of a
 // vector loses the element index in this compiler)
@@ -332,46 +333,60 @@ __device__ __forceinline__ float dot8(const bf16x8& a, const bf16x8& u, float c)
 // it to the end of the loop body).
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 // Wave 0's load of u[stage*64 .. +63] into the slot of ring buffer `slot` (lanes 8..63 write zeros).
-__device__ __forceinline__ void issue_ap(const DotState& dp, int stage, int send, char* lds, int slot) {
+__device__ __forceinline__ void issue_ap(const i32x4& rsrc, int stage, int send, char* lds, int slot) {
   const int lane = threadIdx.x & 63;
   const int off = (stage < send && lane < 8) ? stage * 128 + lane * 16 : OOB;
-  buffer_load_lds(dp.rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
+  buffer_load_lds(rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
 }
-// Slice 1 with the two extra reads first; slice 2 with the four dot products between its first MFMAs.
+// Slice 1 with the NR + 1 extra reads first; slice 2 with the 4 NR dot products, NR between each of its first MFMA
+// pairs.
+template <int NR>
 __device__ __forceinline__ void sched_slice_rd2() {
-  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, NR + 1, 0);
   sched_slice();
 }
+template <int NR, int I_>
+__device__ __forceinline__ void sched_dot_pair() {
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+  __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+  if constexpr (I_ < 4) __builtin_amdgcn_sched_group_barrier(SG_VALU, NR, 0);
+  __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+}
+template <int NR>
 __device__ __forceinline__ void sched_slice_dot() {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-    if (i < 4) __builtin_amdgcn_sched_group_barrier(SG_VALU, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-  }
+  sched_dot_pair<NR, 0>();
+  sched_dot_pair<NR, 1>();
+  sched_dot_pair<NR, 2>();
+  sched_dot_pair<NR, 3>();
+  sched_dot_pair<NR, 4>();
+  sched_dot_pair<NR, 5>();
+  sched_dot_pair<NR, 6>();
+  sched_dot_pair<NR, 7>();
 }
 
 // A slice without loads: reads of slice RK of buffer RBUF into (da, db), the 16 MFMAs of (ua, ub), interleaved by
 // the compiler one read per two MFMAs.
-template <int RBUF, int RK, bool DB = false>
+template <int RBUF, int RK, int DB = 0>
 __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
-                                            DotState* dp = nullptr) {
-  if constexpr (DB && RK == 2) {
-    // slice 1 of the stage (reads slice 2): this wave's extra fragment and u values of the stage's buffer
-    dp->x = frag_at<AOFF + RBUF * I::OPB>(lds, dp->faddr);
+                                            DotState<DB ? DB : 1>* dp = nullptr) {
+  if constexpr (DB > 0 && RK == 2) {
+    // slice 1 of the stage (reads slice 2): this wave's extra fragments and u values of the stage's buffer
+#pragma unroll
+    for (int j = 0; j < DB; ++j) dp->x[j] = frag_at<AOFF + RBUF * I::OPB>(lds, dp->faddr[j]);
     dp->u = frag_at<APOFF + RBUF * 1024>(lds, dp->uaddr);
     read_frags<RBUF, RK>(lds, ad, da, db);
     mma16(acc, ua, ub);
-    sched_slice_rd2();
-  } else if constexpr (DB && RK == 3) {
-    // slice 2 of the stage (reads slice 3): the dot products of the fragment read in slice 1
+    sched_slice_rd2<DB>();
+  } else if constexpr (DB > 0 && RK == 3) {
+    // slice 2 of the stage (reads slice 3): the dot products of the fragments read in slice 1
     read_frags<RBUF, RK>(lds, ad, da, db);
     mma16(acc, ua, ub);
-    dp->acc = dot8(dp->x, dp->u, dp->acc);
-    sched_slice_dot();
-    pin(dp->acc);
+#pragma unroll
+    for (int j = 0; j < DB; ++j) dp->acc[j] = dot8(dp->x[j], dp->u, dp->acc[j]);
+    sched_slice_dot<DB>();
+#pragma unroll
+    for (int j = 0; j < DB; ++j) pin(dp->acc[j]);
   } else {
     read_frags<RBUF, RK>(lds, ad, da, db);
     mma16(acc, ua, ub);
@@ -416,10 +431,10 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
 //   wait for this wave's loads of stage kt+1, barrier: every wave has read all of stage kt and stage kt+1 landed;
 //   slice 3: MFMAs on slice 3, reads of slice 0 of stage kt+1 (NB), loads of stage kt+2's A operand into CB.
 // A stage's loads are thus split in two halves, one load per two MFMAs, landing over three slices of MFMAs.
-template <int CB, bool KF, bool DB = false>
+template <int CB, bool KF, int DB = 0>
 __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4][4], bf16x8 (&fa)[2][4],
                                            bf16x8 (&fb)[2][4], char* lds, const FragAddr& ad, const Stream& sa,
-                                           const Stream& sb, int wave, DotState* dp = nullptr) {
+                                           const Stream& sb, int wave, DotState<DB ? DB : 1>* dp = nullptr) {
   constexpr int NB = CB ^ 1;
   {
     const StageSrc gb = stage_src(sb, stage + 1, send);
@@ -433,8 +448,8 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
     const StageSrc ga = stage_src(sa, stage + 2, send);
     slice_loads<NB, 0, false, CB, KF>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
   }
-  if constexpr (DB) {
-    if (wave == 0) issue_ap(*dp, stage + 2, send, lds, CB);
+  if constexpr (DB > 0) {
+    if (wave == 0) issue_ap(dp->rsrc, stage + 2, send, lds, CB);
   }
 }
 
@@ -481,10 +496,11 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool BIAS = false, bool APC = false, bool DB = false>
+template <bool KF, bool BIAS = false, bool APC = false, int DB = 0>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
-                                          int64_t Vreal = 0, DotState* dp = nullptr, int rg = 0) {
+                                          int64_t Vreal = 0, DotState<DB ? DB : 1>* dp = nullptr, int rg0 = 0,
+                                          int rg_step = 8) {
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
@@ -505,21 +521,27 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
   issue_stage(sa, s0, send, lds, AOFF, wave);
   issue_stage(sb, s0, send, lds, BOFF, wave);
-  if constexpr (DB) {
-    // this lane's extra fragment: row rg*32 + lane%32, 16-byte chunk 2*wave + lane/32 of the stage (slice = wave)
-    const int ra = rg * 32 + (lane & 31), c = 2 * wave + (lane >> 5);
-    if constexpr (APC)
-      dp->faddr = (ra >> 3) * 1024 + ((c ^ ((ra >> 3) & 1)) << 7) + (ra & 7) * 16;
-    else
-      dp->faddr = ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
+  if constexpr (DB > 0) {
+    // this lane's extra fragments: rows rg_j*32 + lane%32 (rg_j = rg0 + j*rg_step), 16-byte chunk 2*wave + lane/32
+    // of the stage (slice = wave)
+#pragma unroll
+    for (int j = 0; j < DB; ++j) {
+      int rg = rg0 + j * rg_step;
+      if (rg > 7) rg = rg0;  // a group past the tile's 8 (tiles_n = 3, 5, 6, 7): computed, never read
+      const int ra = rg * 32 + (lane & 31), c = 2 * wave + (lane >> 5);
+      if constexpr (APC)
+        dp->faddr[j] = (ra >> 3) * 1024 + ((c ^ ((ra >> 3) & 1)) << 7) + (ra & 7) * 16;
+      else
+        dp->faddr[j] = ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
+      dp->acc[j] = 0.f;
+    }
     dp->uaddr = 32 * wave + 16 * (lane >> 5);
-    dp->acc = 0.f;
     // u of stage s0 before the A loads of stage s0+1, so the wait below covers it
-    if (wave == 0) issue_ap(*dp, s0, send, lds, 0);
+    if (wave == 0) issue_ap(dp->rsrc, s0, send, lds, 0);
   }
   issue_stage(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
-  if constexpr (DB) {
-    if (wave == 0) issue_ap(*dp, s0 + 1, send, lds, 1);
+  if constexpr (DB > 0) {
+    if (wave == 0) issue_ap(dp->rsrc, s0 + 1, send, lds, 1);
   }
   if constexpr (BIAS) stash_bias(bslot, btile, m0, Vreal);
   wait_vmcnt<I::LPW>();  // with DB, wave 0's u of stage s0 precedes its last 8 loads
@@ -1422,19 +1444,19 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 
 // ---------------------------------------------------------------------------------------------------------
 // Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
-// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB (tiles_n >= 8): block
-// of tile (tm, tn < 8) also forms sum_k A(m, k) u(k) (u bf16 over the K positions) for the rows m of its 32-row
-// group tn, over its K range: one 32-value partial per block (k_dbias_tiles adds them up). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
-// order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
+// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB > 0 (= fold_nr(tiles_n)):
+// block of tile (tm, tn < 8) also forms sum_k A(m, k) u(k) (u bf16 over the K positions) for the rows m of its
+// 32-row groups tn, tn + tiles_n, .. (DB of them), over its K range: DB 32-value partials per block (k_dbias_tiles
+// adds them up). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16, bool KF, bool APC, bool DB>
+template <bool OUT_BF16, bool KF, bool APC, int DB>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part,
             const float* __restrict__ rscale, const float* __restrict__ go, const uint16_t* __restrict__ u,
             float* __restrict__ upart) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (DB ? 2048 : 0)];
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (DB > 0 ? 2048 : 0)];
   const int b = (int)blockIdx.x;
   int lin, s0 = 0, nk = nk_total, slot = -1;
   if (b < full) {
@@ -1453,22 +1475,28 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
   f32x16 acc[4][4];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
-  if constexpr (DB) {
-    // the tile also forms sum_k A(m, k) u(k) for its row group tn (rows tn*32 .. +31; requires tiles_n >= 8, so
-    // the row groups of a tile row are covered by its first 8 tiles), over its K range: written to
-    // upart[lin * 32 ..] for a whole tile, upart[(tiles_m * tiles_n + q) * 32 ..] for K slice q of the split tail
-    DotState dp;
+  if constexpr (DB > 0) {
+    // the tile also forms sum_k A(m, k) u(k) for its DB row groups rg_j = tn + j*tiles_n (rows rg_j*32 .. +31;
+    // DB = 8 / tiles_n, or 1 with tiles_n >= 8, so the 8 groups of a tile row are covered by its tiles), over its
+    // K range: written to upart[(lin*DB + j) * 32 ..] for a whole tile, upart[((T + q)*DB + j) * 32 ..] for K slice
+    // q of the split tail (T = tiles_m * tiles_n)
+    DotState<DB> dp;
     dp.rsrc = make_rsrc(reinterpret_cast<uint64_t>(u));
-    const int rg = tn < 8 ? tn : 0;
-    gemm_tile<KF, false, APC, true>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, rg);
-    // lanes l and l+32 hold the two K halves of row rg*32 + l%32; the four waves hold the four slices
-    float d = dp.acc + __shfl_xor(dp.acc, 32);
+    const bool active = tn < 8;  // tiles_n > 8: the tiles past the 8th column have no group
+    gemm_tile<KF, false, APC, DB>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, active ? tn : 0, tiles_n);
+    // lanes l and l+32 hold the two K halves of row rg_j*32 + l%32; the four waves hold the four slices
     float* red = reinterpret_cast<float*>(lds);
-    if (lh == 0) red[wave * 32 + lr] = d;
+#pragma unroll
+    for (int j = 0; j < DB; ++j) {
+      const float d = dp.acc[j] + __shfl_xor(dp.acc[j], 32);
+      if (lh == 0) red[(j * 4 + wave) * 32 + lr] = d;
+    }
     __syncthreads();
-    if (t < 32 && tn < 8) {
-      const int64_t row = slot >= 0 ? (int64_t)tiles_m * tiles_n + slot : lin;
-      upart[row * 32 + t] = (red[t] + red[32 + t]) + (red[64 + t] + red[96 + t]);
+    if (t < 32 * DB && active) {
+      const int j = t >> 5, r = t & 31;
+      const int64_t row = (slot >= 0 ? (int64_t)tiles_m * tiles_n + slot : lin) * DB + j;
+      const float* rj = red + j * 128;
+      upart[row * 32 + r] = (rj[r] + rj[32 + r]) + (rj[64 + r] + rj[96 + r]);
     }
   } else {
     gemm_tile<KF, false, APC>(A, B, s0, nk, m0, n0, lds, acc);
@@ -1541,25 +1569,28 @@ __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ p
   }
 }
 
-// dBias of the training path from the dW blocks' dot-product partials (k_gemm<.., DB>): dbias[v] = the partial of
-// tile (v/256, tn = (v%256)/32) at row v%32 -- or, for a tile of the split tail, the sum of its P K-slice partials
-// in a fixed order. One thread per v.
+// dBias of the training path from the dW blocks' dot-product partials (k_gemm<.., DB>): row group rg = (v%256)/32
+// of tile row v/256 belongs to tile column tn = rg % tiles_n as its group j = rg / tiles_n; dbias[v] = that
+// partial at row v%32 -- or, for a tile of the split tail, the sum of its P K-slice partials in a fixed order. One
+// thread per v.
 __device__ __forceinline__ int lin_of(int tm, int tn, int tiles_m, int tiles_n, int group) {
   const int g = tm / group, first = g * group, gsize = min(tiles_m - first, group);
   return g * group * tiles_n + tn * gsize + (tm - first);
 }
 __global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ upart, int tiles_m, int tiles_n,
-                                                     int group, int full, int P, int64_t V, float* __restrict__ dbias) {
+                                                     int nr, int group, int full, int P, int64_t V,
+                                                     float* __restrict__ dbias) {
   const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (v >= V) return;
-  const int tm = (int)(v / BM), tn = (int)((v % BM) / 32), m = (int)(v % 32);
+  const int tm = (int)(v / BM), rg = (int)((v % BM) / 32), m = (int)(v % 32);
+  const int tn = rg % tiles_n, j = rg / tiles_n;
   const int64_t T = (int64_t)tiles_m * tiles_n;
   const int lin = lin_of(tm, tn, tiles_m, tiles_n, group);
   float s = 0.f;
   if (lin < full) {
-    s = upart[(int64_t)lin * 32 + m];
+    s = upart[((int64_t)lin * nr + j) * 32 + m];
   } else {
-    for (int p = 0; p < P; ++p) s += upart[(T + (int64_t)(lin - full) * P + p) * 32 + m];
+    for (int p = 0; p < P; ++p) s += upart[((T + (int64_t)(lin - full) * P + p) * nr + j) * 32 + m];
   }
   dbias[v] = s;
 }
@@ -1569,6 +1600,9 @@ __global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ u
 int g_last_hip_error = 0;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// Row groups per tile for the dot products of k_gemm<.., DB> over a grid `tiles_n` tiles wide: the 8 row groups of a
+// tile row are spread over its first min(tiles_n, 8) tiles.
+inline int fold_nr(int64_t tiles_n) { return tiles_n >= 8 ? 1 : (int)cdiv(8, tiles_n); }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -1667,27 +1701,43 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (p_out) *p_out = P;
   if (full_out) *full_out = full;
   if (u != nullptr) {
-    // dot products with u: only for an A operand in the piece layout (G^T), fp32 output
-    if (!A.cm || OUT_BF16 || upart == nullptr) return MCE_EINVAL;
-    if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m,
-                         tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart);
-    else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart);
+    // dot products with u: only for an A operand in the piece layout (G^T), fp32 output; with more than one row
+    // group per tile only for whole K stages
+    const int nr = fold_nr(tiles_n);
+    if constexpr (OUT_BF16) {
+      return MCE_EINVAL;
+    } else {
+      if (!A.cm || upart == nullptr || (nr > 1 && !kf)) return MCE_EINVAL;
+#define MCE_GEMM_DB(KF_, NR_)                                                                                \
+  hipLaunchKernelGGL((k_gemm<false, KF_, true, NR_>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, \
+                     tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart)
+      if (!kf)
+        MCE_GEMM_DB(false, 1);
+      else if (nr == 1)
+        MCE_GEMM_DB(true, 1);
+      else if (nr == 2)
+        MCE_GEMM_DB(true, 2);
+      else if (nr == 3)
+        MCE_GEMM_DB(true, 3);
+      else if (nr == 4)
+        MCE_GEMM_DB(true, 4);
+      else
+        MCE_GEMM_DB(true, 8);
+#undef MCE_GEMM_DB
+    }
   } else if (A.cm) {
     if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
     else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
   } else {
     if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
     else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false, false>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
   }
   int rc = launch_status();
@@ -1839,7 +1889,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.uperm = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * np);
   // dW blocks' dBias partials: 32 values per tile of the dW grid and per tail K slice
   w.upart = reinterpret_cast<float*>(base + off);
-  off = align256(off + sizeof(float) * 32 * ((w.b.vp / BM) * cdiv(K, BN) + TAIL_SLOTS));
+  off = align256(off + sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.b.vp / BM) * cdiv(K, BN) + TAIL_SLOTS));
   w.flag = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
   w.flag_list = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
   w.flag_count = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
@@ -1952,17 +2002,17 @@ int bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N
     const Operand Aop{w.b.Gt, 0, V, w.b.np, w.b.vp * BLK, 1};
     const Operand Bop{w.b.Ht, BLK, K, w.b.np, K * BLK, 0};
     int P = 1, full = 0;
-    const bool fold = dBias != nullptr && cdiv(K, BN) >= 8;  // the dW tiles form dBias (8 row groups per tile row)
+    const bool fold = dBias != nullptr;  // the dW tiles form dBias
     if ((rc = launch_gemm<false>(Aop, Bop, (int)(w.b.np / BK), V, K, 4, dW, lddw, w.b.part, st, nullptr, nullptr,
                                  fold ? w.uperm : nullptr, w.upart, &P, &full)))
       return rc;
     if (fold) {
       hipLaunchKernelGGL(k_dbias_tiles, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.upart, (int)cdiv(V, BM),
-                         (int)cdiv(K, BN), 4, full, P, V, dBias);
+                         (int)cdiv(K, BN), fold_nr(cdiv(K, BN)), 4, full, P, V, dBias);
       return launch_status();
     }
   }
-  if (dBias) {  // dBias without dW, or K < 1793: a pass over G^T
+  if (dBias) {  // dBias without dW: a pass over G^T
     const int nt = (int)(w.b.np / BM);
     const int per = (int)cdiv(nt, DBIAS_SPLITS);
     const int splits = (int)cdiv(nt, per);

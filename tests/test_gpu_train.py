@@ -27,8 +27,12 @@ SHAPES = [
     (1, 64, 300, 257, True),
     (777, 520, 2051, 2000, True),
     (64, 2064, 1024, None, False),
-    (300, 2048, 1300, 1290, True),     # K >= 1793: dBias formed inside the dW GEMM
+    (300, 2048, 1300, 1290, True),     # 8 dW tile columns: one row group of dBias per tile
     (300, 2048, 9000, 8990, True),     # ... with a K-split tail in the dW grid (36 x 8 tiles)
+    (300, 1024, 5000, 4990, True),     # 4 dW tile columns: 2 row groups of dBias per tile
+    (300, 1024, 17000, 16990, True),   # ... with a K-split tail (67 x 4 tiles)
+    (200, 392, 700, None, True),       # 2 tile columns: 4 row groups per tile
+    (200, 1600, 800, None, True),      # 7 tile columns: 2 row groups per tile, one of them unused
 ]
 
 
