@@ -43,12 +43,19 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 # (default): mce_fwd_train, mce_bwd_train_dhidden, mce_bwd_train_dweight; recompute path: mce_fwd,
 # mce_bwd_logits_grad, mce_bwd_dhidden, mce_bwd_dweight.
 STAGE_OF_CALL = {"mce_fwd_train": ("fwd", "k_fwd_train<true>"),
-                 "mce_bwd_train_dhidden": ("dhidden", "k_gemm<true, true, true, false>"),
-                 "mce_bwd_train_dweight": ("dweight", "k_gemm<false, true, true, true>"),
+                 "mce_bwd_train_dhidden": ("dhidden", "k_gemm<true, true, true, 0>"),
+                 "mce_bwd_train_dweight": ("dweight", "k_gemm<false, true, true, {nr}>"),
                  "mce_fwd": ("fwd", "k_fwd_tiles<true>"),
                  "mce_bwd_logits_grad": ("logits_grad", "k_bwd_grad<true>"),
-                 "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true, false>"),
-                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, false>")}
+                 "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true, 0>"),
+                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, 0>")}
+
+
+def fold_nr(d):
+    """Row groups of dBias per dW tile (the last template argument of the dW kernel): the 8 32-row groups of a
+    256-row tile row are spread over its first min(tiles, 8) tile columns, tiles = ceil(d / 256)."""
+    tiles = -(-d // 256)
+    return 1 if tiles >= 8 else -(-8 // tiles)
 
 
 def _args():
@@ -300,7 +307,7 @@ def main():
         assert name == name1 and ph0 == "begin" and ph1 == "end"
         stage, kern = STAGE_OF_CALL[name]
         live.setdefault(stage, []).append(e0.elapsed_time(e1))
-        kernel_of[stage] = kern
+        kernel_of[stage] = kern.format(nr=fold_nr(d))
     stages = {k: sum(v) / len(v) for k, v in live.items()}
     tok_s = n / dt
     flops = 6.0 * n * v * d

@@ -1447,7 +1447,8 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 // nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB > 0 (= fold_nr(tiles_n)):
 // block of tile (tm, tn < 8) also forms sum_k A(m, k) u(k) (u bf16 over the K positions) for the rows m of its
 // 32-row groups tn, tn + tiles_n, .. (DB of them), over its K range: DB 32-value partials per block (k_dbias_tiles
-// adds them up). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
+// adds them up). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
+// order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
 template <bool OUT_BF16, bool KF, bool APC, int DB>
