@@ -64,7 +64,7 @@ def gpu_run(case, dev="cuda", h_dtype=torch.bfloat16, go=1.0, biased=None):
         loss = fused_ops.linear_ce_mix(h, w, y, gate, hit)
     (loss * go).backward()
     torch.cuda.synchronize()
-    out = dict(loss=float(loss), dh=h.grad.float().cpu().numpy(), dw=w.grad.float().cpu().numpy(),
+    out = dict(loss=float(loss.detach()), dh=h.grad.float().cpu().numpy(), dw=w.grad.float().cpu().numpy(),
                dgate=gate.grad.float().cpu().numpy())
     out["dbias"] = None if b is None else b.grad.float().cpu().numpy()
     return out

@@ -161,3 +161,35 @@ def test_no_grad_forward_matches_training_forward():
     args[0].requires_grad_()
     l1 = float(fused_ops.linear_ce_mix_biased(*args))
     assert abs(l0 - l1) <= 1e-5 * abs(l0)
+
+
+@pytest.mark.parametrize("recompute", [False, True], ids=["one_pass", "recompute"])
+def test_per_row_logit_offsets(recompute, monkeypatch):
+    """Per-row logit offsets up to +-2000 (the range test_ce_offset.py:43-52 checks for the reference's kernel),
+    through the folded-bias layout of full2.py:1842-1851: h' = [h, s_n, 0 x 15], W' = [W, 1, 0 x 15], so every logit
+    of row n is shifted by s_n (values exact in bf16). The loss and the gradients of h, W and the gate are
+    invariant to such a shift (the softmax null space makes dH's extra column zero up to the bf16 rounding of G), so
+    the shifted run is checked against the oracle of the shifted inputs and against the oracle of the unshifted
+    ones."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", recompute)
+    N, d, V = 300, 128, 1000
+    base = random_case(N, d, V, None, False, seed=77)
+    offsets = torch.tensor([0.0, 2000.0, -2000.0, 1000.0, -1000.0, 500.0, 1536.0, -768.0])[torch.arange(N) % 8]
+    h2 = torch.zeros(N, d + 16)
+    h2[:, :d] = base["h"]
+    h2[:, d] = offsets
+    w2 = torch.zeros(V, d + 16)
+    w2[:, :d] = base["w"]
+    w2[:, d] = 1.0
+    shifted = dict(base, h=h2, w=w2)
+    got = gpu_run(shifted, go=1.0 / N)
+    fwd, bwd = oracle_of(shifted, go=1.0 / N)
+    assert_parity(got, fwd, bwd, f"offsets recompute={recompute}")
+    f0, b0 = oracle_of(base, go=1.0 / N)
+    assert abs(got["loss"] - f0["loss_sum"]) <= 1e-3 * abs(f0["loss_sum"])
+    for key in ("dh", "dw"):
+        ref = b0[key]
+        err = np.linalg.norm(got[key][:, :d] - ref) / np.linalg.norm(ref)
+        print(key, f"vs unshifted {err:.2e}", flush=True)
+        assert err <= 2e-2, (key, err)
