@@ -48,7 +48,13 @@ STAGE_OF_CALL = {"mce_fwd_train": ("fwd", "k_fwd_train<true>"),
                  "mce_fwd": ("fwd", "k_fwd_tiles<true>"),
                  "mce_bwd_logits_grad": ("logits_grad", "k_bwd_grad<true>"),
                  "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true, 0>"),
-                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, 0>")}
+                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, 0>"),
+                 "mce_fwd_sparse": ("fwd", "k_fwd_tiles<true>"),
+                 "mce_bwd_logits_grad_sparse": ("logits_grad", "k_bwd_grad<true>"),
+                 "mce_lse_fwd": ("fwd", "k_fwd_tiles<true>"),
+                 "mce_bwd_lse_grad": ("logits_grad", "k_bwd_grad<true>")}
+# the siblings of the north-star op (--op): the same contractions on the same configuration inputs
+SIBLING_OPS = ("linear_ce", "linear_ce_sparse", "chunk_ce")
 
 
 def fold_nr(d):
@@ -68,8 +74,10 @@ def _args():
     ap.add_argument("--stage-reps", type=int, default=0,
                     help="extra isolated timed repetitions of each C-ABI stage after the timed steps (0: none)")
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
-    ap.add_argument("--op", choices=("fused_ce", "swiglu"), default="fused_ce",
-                    help="fused_ce: the north-star operator (default); swiglu: the SwiGLU gate kernels")
+    ap.add_argument("--op", choices=("fused_ce",) + SIBLING_OPS + ("induct", "swiglu"), default="fused_ce",
+                    help="fused_ce: the north-star operator (default); linear_ce, linear_ce_sparse, chunk_ce: its "
+                         "siblings (fused_ops.py:39-101, full2.py:753-836) on the same inputs; induct: the "
+                         "keys-and-locks producer (full2.py:1499-1535); swiglu: the SwiGLU gate kernels")
     ap.add_argument("--path", choices=("one-pass", "recompute"), default="one-pass",
                     help="one-pass: the logits gradient formed in the forward (default); recompute: the backward "
                          "recomputes the logits")
@@ -140,13 +148,16 @@ def traffic_bytes(kernel, cfg_index):
     return None
 
 
-def cpu_baseline(cfg, rows, chunk=4096):
-    """The oracle's torch restatement of the reference eager formula (full2.py:1917-1929), fp32 fwd+bwd with
+def cpu_baseline(cfg, rows, chunk=4096, op="fused_ce"):
+    """The oracle's torch restatement of the reference eager formula (full2.py:1917-1929; for the siblings the
+    plain, sparse-bias (full2.py:1920-1923) and chunk_ce (full2.py:758-790) forms), fp32 fwd+bwd with
     materialised logits, over the first `rows` rows of the configuration's inputs in chunks of `chunk` rows
     (rows are independent, so the time is linear in rows). Only the compute is timed."""
     from memarch_amd.workloads import make_inputs
-    from oracle.mce_oracle import eager_ce_part
+    from oracle.mce_oracle import eager_ce_part, eager_ce_sparse, eager_chunk_ce
     inp = make_inputs(cfg, rows=rows)
+    if op != "fused_ce":
+        return cpu_baseline_sibling(cfg, inp, rows, chunk, op, eager_ce_part, eager_ce_sparse, eager_chunk_ce)
     w = inp.w.bfloat16().float().requires_grad_()
     b = inp.bias.clone()
     b[cfg.v_real:] = float("-inf")  # padded ids masked, as the GPU path does with v_real
@@ -164,6 +175,92 @@ def cpu_baseline(cfg, rows, chunk=4096):
                 sample=f"first {rows} of {cfg.n} rows of config {cfg.index} (d={cfg.d}, V={cfg.v}), fp32 torch eager "
                        f"fwd+bwd in {chunk}-row chunks, {dt:.1f} s on {torch.get_num_threads()} threads "
                        f"(os.cpu_count()={os.cpu_count()}); rows are independent, so tokens/s holds for all N")
+
+
+def sparse_bias(y, c1, v_real, gen=None):
+    """Three candidates per row for the sparse logit bias: the pointer candidate (0 where none), the target and
+    the next id, with values ~ N(0, 1) (the shape `_induct_raw`'s tongue bias has: 2-3 ids per row)."""
+    cand = torch.stack([c1.clamp(min=0), y, (y + 1) % v_real], 1)
+    val = torch.randn(cand.shape, generator=gen if gen is not None else torch.Generator().manual_seed(7))
+    return cand, val
+
+
+def cpu_baseline_sibling(cfg, inp, rows, chunk, op, eager_ce_part, eager_ce_sparse, eager_chunk_ce):
+    w = inp.w.bfloat16().float().requires_grad_()
+    b = inp.bias.clone()
+    b[cfg.v_real:] = float("-inf")
+    b.requires_grad_()
+    hb = inp.h.bfloat16().float()
+    cand, val = sparse_bias(inp.y, inp.c1, cfg.v_real)
+    dt = 0.0
+    for i in range(0, rows, chunk):
+        h = hb[i:i + chunk].clone().requires_grad_()
+        y = inp.y[i:i + chunk]
+        t0 = time.perf_counter()
+        if op == "linear_ce":
+            loss = eager_ce_part(h, w, None, y, y, torch.zeros(len(y)))
+        elif op == "linear_ce_sparse":
+            v = val[i:i + chunk].clone().requires_grad_()
+            loss = eager_ce_sparse(h, w, None, y, cand[i:i + chunk], v)
+        else:
+            lse, ly = eager_chunk_ce(h, w, b, y)
+            loss = (lse - ly).sum()
+        (loss / cfg.n).backward()
+        dt += time.perf_counter() - t0
+    return dict(value=round(rows / dt, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"first {rows} of {cfg.n} rows of config {cfg.index} (d={cfg.d}, V={cfg.v}), fp32 torch eager "
+                       f"{op} fwd+bwd in {chunk}-row chunks, {dt:.1f} s on {torch.get_num_threads()} threads")
+
+
+def bench_induct(args):
+    """The keys-and-locks producer (`_induct_raw`, full2.py:1499-1535; locks = 3, the longest firing lock kept)
+    on the token texts of the configuration (config 2: 32 texts x 1024 tokens), timed with torch events on the
+    current stream. It is a per-text sort in LDS: the HBM roofline is reported for its algorithmic bytes
+    (x in, cand / on / bk out: 8 + 24 + 3 + 8 bytes per token), not as its bound."""
+    from memarch_amd import _lib, induct
+    from memarch_amd.workloads import CONFIGS, token_stream
+    from oracle.induct_oracle import sorted_scan
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    x_np = token_stream(cfg)[:, :-1]
+    x = torch.from_numpy(x_np.copy()).to(dev)
+    n = x.numel()
+    for _ in range(args.warmup):
+        induct.induct_raw(x, locks=3, longest=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        induct.induct_raw(x, locks=3, longest=True)
+    e1.record()
+    torch.cuda.synchronize()
+    dt = e0.elapsed_time(e1) / args.steps * 1e-3
+    nbytes = n * (8 + 24 + 3 + 8)
+    res = {
+        "metric": "tokens/s keys-and-locks producer (3 locks, longest kept)", "value": round(n / dt, 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": f"synthetic (seeded config {cfg.index} token texts)",
+        "config": {"workload": f"_induct_raw on config {cfg.index}'s texts", "texts": int(x.shape[0]),
+                   "seq": int(x.shape[1]), "locks": 3},
+        "roofline": {"bound": "hbm", "kernel": "k_induct", "achieved": round(nbytes / dt / 1e9, 2),
+                     "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(nbytes / dt / PEAK_HBM, 6),
+                     "bytes_per_launch": nbytes, "traffic": None,
+                     "note": "LDS sort bound: one workgroup per text"},
+    }
+    if args.cpu_rows > 0:
+        # all texts of the configuration, repeated until about 2 s of CPU work have been timed
+        reps, ct = 0, 0.0
+        while ct < 2.0:
+            t0 = time.perf_counter()
+            sorted_scan(x_np, cfg.v_real, locks=3, longest=True)
+            ct += time.perf_counter() - t0
+            reps += 1
+        res["cpu_baseline"] = dict(value=round(reps * n / ct, 1), unit="tokens/s", cores=1, kind="port",
+                                   sample=f"all {x_np.shape[0]} texts of config {cfg.index}, {reps} passes of the "
+                                   f"numpy argsort restatement (oracle.induct_oracle.sorted_scan), {ct:.1f} s, "
+                                   f"1 thread")
+    print(json.dumps(res), flush=True)
 
 
 def calibrate_copy():
@@ -249,7 +346,11 @@ def main():
     if args.op == "swiglu":
         bench_swiglu(args)
         return
+    if args.op == "induct":
+        bench_induct(args)
+        return
     from memarch_amd import fused_ops
+    from memarch_amd.chunk_ce import chunk_ce
     from memarch_amd.workloads import CONFIGS, make_inputs
     cfg = CONFIGS[args.config]
     if not cfg.backward:
@@ -263,9 +364,20 @@ def main():
     b = inp.bias.detach().requires_grad_()
     gate = inp.gate.detach().requires_grad_()
 
+    cand, cval = sparse_bias(inp.y.cpu(), inp.c1.cpu(), cfg.v_real)
+    cand, cval = cand.to(dev), cval.to(dev).requires_grad_()
+
     def step():
-        h.grad = w.grad = b.grad = gate.grad = None
-        loss = fused_ops.linear_ce_mix_biased(h, w, b, inp.y, gate, inp.hit, v_real=cfg.v_real)
+        h.grad = w.grad = b.grad = gate.grad = cval.grad = None
+        if args.op == "linear_ce":
+            loss = fused_ops.linear_ce(h, w, inp.y)
+        elif args.op == "linear_ce_sparse":
+            loss = fused_ops.linear_ce_sparse(h, w, inp.y, cand, cval)
+        elif args.op == "chunk_ce":
+            lse, ly = chunk_ce(h, w, b, inp.y)
+            loss = (lse - ly).sum()
+        else:
+            loss = fused_ops.linear_ce_mix_biased(h, w, b, inp.y, gate, inp.hit, v_real=cfg.v_real)
         (loss / n).backward()
         return loss
 
@@ -317,13 +429,14 @@ def main():
     dom = max(stages, key=stages.get)
     kflops = 2.0 * n * v * d   # every stage's kernel is one N x V x d contraction
     ach = kflops / (stages[dom] * 1e-3)
-    traffic = traffic_bytes(kernel_of[dom], cfg.index)
+    traffic = traffic_bytes(kernel_of[dom], cfg.index) if args.op == "fused_ce" else None
     res = {
-        "metric": METRIC,
+        "metric": METRIC if args.op == "fused_ce" else f"tokens/s {args.op} fwd+bwd, d={d} V={v}; % bf16 MFMA peak",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": f"synthetic (seeded config {cfg.index} distributions, random-init weights)",
-        "config": {"workload": f"config {cfg.index}: fused linear+CE+pointer fwd+bwd, one batch per step",
+        "config": {"workload": f"config {cfg.index}: " + ("fused linear+CE+pointer" if args.op == "fused_ce" else
+                                                             args.op) + " fwd+bwd, one batch per step",
                    "N": n, "d": d, "V": v, "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
         "roofline": {"bound": "mfma", "kernel": kernel_of[dom], "stage": dom, "achieved": round(ach / 1e12, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16, 4),
@@ -332,8 +445,8 @@ def main():
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
     }
-    res["path"] = args.path
-    if args.other_path_steps > 0:
+    res["path"] = args.path if args.op in ("fused_ce", "linear_ce") else "recompute"
+    if args.other_path_steps > 0 and args.op in ("fused_ce", "linear_ce"):
         other = "recompute" if args.path == "one-pass" else "one-pass"
         print(f"[bench] {other} path for comparison", file=sys.stderr, flush=True)
         res["other_path"] = {"path": other,
@@ -343,7 +456,7 @@ def main():
         res["isolated_stages_ms"] = {k: round(x, 3) for k, x in isolated.items()}
     if args.cpu_rows > 0:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        res["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_rows, n))
+        res["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_rows, n), op=args.op)
     print(json.dumps(res), flush=True)
 
 
