@@ -1400,7 +1400,7 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
                                                            const float* __restrict__ rscale = nullptr,
                                                            const float* __restrict__ go = nullptr,
                                                            uint16_t* __restrict__ uperm = nullptr) {
-  __shared__ uint16_t tile[64][66];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][66];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   if (uperm != nullptr && blockIdx.y == 0 && t < 64) {
@@ -1421,15 +1421,18 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
         for (int e = 0; e < 8; ++e) v[e] = to_bf16(f * bf16_to_f32(v[e]));
       }
     }
+    // four 4-byte LDS writes (every 132-byte row starts 4-byte aligned and cl is a multiple of 8)
+    uint32_t* row = reinterpret_cast<uint32_t*>(&tile[rl][cl]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) tile[rl][cl + e] = v[e];
+    for (int e = 0; e < 4; ++e) row[e] = (uint32_t)v[2 * e] | ((uint32_t)v[2 * e + 1] << 16);
   }
   __syncthreads();
-  // output: 64 rows c, each 64 consecutive r = 8 chunks of 8; lanes take consecutive c for conflict-free reads
+  // output: 64 rows c, each 64 consecutive r = 8 chunks of 8 (128 contiguous bytes); the 8 lanes of a lane group
+  // take the 8 chunks of one c, so every store instruction writes eight whole 128-byte runs
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int id = t + 256 * h;
-    const int cl = id & 63, rq = id >> 6;
+    const int cl = id >> 3, rq = id & 7;
     const int64_t c = c0 + cl;
     if (c < C) {
       // output positions r0 + 8rq .. +7 (kperm order) hold the rows kperm_inv(8rq + e)
