@@ -50,6 +50,7 @@ STAGE_OF_CALL = {"mce_fwd_train": ("fwd", "k_fwd_train<true>"),
                  "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true, 0>"),
                  "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, 0>"),
                  "mce_fwd_sparse": ("fwd", "k_fwd_tiles<true>"),
+                 "mce_fwd_train_sparse": ("fwd", "k_fwd_train<true>"),
                  "mce_bwd_logits_grad_sparse": ("logits_grad", "k_bwd_grad<true>"),
                  "mce_lse_fwd": ("fwd", "k_fwd_tiles<true>"),
                  "mce_bwd_lse_grad": ("logits_grad", "k_bwd_grad<true>")}
@@ -445,8 +446,9 @@ def main():
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
     }
-    res["path"] = args.path if args.op in ("fused_ce", "linear_ce") else "recompute"
-    if args.other_path_steps > 0 and args.op in ("fused_ce", "linear_ce"):
+    one_pass_ops = ("fused_ce", "linear_ce", "linear_ce_sparse")   # chunk_ce: gradient coefficients known only in the backward
+    res["path"] = args.path if args.op in one_pass_ops else "recompute"
+    if args.other_path_steps > 0 and args.op in one_pass_ops:
         other = "recompute" if args.path == "one-pass" else "one-pass"
         print(f"[bench] {other} path for comparison", file=sys.stderr, flush=True)
         res["other_path"] = {"path": other,

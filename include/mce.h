@@ -214,6 +214,26 @@ MCE_API int mce_bwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int
                           float* dW, int64_t lddw, float* dBias, float* dGate, void* ws, size_t ws_bytes,
                           void* stream);
 
+/*
+ * Forward of the training path with a sparse logit bias (plain cross-entropy): logits[n, cand[n, j]] += cval[n, j]
+ * (j < kc <= 8; repeated ids add up; ids outside [0, V_real) are ignored), as mce_fwd_sparse. Writes E' and a into
+ * ws like mce_fwd_train, with the candidates' entries from their biased logits, so the backward is
+ * mce_bwd_train_dhidden / mce_bwd_train_dweight plus mce_bwd_train_dcval. Replaces `_LinearCESparse.forward`
+ * (fused_ops.py:71-91): the logits GEMM, the scatter of b into the bf16 logits (fused_ops.py:84) and
+ * `_ce_grad_kernel`.
+ */
+MCE_API int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                                 const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N,
+                                 int64_t K, int64_t V, int64_t V_real, float* loss_rows, float* lse_rows,
+                                 float* wgt_rows, float* loss_sum, void* ws, size_t ws_bytes, void* stream);
+
+/* Gradient of the sparse bias values after mce_fwd_train_sparse: dCval[n, j] = go * G[n, cand[n, j]] (0 for
+ * ignored ids), from the candidate logits kept in ws and the forward's lse_rows / wgt_rows. Replaces the
+ * `g.gather(1, cand)` of `_LinearCESparse.forward` (fused_ops.py:86) and its `* go` in the backward. */
+MCE_API int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval, int kc,
+                                const float* lse_rows, const float* wgt_rows, const float* go, int64_t N, int64_t K,
+                                int64_t V, int64_t V_real, float* dCval, void* ws, size_t ws_bytes, void* stream);
+
 /* Copies the number of rows the last mce_fwd_train on this workspace wrote by the exact fallback pass into
  * *out (a device int), on `stream`. No counterpart in the reference (diagnostics and tests). */
 MCE_API int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int* out, void* stream);

@@ -40,6 +40,9 @@ SIGNATURES = {
     "mce_bwd_train_dhidden": (_INT, [_P, _I, _P, _I, _I, _I, _P, _INT, _I, _P, _S, _P]),
     "mce_bwd_train_dweight": (_INT, [_P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _S, _P]),
     "mce_bwd_train": (_INT, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P, _S, _P]),
+    "mce_fwd_train_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _P, _P, _P, _P, _P, _S,
+                                    _P]),
+    "mce_bwd_train_dcval": (_INT, [_P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _P, _P, _S, _P]),
     "mce_train_flagged": (_INT, [_P, _I, _I, _I, _P, _P]),
     "mce_train_set_threshold": (None, [ctypes.c_float]),
     # include/mce_induct.h

@@ -30,7 +30,7 @@
 
 #include "../../include/mce.h"
 
-#define MCE_VERSION 400
+#define MCE_VERSION 401
 
 typedef int32_t mce_i32x4 __attribute__((ext_vector_type(4)));
 // The LLVM intrinsic behind `buffer_load_dword... lds`: (resource, LDS base, bytes per lane, per-lane offset,
@@ -862,13 +862,14 @@ __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__
     if (c >= 0 && c < Vreal)
       g = c == yn ? cn * (expf(xy[n] - lse) - 1.f) : cn * expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - lse);
     if (dcval != nullptr) dcval[n * kc + k] = g;
-    if (c != yn && first_valid(cand, kc, n, k, Vreal)) {
+    if (fix_col != nullptr && c != yn && first_valid(cand, kc, n, k, Vreal)) {
       fix_col[n * MAX_KC + f] = (int)c;
       fix_val[n * MAX_KC + f] = g;
       ++f;
     }
   }
-  for (; f < MAX_KC; ++f) fix_col[n * MAX_KC + f] = -1;
+  if (fix_col != nullptr)
+    for (; f < MAX_KC; ++f) fix_col[n * MAX_KC + f] = -1;
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1143,8 +1144,10 @@ __device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(pack_bf
 // logit when the target lies outside tile 0; also clears the flags and the flagged-row counter.
 __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_m, const float* __restrict__ part_s,
                                                  const float* __restrict__ xy, const int64_t* __restrict__ y,
-                                                 int64_t N, int64_t Np, float* __restrict__ lse_est,
-                                                 int* __restrict__ flag, int* __restrict__ flag_count) {
+                                                 const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                 const float* __restrict__ xc, int kc, int64_t Vreal, int64_t N,
+                                                 int64_t Np, float* __restrict__ lse_est, int* __restrict__ flag,
+                                                 int* __restrict__ flag_count) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (n == 0) *flag_count = 0;
   if (n >= Np) return;
@@ -1166,6 +1169,21 @@ __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_
   if (y[n] >= BM && x != -INFINITY) {
     const float mm = fmaxf(l, x);
     l = mm + logf(expf(l - mm) + expf(x - mm));
+  }
+  if (kc > 0) {
+    // sparse bias: the tile saw the logits without it, so its logsumexp bounds lse_n from below only while no
+    // candidate of the first tile has a negative total bias; otherwise the largest true logit among the target
+    // and the candidates is the bound
+    bool neg = false;
+    float mx = x;
+    for (int k = 0; k < kc; ++k)
+      if (first_valid(cand, kc, n, k, Vreal)) {
+        const int64_t c = cand[n * kc + k];
+        const float B = sparse_bias(cand, cval, kc, n, c);
+        if (c < BM && B < 0.f) neg = true;
+        mx = fmaxf(mx, xc[n * kc + k] + B);
+      }
+    if (neg) l = mx;
   }
   lse_est[n] = l;
 }
@@ -1253,9 +1271,12 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
   }
 }
 
-// After the merge: a_n = wgt_n exp(e_n - lse_n), and the target element of E' (both buffers) for unflagged rows;
-// flagged rows get a_n = wgt_n and are appended to flag_list for k_repair. Rows N .. Np-1 get a_n = 0.
+// After the merge: a_n = wgt_n exp(e_n - lse_n), and the target element of E' (both buffers) for unflagged rows,
+// with a sparse bias also the entries of the row's candidates; flagged rows get a_n = wgt_n and are appended to
+// flag_list for k_repair. Rows N .. Np-1 get a_n = 0.
 __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ y, const float* __restrict__ xy,
+                                                    const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                    const float* __restrict__ xc, int kc,
                                                     const float* __restrict__ lse_est,
                                                     const float* __restrict__ lse_rows,
                                                     const float* __restrict__ wgt_rows, const int* __restrict__ flag,
@@ -1270,18 +1291,29 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
     return;
   }
   const float w = wgt_rows[n];
-  if (flag[n]) {
+  const float e = lse_est[n], l = lse_rows[n];
+  // every E' value of the row is at most exp(lse - e_n): a row whose lse exceeds e_n by more than 60 (possible
+  // only through a large sparse bias, which the tiles do not see) also takes the exact pass
+  if (flag[n] || !(l - e <= 60.f)) {
     arow[n] = w;
     flag_list[atomicAdd(flag_count, 1)] = (int)n;
     return;
   }
-  const float e = lse_est[n], l = lse_rows[n];
   arow[n] = w * expf(e - l);
   const int64_t yn = y[n];
   if (yn >= 0 && yn < Vreal) {
     const uint16_t b = to_bf16((expf(xy[n] - l) - 1.f) * expf(l - e));
     G[cm_index(n, yn, Np)] = b;
     Gt[cm_index(yn, n, Vp)] = b;
+  }
+  // sparse bias: each distinct valid candidate other than the target gets its true logit x_c + B_c (the target's
+  // x_y already includes its bias)
+  for (int k = 0; k < kc; ++k) {
+    const int64_t c = cand[n * kc + k];
+    if (c == yn || !first_valid(cand, kc, n, k, Vreal)) continue;
+    const uint16_t b = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - e));
+    G[cm_index(n, c, Np)] = b;
+    Gt[cm_index(c, n, Vp)] = b;
   }
 }
 
@@ -1295,7 +1327,8 @@ constexpr int REPAIR_KC = 16384;
 __global__ __launch_bounds__(256) void k_repair(const uint16_t* __restrict__ H, int64_t ldh,
                                                 const uint16_t* __restrict__ W, int64_t ldw,
                                                 const float* __restrict__ bias, const int64_t* __restrict__ y,
-                                                const float* __restrict__ lse_rows,
+                                                const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                int kc, const float* __restrict__ lse_rows,
                                                 const float* __restrict__ wgt_rows, int64_t K, int64_t V, int64_t Vp,
                                                 int64_t Vreal, int64_t Np, const int* __restrict__ flag_count,
                                                 const int* __restrict__ flag_list, uint16_t* __restrict__ G,
@@ -1336,7 +1369,7 @@ __global__ __launch_bounds__(256) void k_repair(const uint16_t* __restrict__ H, 
       }
     }
     float g = 0.f;
-    if (v < Vreal) g = expf(x + (bias != nullptr ? bias[v] : 0.f) - l);
+    if (v < Vreal) g = expf(x + (bias != nullptr ? bias[v] : 0.f) + (kc > 0 ? sparse_bias(cand, cval, kc, n, v) : 0.f) - l);
     if (v == yn) g -= 1.f;
     const uint16_t b = to_bf16(g);
     G[cm_index(n, v, Np)] = b;
@@ -1907,11 +1940,13 @@ constexpr int REPAIR_BLOCKS = 1024;
 // Forward of the one-pass training path (mixture or plain cross-entropy, no sparse bias): the per-row outputs of
 // fwd_impl plus E' in the workspace's G / Gt and a_n.
 int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
-                   const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
-                   int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
-                   float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
+                   const int64_t* y, const float* gate, const float* hit, const int64_t* cand, const float* cval,
+                   int kc, int64_t N, int64_t K, int64_t V, int64_t V_real, float* loss_rows, float* lse_rows,
+                   float* wgt_rows, float* dgr_rows, float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (!rc) rc = check_bias(bias);
+  if (!rc) rc = check_sparse(cand, cval, kc);
+  if (!rc && kc > 0 && gate != nullptr) rc = MCE_EINVAL;  // the sparse bias is for plain cross-entropy
   if (rc) return rc;
   if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr)) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1925,8 +1960,8 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   const bool kf = K % BK == 0;
-  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, nullptr,
-                     nullptr, 0, N, K, V_real, w.f.xy, w.f.xc);
+  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand,
+                     cval, kc, N, K, V_real, w.f.xy, w.f.xc);
   if ((rc = launch_status())) return rc;
   // e_n: the first vocabulary tile (one tile row of k_fwd_tiles) and the target logit
   if (kf)
@@ -1937,7 +1972,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
                        w.f.part_m, w.f.part_s);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, w.f.part_m, w.f.part_s, w.f.xy,
-                     y, N, w.b.np, w.lse_est, w.flag, w.flag_count);
+                     y, cand, cval, w.f.xc, kc, V_real, N, w.b.np, w.lse_est, w.flag, w.flag_count);
   if ((rc = launch_status())) return rc;
   if (kf)
     hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est, N,
@@ -1949,15 +1984,16 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
                        w.flag);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.f.part_m, w.f.part_s, w.f.xy,
-                     nullptr, nullptr, nullptr, 0, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows,
-                     dgr_rows, w.f.loss_part);
+                     cand, cval, w.f.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows,
+                     w.f.loss_part);
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_train_rows, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, y, w.f.xy, w.lse_est,
+  hipLaunchKernelGGL(k_train_rows, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, y, w.f.xy, cand, cval,
+                     w.f.xc, kc, w.lse_est,
                      lse_rows, wgt_rows, w.flag, N, w.b.np, w.b.vp, V_real, w.arow, w.flag_count, w.flag_list, w.b.G,
                      w.b.Gt);
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, y, lse_rows, wgt_rows, K,
-                     V, w.b.vp, V_real, w.b.np, w.flag_count, w.flag_list, w.b.G, w.b.Gt);
+  hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval, kc,
+                     lse_rows, wgt_rows, K, V, w.b.vp, V_real, w.b.np, w.flag_count, w.flag_list, w.b.G, w.b.Gt);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.f.loss_part, (int64_t)cdiv(N, 32), loss_sum);
   return launch_status();
@@ -2181,8 +2217,31 @@ int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw
                   const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
                   int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
                   float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
-  return fwd_train_impl(H, ldh, W, ldw, bias, y, gate, hit, N, K, V, V_real, loss_rows, lse_rows, wgt_rows, dgr_rows,
-                        loss_sum, ws, ws_bytes, stream);
+  return fwd_train_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, loss_rows, lse_rows,
+                        wgt_rows, dgr_rows, loss_sum, ws, ws_bytes, stream);
+}
+
+int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                         const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K,
+                         int64_t V, int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows,
+                         float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
+  return fwd_train_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, cand, cval, kc, N, K, V, V_real, loss_rows,
+                        lse_rows, wgt_rows, nullptr, loss_sum, ws, ws_bytes, stream);
+}
+
+int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
+                        const float* wgt_rows, const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real,
+                        float* dCval, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_sparse(cand, cval, kc);
+  if (rc) return rc;
+  if (N < 0 || K <= 0 || V <= 0 || V_real < 0 || V_real > V) return MCE_EINVAL;
+  if (N == 0 || kc == 0) return MCE_OK;
+  if (!y || !lse_rows || !wgt_rows || !go || !dCval || !ws) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     y, cand, cval, kc, w.f.xy, w.f.xc, lse_rows, wgt_rows, go, N, V_real, nullptr, nullptr, dCval);
+  return launch_status();
 }
 
 int mce_bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V, void* dH,

@@ -6,11 +6,12 @@ call signatures, same return value (the fp32 loss SUM over rows) and the same gr
 w, gate and the sparse values b in their own dtypes; None for y, hit, cand and chunk). All device work runs in libmce.so (HIP, gfx950) on torch's
 current stream; there is no other code path, and a tensor that is not on a GPU raises.
 
-When any input needs a gradient (and there is no sparse bias), the forward runs the one-pass training path
-(mce_fwd_train): like the reference (fused_ops.py:148-155) it forms the logits gradient during the forward, as a
-bf16 N x V buffer of exp(x - e_n) with one per-row factor left to the backward, and never stores the logits; the
-backward then runs only the dH and dW contractions. Otherwise -- no gradient needed, a sparse bias, or
-RECOMPUTE set (environment MEMARCH_AMD_RECOMPUTE=1) -- the forward computes only the per-row statistics and the
+When any input needs a gradient, the forward runs the one-pass training path (mce_fwd_train, or
+mce_fwd_train_sparse with a sparse bias): like the reference (fused_ops.py:148-155) it forms the logits gradient
+during the forward, as a bf16 N x V buffer of exp(x - e_n) with one per-row factor left to the backward, and never
+stores the logits; the backward then runs only the dH and dW contractions (and the candidates' gradient from the
+per-row state). Otherwise -- no gradient needed, or RECOMPUTE set (environment MEMARCH_AMD_RECOMPUTE=1) -- the
+forward computes only the per-row statistics and the
 backward recomputes the logits tile by tile to form the gradient. `chunk` is accepted and ignored (tiling is
 internal). Logits are fp32 in both paths (never rounded to bf16), and rows with P below the 1e-30 clamp get zero
 gradient, as the reference's eager formula does (full2.py:1925-1929).
@@ -106,12 +107,18 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
     loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
     loss_sum = torch.empty((), **f32)
     lib = _lib.load()
-    if train and kc == 0:
+    if train:
         ws_bytes = lib.mce_train_ws_bytes(n, kp, v)
         tws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
-                  _ptr(hf), n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum),
-                  _ptr(tws), ws_bytes, _stream(dev))
+        if kc:
+            _lib.call("mce_fwd_train_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
+                      _ptr(cand64), _ptr(cval32), kc, n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt),
+                      _ptr(loss_sum), _ptr(tws), ws_bytes, _stream(dev))
+            dgr.zero_()
+        else:
+            _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
+                      _ptr(hf), n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum),
+                      _ptr(tws), ws_bytes, _stream(dev))
         rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
         return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real), tws
     ws_bytes = lib.mce_fwd_ws_bytes(n, kp, v)
@@ -130,7 +137,7 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
 
 
 def _forward(ctx, h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
-    train = ctx is not None and any(ctx.needs_input_grad) and cand is None and not RECOMPUTE
+    train = ctx is not None and any(ctx.needs_input_grad) and not RECOMPUTE
     (hd, wd, bf, y64, c64, cv32), rows, loss_sum, meta, tws = _fwd_launch(h, w, bias, y, gate, hit, v_real, cand,
                                                                           cval, train)
     ctx.save_for_backward(hd, wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"], c64, cv32)
@@ -190,6 +197,9 @@ def _backward(ctx, go, need_h, need_w, need_b, need_g, need_c=False):
         if dgate is not None:
             _lib.call("mce_bwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(go32), _ptr(dgr), n, kp,
                       v, None, 0, kp, None, kp, None, _ptr(dgate), _ptr(tws), nb, st)
+        if dcval is not None:
+            _lib.call("mce_bwd_train_dcval", _ptr(y64), _ptr(c64), _ptr(cv32), c64.shape[1], _ptr(lse), _ptr(wgt),
+                      _ptr(go32), n, kp, v, v_real, _ptr(dcval), _ptr(tws), nb, st)
     elif need_h or need_w or need_g or dbias is not None or dcval is not None:
         lib = _lib.load()
         ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)

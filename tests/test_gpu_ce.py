@@ -120,19 +120,32 @@ SPARSE = [
     (777, 520, 2051, 8, 3.0),     # the largest kc
     (129, 2064, 1024, 2, 8.0),    # candidates dominate their rows
     (200, 256, 800, 4, -20.0),    # candidates pushed far below the rest
+    (160, 128, 600, 2, 70.0),     # candidates far above: rows whose lse exceeds e_n by over 60 take the exact pass
 ]
 
 
+@pytest.mark.parametrize("mode", ["one_pass", "recompute", "fallback"])
 @pytest.mark.parametrize("shape", SPARSE, ids=lambda s: "N{}_K{}_V{}_kc{}_s{}".format(*s))
-def test_linear_ce_sparse_parity(shape):
-    from memarch_amd import fused_ops
+def test_linear_ce_sparse_parity(shape, mode, monkeypatch):
+    """one_pass: mce_fwd_train_sparse (the candidates' E' entries from their biased logits, mce_bwd_train_dcval);
+    recompute: mce_fwd_sparse + mce_bwd_logits_grad_sparse; fallback: the one-pass path with every row flagged
+    from the host, so every E' row comes from the exact pass with the sparse bias added."""
+    from memarch_amd import _lib, fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", mode == "recompute")
     N, K, V, kc, scale = shape
-    print(f"linear_ce_sparse {shape}", flush=True)
+    print(f"linear_ce_sparse {shape} {mode}", flush=True)
     c = _case(N, K, V, kc, seed=N + kc, v_scale=scale)
     h = c["h"].cuda().bfloat16().requires_grad_()
     w = c["w"].cuda().requires_grad_()
     b = c["cval"].cuda().requires_grad_()
-    loss = fused_ops.linear_ce_sparse(h, w, c["y"].cuda(), c["cand"].cuda(), b)
+    lib = _lib.load()
+    if mode == "fallback":
+        lib.mce_train_set_threshold(1e-30)
+    try:
+        loss = fused_ops.linear_ce_sparse(h, w, c["y"].cuda(), c["cand"].cuda(), b)
+    finally:
+        if mode == "fallback":
+            lib.mce_train_set_threshold(0.0)
     (loss * 0.5).backward()
     fwd, bwd = _oracle(c, go=0.5)
     assert b.grad.shape == (N, kc) and b.grad.dtype == torch.float32
