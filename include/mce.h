@@ -55,6 +55,7 @@ extern "C" {
 #define MCE_EALIGN 2     /* pointer or leading dimension not aligned as required */
 #define MCE_EWORKSPACE 3 /* workspace too small */
 #define MCE_ELAUNCH 4    /* a HIP launch failed (see mce_last_hip_error) */
+#define MCE_ESCRATCH 5   /* the shape needs more than the fixed scratch of mce_fwd_noalloc */
 
 /* Library version (major*10000 + minor*100 + patch). No counterpart in the reference. */
 MCE_API int mce_version(void);
@@ -79,6 +80,21 @@ MCE_API int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
             const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
             int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
             void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Allocation-free variant of mce_fwd: the same arguments, outputs and kernels, without `ws` / `ws_bytes`. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving or evaluation loops, harnesses that forbid hipMalloc). Its scratch is a fixed 64 MiB
+ * device array inside the library, one copy per GPU, held until the process ends; a shape whose mce_fwd
+ * workspace (mce_fwd_ws_bytes(N, K, V)) exceeds 64 MiB -- e.g. N > ~21000 rows at V = 50304, N > ~8100 at
+ * V = 131072 -- is rejected with MCE_ESCRATCH before any GPU work. The call allocates nothing, records no memset,
+ * and needs nothing cleared beforehand. All calls on one GPU share that GPU's scratch: calls that overlap in time
+ * on one GPU (different streams, or other host threads) race and must be ordered by the caller.
+ */
+MCE_API int mce_fwd_noalloc(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                    const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
+                    int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
+                    float* loss_sum, void* stream);
 
 /*
  * Forward of plain cross-entropy with a sparse additive logit bias (kc candidates per row, kc <= 8; kc = 0 is

@@ -24,6 +24,7 @@ SIGNATURES = {
     "mce_last_hip_error": (_INT, []),
     "mce_fwd_ws_bytes": (_S, [_I, _I, _I]),
     "mce_fwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P]),
+    "mce_fwd_noalloc": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "mce_fwd_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _P, _P, _P, _P, _P, _S, _P]),
     "mce_bwd_ws_bytes": (_S, [_I, _I, _I]),
     "mce_bwd_logits_grad": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _S, _P]),

@@ -28,6 +28,8 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <mutex>
+
 #include "../../include/mce.h"
 
 #define MCE_VERSION 401
@@ -823,6 +825,13 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
     for (int i = 0; i < 32; ++i) tot += rl[i];
     loss_part[blockIdx.x] = tot;
   }
+}
+
+// p[0 .. n-1] = v (a fill kernel rather than hipMemsetAsync, so that a call captured into a HIP graph records no
+// memset node).
+__global__ __launch_bounds__(256) void k_fill_f32(float* __restrict__ p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 // Deterministic sum of `count` partials into out[0] (one block).
@@ -1836,7 +1845,7 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
   if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr)) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
-    (void)hipMemsetAsync(loss_sum, 0, sizeof(float), st);
+    hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, loss_sum, (int64_t)1, 0.f);
     return launch_status();
   }
   if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
@@ -2068,6 +2077,51 @@ int bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------------------------
+// Fixed device scratch of the allocation-free forward (mce_fwd_noalloc): the mce_fwd workspace (per-half-tile
+// partials, target logits, loss partials) for callers that cannot allocate. Every GPU the library runs on holds
+// its own copy until the process ends. In host code `scratch` names a host-side stand-in, not a device address:
+// the kernels get the address that hipGetSymbolAddress returns for the device of the call's stream, looked up once
+// per device (with that device current) and kept in g_scratch_dev. Nothing in it has to start at zero: the
+// forward kernels write every element they later read.
+constexpr size_t SCRATCH_BYTES = size_t(64) << 20;
+static __device__ __align__(256) char scratch[SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[SCRATCH_MAX_DEVICES];
+
+// Device address of `scratch` on the device of stream `st`.
+int scratch_for_stream(hipStream_t st, void** out) {
+  int dev = 0;
+  hipError_t e = hipStreamGetDevice(st, &dev);
+  if (e != hipSuccess) {
+    g_last_hip_error = (int)e;
+    return MCE_ELAUNCH;
+  }
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return MCE_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess || (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)) {
+      g_last_hip_error = (int)e;
+      return MCE_ELAUNCH;
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t er = cur != dev ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess || p == nullptr || er != hipSuccess) {
+      g_last_hip_error = (int)(e != hipSuccess ? e : er);
+      return MCE_ELAUNCH;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return MCE_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int mce_version(void) { return MCE_VERSION; }
@@ -2079,6 +2133,7 @@ const char* mce_error_string(int code) {
     case MCE_EALIGN: return "alignment: K and leading dimensions must be multiples of 8, H and W 16-byte aligned";
     case MCE_EWORKSPACE: return "workspace too small";
     case MCE_ELAUNCH: return "HIP kernel launch failed";
+    case MCE_ESCRATCH: return "shape exceeds the fixed 64 MiB scratch of the allocation-free entry point";
     default: return "unknown error";
   }
 }
@@ -2102,6 +2157,19 @@ int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
             void* stream) {
   return fwd_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, loss_rows, lse_rows,
                   wgt_rows, dgr_rows, loss_sum, ws, ws_bytes, stream);
+}
+
+int mce_fwd_noalloc(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                    const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
+                    int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
+                    float* loss_sum, void* stream) {
+  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (rc) return rc;
+  if (fwd_ws_layout(nullptr, N, V).bytes > SCRATCH_BYTES) return MCE_ESCRATCH;
+  void* ws = nullptr;
+  if ((rc = scratch_for_stream(reinterpret_cast<hipStream_t>(stream), &ws))) return rc;
+  return fwd_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, loss_rows, lse_rows,
+                  wgt_rows, dgr_rows, loss_sum, ws, SCRATCH_BYTES, stream);
 }
 
 int mce_fwd_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,

@@ -34,7 +34,7 @@ def test_exports_every_declared_symbol(lib):
 
 def test_version_and_errors(lib):
     assert lib.mce_version() >= 100
-    for code in range(5):
+    for code in range(6):
         assert lib.mce_error_string(code)
 
 
