@@ -264,6 +264,87 @@ def bench_induct(args):
     print(json.dumps(res), flush=True)
 
 
+def cpu_forward_config0(cfg, min_seconds=10.0):
+    """Config 0's CPU case at full size: the oracle's torch restatement of the eager formula (`_ce_part`,
+    full2.py:1900-1930) on all N = 4096 rows in fp32 (fp32 h and W, no bf16 rounding: the reference's eager CPU
+    path), forward only, repeated until `min_seconds` of CPU work have been timed; all host threads."""
+    from memarch_amd.workloads import make_inputs
+    from oracle.mce_oracle import eager_ce_part
+    inp = make_inputs(cfg)
+    reps, dt, loss = 0, 0.0, None
+    with torch.no_grad():
+        while dt < min_seconds or reps < 2:
+            t0 = time.perf_counter()
+            loss = eager_ce_part(inp.h, inp.w, inp.bias, inp.y, inp.c1, inp.gate)
+            dt += time.perf_counter() - t0
+            reps += 1
+    return dict(value=round(reps * cfg.n / dt, 1), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"all {cfg.n} rows of config 0 (d={cfg.d}, V={cfg.v}), fp32 torch eager forward (materialised "
+                       f"fp32 logits), {reps} passes in {dt:.1f} s on {torch.get_num_threads()} threads "
+                       f"(os.cpu_count()={os.cpu_count()})"), float(loss)
+
+
+def bench_config0(args):
+    """Config 0 (the reference's CPU-runnable case, forward loss only): the GPU forward of the fused op (the
+    statistics-only forward mce_fwd that runs under torch.no_grad(); bf16 operands from the fp32 inputs, as
+    fused_ops.py:142 casts them) beside the full-size CPU fp32 eager forward."""
+    from memarch_amd import _lib, fused_ops
+    from memarch_amd.workloads import CONFIGS, make_inputs
+    cfg = CONFIGS[0]
+    dev = torch.device("cuda", 0)
+    inp = make_inputs(cfg).to(dev)
+    n, d, v = cfg.n, cfg.d, cfg.v
+
+    def step():
+        with torch.no_grad():
+            return fused_ops.linear_ce_mix_biased(inp.h, inp.w, inp.bias, inp.y, inp.gate, inp.hit,
+                                                  v_real=cfg.v_real)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    marks = []
+
+    def hook(name, phase):
+        if name == "mce_fwd":
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            marks.append(ev)
+
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    _lib.set_call_hook(hook)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    _lib.set_call_hook(None)
+    peak = torch.cuda.max_memory_allocated(dev)
+    fwd_ms = sum(a.elapsed_time(b) for a, b in zip(marks[0::2], marks[1::2])) / args.steps
+    kflops = 2.0 * n * v * d
+    res = {
+        "metric": f"tokens/s fused out+CE+pointer fwd (config 0: N={n}, d={d}, V={v}); % bf16 MFMA peak",
+        "value": round(n / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded config 0 distributions, random-init weights)",
+        "config": {"workload": "config 0: fused linear+CE+pointer forward loss only", "N": n, "d": d, "V": v,
+                   "V_real": cfg.v_real, "operands": "bf16 (cast from fp32 inputs)", "accumulate": "fp32"},
+        "roofline": {"bound": "mfma", "kernel": "k_fwd_tiles<true>", "stage": "fwd",
+                     "achieved": round(kflops / (fwd_ms * 1e-3) / 1e12, 2), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(kflops / (fwd_ms * 1e-3) / PEAK_BF16, 4),
+                     "flops_per_launch": kflops, "traffic": None},
+        "stages_ms": {"fwd": round(fwd_ms, 4)},
+        "peak_mem_gb": round(peak / 1e9, 4), "step_mem_gb": round((peak - base) / 1e9, 4),
+        "path": "forward (statistics only)",
+        "loss": float(loss),
+    }
+    if args.cpu_rows > 0:
+        print("[bench] cpu baseline (config 0 at full size)", file=sys.stderr, flush=True)
+        res["cpu_baseline"], res["cpu_loss"] = cpu_forward_config0(cfg)
+    print(json.dumps(res), flush=True)
+
+
 def calibrate_copy():
     """A plain device copy of 1 GiB, five times: each launch reads and writes exactly 2^30 bytes."""
     dev = torch.device("cuda", 0)
@@ -355,7 +436,10 @@ def main():
     from memarch_amd.workloads import CONFIGS, make_inputs
     cfg = CONFIGS[args.config]
     if not cfg.backward:
-        raise SystemExit(f"config {cfg.index} is the CPU-only forward case; bench configs 1-4")
+        if args.op != "fused_ce":
+            raise SystemExit(f"config {cfg.index} is the forward-only case of the fused op; --op {args.op} needs 1-4")
+        bench_config0(args)
+        return
     dev = torch.device("cuda", 0)
     print(f"[bench] generating config {cfg.index} inputs ({cfg.name})", file=sys.stderr, flush=True)
     inp = make_inputs(cfg).to(dev)
@@ -408,6 +492,10 @@ def main():
             marks.append((name, phase, ev))
 
     print("[bench] timed steps", file=sys.stderr, flush=True)
+    h.grad = w.grad = b.grad = gate.grad = cval.grad = None
+    torch.cuda.synchronize()
+    mem_base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
     _lib.set_call_hook(hook)
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -415,6 +503,7 @@ def main():
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
     _lib.set_call_hook(None)
+    mem_peak = torch.cuda.max_memory_allocated(dev)
     live, kernel_of = {}, {}
     for (name, ph0, e0), (name1, ph1, e1) in zip(marks[0::2], marks[1::2]):
         assert name == name1 and ph0 == "begin" and ph1 == "end"
@@ -445,6 +534,9 @@ def main():
         "op_roofline": {"achieved": round(flops / dt / 1e12, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
+        # torch.cuda.max_memory_allocated over the timed steps (inputs included), and its excess over what was
+        # allocated before them (the op's workspace, saved state and gradients), as bench_fused.py:21-30 reports
+        "peak_mem_gb": round(mem_peak / 1e9, 4), "step_mem_gb": round((mem_peak - mem_base) / 1e9, 4),
     }
     one_pass_ops = ("fused_ce", "linear_ce", "linear_ce_sparse")   # chunk_ce: gradient coefficients known only in the backward
     res["path"] = args.path if args.op in one_pass_ops else "recompute"
