@@ -23,6 +23,7 @@ throughput against the 8 TB/s roofline (algorithmic bytes: forward reads gu and 
 elements; backward reads gu and go and writes d gu, 5 rows x H elements).
 """
 import argparse
+import ctypes
 import json
 import os
 import re
@@ -39,21 +40,16 @@ PEAK_HBM = 8.0e12      # MI355X HBM3E, B/s
 METRIC = "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA peak"
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 
-# C-ABI call -> (stage, the kernel that dominates it); the stages also run small helper kernels. One-pass path
-# (default): mce_fwd_train, mce_bwd_train_dhidden, mce_bwd_train_dweight; recompute path: mce_fwd,
+# C-ABI call -> stage. One-pass path (default): mce_fwd_train (row blocks: logits tiles, merge, and every block
+# but the last its dH / dW contractions), mce_bwd_train (the last block's contractions); recompute path: mce_fwd,
 # mce_bwd_logits_grad, mce_bwd_dhidden, mce_bwd_dweight.
-STAGE_OF_CALL = {"mce_fwd_train": ("fwd", "k_fwd_train<true>"),
-                 "mce_bwd_train_dhidden": ("dhidden", "k_gemm<true, true, true, 0>"),
-                 "mce_bwd_train_dweight": ("dweight", "k_gemm<false, true, true, {nr}>"),
-                 "mce_fwd": ("fwd", "k_fwd_tiles<true>"),
-                 "mce_bwd_logits_grad": ("logits_grad", "k_bwd_grad<true>"),
-                 "mce_bwd_dhidden": ("dhidden", "k_gemm<true, true, true, 0>"),
-                 "mce_bwd_dweight": ("dweight", "k_gemm<false, true, true, 0>"),
-                 "mce_fwd_sparse": ("fwd", "k_fwd_tiles<true>"),
-                 "mce_fwd_train_sparse": ("fwd", "k_fwd_train<true>"),
-                 "mce_bwd_logits_grad_sparse": ("logits_grad", "k_bwd_grad<true>"),
-                 "mce_lse_fwd": ("fwd", "k_fwd_tiles<true>"),
-                 "mce_bwd_lse_grad": ("logits_grad", "k_bwd_grad<true>")}
+STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_sparse": "fwd",
+                 "mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
+                 "mce_bwd_dweight": "dweight", "mce_fwd_sparse": "fwd", "mce_bwd_logits_grad_sparse": "logits_grad",
+                 "mce_lse_fwd": "fwd", "mce_bwd_lse_grad": "logits_grad"}
+# kernel classes of mce_prof_stop (include/mce.h) -> kernel name; each class runs one N x V x d contraction per step
+PROF_KERNELS = ("k_fwd_train<true>", "k_fwd_tiles<true>", "k_bwd_grad<true>", "k_gemm<true, true, true, 0>",
+                "k_gemm<false, true, true, {nr}>")
 # the siblings of the north-star op (--op): the same contractions on the same configuration inputs
 SIBLING_OPS = ("linear_ce", "linear_ce_sparse", "chunk_ce")
 
@@ -496,30 +492,40 @@ def main():
     torch.cuda.synchronize()
     mem_base = torch.cuda.memory_allocated(dev)
     torch.cuda.reset_peak_memory_stats(dev)
+    lib = _lib.load()
     _lib.set_call_hook(hook)
+    lib.mce_prof_start()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
     _lib.set_call_hook(None)
+    kern_ms = (ctypes.c_double * len(PROF_KERNELS))()
+    kern_n = (ctypes.c_int64 * len(PROF_KERNELS))()
+    _lib.check(lib.mce_prof_stop(kern_ms, kern_n, len(PROF_KERNELS)), "mce_prof_stop")
     mem_peak = torch.cuda.max_memory_allocated(dev)
-    live, kernel_of = {}, {}
+    live = {}
     for (name, ph0, e0), (name1, ph1, e1) in zip(marks[0::2], marks[1::2]):
         assert name == name1 and ph0 == "begin" and ph1 == "end"
-        stage, kern = STAGE_OF_CALL[name]
-        live.setdefault(stage, []).append(e0.elapsed_time(e1))
-        kernel_of[stage] = kern.format(nr=fold_nr(d))
-    stages = {k: sum(v) / len(v) for k, v in live.items()}
+        live.setdefault(STAGE_OF_CALL[name], []).append(e0.elapsed_time(e1))
+    stages = {k: sum(x) / args.steps for k, x in live.items()}
+    # the contraction kernels, timed by the library's HIP events around each launch on the launch stream: every
+    # class present runs one N x V x d contraction per step, over one or several launches (row blocks)
+    nr = fold_nr(d) if (args.op == "fused_ce" and args.path == "one-pass") else 0   # dBias inside the dW tiles
+    kernels = {PROF_KERNELS[c].format(nr=nr): (kern_ms[c], kern_n[c] // args.steps)
+               for c in range(len(PROF_KERNELS)) if kern_n[c] > 0}
     tok_s = n / dt
     flops = 6.0 * n * v * d
     if args.stage_reps > 0:
         print("[bench] isolated stage timing", file=sys.stderr, flush=True)
         isolated = stage_times(inp, args.stage_reps)
-    dom = max(stages, key=stages.get)
-    kflops = 2.0 * n * v * d   # every stage's kernel is one N x V x d contraction
-    ach = kflops / (stages[dom] * 1e-3)
-    traffic = traffic_bytes(kernel_of[dom], cfg.index) if args.op == "fused_ce" else None
+    dom = max(kernels, key=lambda kname: kernels[kname][0])
+    launches = kernels[dom][1]
+    kflops = 2.0 * n * v * d / launches                     # per launch: one row block's contraction
+    avg_ms = kernels[dom][0] / (args.steps * launches)    # average launch duration
+    ach = kflops / (avg_ms * 1e-3)
+    traffic = traffic_bytes(dom, cfg.index) if args.op == "fused_ce" else None
     res = {
         "metric": METRIC if args.op == "fused_ce" else f"tokens/s {args.op} fwd+bwd, d={d} V={v}; % bf16 MFMA peak",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -528,12 +534,16 @@ def main():
         "config": {"workload": f"config {cfg.index}: " + ("fused linear+CE+pointer" if args.op == "fused_ce" else
                                                              args.op) + " fwd+bwd, one batch per step",
                    "N": n, "d": d, "V": v, "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
-        "roofline": {"bound": "mfma", "kernel": kernel_of[dom], "stage": dom, "achieved": round(ach / 1e12, 2),
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach / 1e12, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16, 4),
-                     "flops_per_launch": kflops, "traffic": traffic},
+                     "flops_per_launch": kflops, "launches_per_step": launches, "avg_launch_ms": round(avg_ms, 4),
+                     "traffic": traffic},
         "op_roofline": {"achieved": round(flops / dt / 1e12, 2), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
                         "frac": round(flops / dt / PEAK_BF16, 4), "flops_per_step": flops},
         "stages_ms": {k: round(x, 3) for k, x in stages.items()},
+        "kernels_ms_per_step": {k: round(t / args.steps, 3) for k, (t, _) in kernels.items()},
+        "kernels_frac_of_peak": {k: round(2.0 * n * v * d / (t / args.steps * 1e-3) / PEAK_BF16, 4)
+                                 for k, (t, _) in kernels.items()},
         # torch.cuda.max_memory_allocated over the timed steps (inputs included), and its excess over what was
         # allocated before them (the op's workspace, saved state and gradients), as bench_fused.py:21-30 reports
         "peak_mem_gb": round(mem_peak / 1e9, 4), "step_mem_gb": round((mem_peak - mem_base) / 1e9, 4),

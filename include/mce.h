@@ -183,81 +183,106 @@ MCE_API int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
             float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream);
 
 /*
- * One-pass training path (mixture or plain cross-entropy, no sparse bias). The reference computes its
- * gradients during the forward (fused_ops.py:148-155); so does this path, without materialising logits and
- * without a second pass over them:
- *   mce_fwd_train writes, besides the per-row outputs of mce_fwd, the logits gradient into the workspace as
- *   E'[n, v] = G[n, v] / (go a_n), a_n = wgt_n exp(e_n - lse_n), where e_n <= lse_n is the logsumexp of the first
- *   vocabulary tile and the target logit; rows whose logits exceed e_n by too much for the exponent range are
- *   detected on the device and written exactly by a fallback pass (with a_n = wgt_n). The backward then applies
- *   go a_n in the epilogue of dH = go a . (E' W), in the row-scaled H^T copy of dW = E'^T (go a . H) and in
- *   dBias = E'^T (go a).
- * The workspace (mce_train_ws_bytes) must be kept unchanged between mce_fwd_train and the backward calls.
+ * One-pass training path (mixture or plain cross-entropy, optionally a sparse bias). The reference computes its
+ * gradients during the forward, 4096 rows at a time (fused_ops.py:148-155); so does this path, in row blocks,
+ * without materialising logits and without a second pass over them. For each block the forward's tile kernel
+ * writes E'[n, v] = G[n, v] / (go a_n), a_n = wgt_n exp(e_n - lse_n), where e_n <= lse_n is the logsumexp of the
+ * first vocabulary tile and the target logit (rows whose logits exceed e_n by too much for the exponent range are
+ * detected on the device and written exactly by a fallback pass, with a_n = wgt_n), then the block's gradient
+ * contractions dH = a . (E' W), dW += E'^T (a . H), dBias += E'^T a run with go = 1 into caller-owned partial
+ * sums. The last block's contractions wait for the backward (mce_bwd_train), where go is known: its epilogues
+ * write go * (partial + last block) into the outputs, so the partial sums are never rescaled in a separate pass
+ * (only the earlier blocks' dH rows are, once).
+ *
+ * Blocks: `block_rows` rows each (rounded up to a multiple of 256 and evened out over the blocks), or, with
+ * block_rows = 0, as many as keep the block's E' (two bf16 copies, 4 * rows * V bytes) within 2 GiB: 8192 rows at
+ * V = 50304, 4096 at V = 131072. mce_train_ws_bytes bounds the workspace by one block, whatever N is. The same
+ * block_rows, `want` and buffers must be passed to the forward and the backward of one step, and the workspace
+ * kept unchanged between them (it holds the last block's E' and the per-row state).
  */
-MCE_API size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V);
+#define MCE_GRAD_H 1     /* want: dH */
+#define MCE_GRAD_W 2     /* want: dW */
+#define MCE_GRAD_BIAS 4  /* want: dBias (needs bias) */
+MCE_API size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V, int64_t block_rows);
+
+/* Rows per block of the training path for this shape (the last block holds the rest). No counterpart in the
+ * reference (its chunk argument, fused_ops.py:148). */
+MCE_API int64_t mce_train_block_rows(int64_t N, int64_t K, int64_t V, int64_t block_rows);
 
 /*
  * Forward of the training path. Outputs as mce_fwd (loss_rows, lse_rows, wgt_rows, dgr_rows fp32 [N], loss_sum
- * fp32 [1]) plus E' and a in ws. Replaces `_LinearCEMix.forward` (fused_ops.py:138-157): the logits GEMM
- * (fused_ops.py:150) and `_ce_mix_kernel` (fused_ops.py:104-134); gate = hit = NULL replaces
- * `_LinearCE.forward` (fused_ops.py:44-58) and `_ce_grad_kernel` (fused_ops.py:10-36).
+ * fp32 [1]); with more than one block also the partial sums of the gradients `want` asks for over the rows of all
+ * blocks but the last, for go = 1: dH_part rows [0, R) (bf16 when dh_bf16, else fp32; row stride lddh), dW_part
+ * fp32 [V, K] (row stride lddw), dBias_part fp32 [V], where R = (blocks - 1) * mce_train_block_rows(...). With one
+ * block they are not touched and may be NULL. Replaces `_LinearCEMix.forward` (fused_ops.py:138-157): the chunk
+ * loop of the logits GEMM (fused_ops.py:150), `_ce_mix_kernel` (fused_ops.py:104-134) and the gradient GEMMs
+ * `gh[i] = logits @ wd`, `gw += (logits.T @ hc).float()` (fused_ops.py:153-154); gate = hit = NULL replaces
+ * `_LinearCE.forward` (fused_ops.py:44-58) and `_ce_grad_kernel` (fused_ops.py:10-36). dBias replaces the bias
+ * column of `gw` in the folded layout (full2.py:1842-1851).
  */
 MCE_API int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                           const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
-                          int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
-                          float* loss_sum, void* ws, size_t ws_bytes, void* stream);
-
-/*
- * dH = G W of the training path (W^T is written into ws here; `go` is the fp32 upstream gradient on the
- * device). dH as for mce_bwd_dhidden. Replaces `gh[i] = logits @ wd` (fused_ops.py:153) and the `gh * go` of
- * `_LinearCEMix.backward` (fused_ops.py:161).
- */
-MCE_API int mce_bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V,
-                                  void* dH, int dh_bf16, int64_t lddh, void* ws, size_t ws_bytes, void* stream);
-
-/*
- * dW = G^T H (fp32 [V, K], row stride lddw, overwritten; may be NULL) and dBias = sum_n G[n, :] (fp32 [V]; may be
- * NULL) of the training path (the row-scaled H^T is written into ws here). Replaces `gw += (logits.T @
- * hc).float()` (fused_ops.py:154) and the `gw * go` of `_LinearCEMix.backward` (fused_ops.py:161); dBias replaces
- * the bias column of `gw` in the folded layout (full2.py:1842-1851).
- */
-MCE_API int mce_bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N, int64_t K, int64_t V,
-                                  float* dW, int64_t lddw, float* dBias, void* ws, size_t ws_bytes, void* stream);
-
-/* The training-path backward in one call: dH, dW / dBias, and dGate = go * dgr_rows (each may be NULL). */
-MCE_API int mce_bwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* go,
-                          const float* dgr_rows, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16, int64_t lddh,
-                          float* dW, int64_t lddw, float* dBias, float* dGate, void* ws, size_t ws_bytes,
+                          int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows,
+                          float* wgt_rows, float* dgr_rows, float* loss_sum, void* dH_part, int dh_bf16,
+                          int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes,
                           void* stream);
 
 /*
  * Forward of the training path with a sparse logit bias (plain cross-entropy): logits[n, cand[n, j]] += cval[n, j]
- * (j < kc <= 8; repeated ids add up; ids outside [0, V_real) are ignored), as mce_fwd_sparse. Writes E' and a into
- * ws like mce_fwd_train, with the candidates' entries from their biased logits, so the backward is
- * mce_bwd_train_dhidden / mce_bwd_train_dweight plus mce_bwd_train_dcval. Replaces `_LinearCESparse.forward`
- * (fused_ops.py:71-91): the logits GEMM, the scatter of b into the bf16 logits (fused_ops.py:84) and
- * `_ce_grad_kernel`.
+ * (j < kc <= 8; repeated ids add up; ids outside [0, V_real) are ignored), as mce_fwd_sparse; otherwise as
+ * mce_fwd_train (the candidates' E' entries come from their biased logits), followed by mce_bwd_train and
+ * mce_bwd_train_dcval. Replaces `_LinearCESparse.forward` (fused_ops.py:71-91): the logits GEMM, the scatter of b
+ * into the bf16 logits (fused_ops.py:84), `_ce_grad_kernel` and the gradient GEMMs.
  */
 MCE_API int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                                  const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N,
-                                 int64_t K, int64_t V, int64_t V_real, float* loss_rows, float* lse_rows,
-                                 float* wgt_rows, float* loss_sum, void* ws, size_t ws_bytes, void* stream);
+                                 int64_t K, int64_t V, int64_t V_real, int64_t block_rows, int want,
+                                 float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* dH_part,
+                                 int dh_bf16, int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part,
+                                 void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Backward of the training path (`go`: the fp32 upstream gradient of the loss sum on the device): dH = go * G W
+ * (bf16 or fp32 like dH_part, row stride lddh), dW = go * G^T H (fp32 [V, K], row stride lddw), dBias =
+ * go * sum_n G[n, :] and dGate = go * dgr_rows; each output may be NULL, but the set of dH / dW / dBias must be the
+ * forward's `want`. With more than one block the forward's partial sums are read (dH_part rows are scaled into dH;
+ * dW_part / dBias_part are added in the last block's epilogues) and are left unchanged, so a second backward of the
+ * same forward gives the same result; an output may also be its own partial sum (in place). Replaces
+ * `_LinearCEMix.backward` (fused_ops.py:159-162): `gh * go`, `gw * go`, `dg * go`, and the last chunk's GEMMs.
+ */
+MCE_API int mce_bwd_train(const uint16_t* H, int64_t ldh, const float* go, const float* dgr_rows, int64_t N,
+                          int64_t K, int64_t V, int64_t block_rows, const void* dH_part, const float* dW_part,
+                          const float* dBias_part, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
+                          float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream);
 
 /* Gradient of the sparse bias values after mce_fwd_train_sparse: dCval[n, j] = go * G[n, cand[n, j]] (0 for
  * ignored ids), from the candidate logits kept in ws and the forward's lse_rows / wgt_rows. Replaces the
  * `g.gather(1, cand)` of `_LinearCESparse.forward` (fused_ops.py:86) and its `* go` in the backward. */
 MCE_API int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval, int kc,
                                 const float* lse_rows, const float* wgt_rows, const float* go, int64_t N, int64_t K,
-                                int64_t V, int64_t V_real, float* dCval, void* ws, size_t ws_bytes, void* stream);
+                                int64_t V, int64_t V_real, int64_t block_rows, float* dCval, void* ws, size_t ws_bytes,
+                                void* stream);
 
-/* Copies the number of rows the last mce_fwd_train on this workspace wrote by the exact fallback pass into
- * *out (a device int), on `stream`. No counterpart in the reference (diagnostics and tests). */
-MCE_API int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int* out, void* stream);
+/* Copies the number of rows the last mce_fwd_train on this workspace wrote by the exact fallback pass (all
+ * blocks) into *out (a device int), on `stream`. No counterpart in the reference (diagnostics and tests). */
+MCE_API int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, int* out,
+                              void* stream);
 
 /* Test hook: the bound on a row's sum of E over one half tile (128 vocabulary rows) above which the row takes
  * the exact fallback pass; s_max <= 0 restores the default 2^64. Process-wide; affects later mce_fwd_train
  * calls. No counterpart in the reference. */
 MCE_API void mce_train_set_threshold(float s_max);
+
+/*
+ * Kernel timing for benchmarks. No counterpart in the reference. After mce_prof_start(), every launch of the
+ * library's contraction kernels records a pair of HIP events on its stream; mce_prof_stop() waits for them and
+ * writes, per class c < nclass, the summed kernel time in ms (ms[c]) and the number of launches (launches[c]), then
+ * stops recording. Classes: 0 the one-pass logits tiles (k_fwd_train), 1 the statistics-only logits tiles
+ * (k_fwd_tiles over all vocabulary tiles), 2 the recompute logits-gradient tiles (k_bwd_grad), 3 dH GEMMs, 4 dW
+ * GEMMs. Not for use inside graph capture.
+ */
+MCE_API int mce_prof_start(void);
+MCE_API int mce_prof_stop(double* ms, int64_t* launches, int nclass);
 
 #ifdef __cplusplus
 }

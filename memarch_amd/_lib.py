@@ -36,16 +36,18 @@ SIGNATURES = {
     "mce_bwd_dweight": (_INT, [_P, _I, _I, _I, _I, _P, _I, _P, _S, _P]),
     "mce_bwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P,
                        _S, _P]),
-    "mce_train_ws_bytes": (_S, [_I, _I, _I]),
-    "mce_fwd_train": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P]),
-    "mce_bwd_train_dhidden": (_INT, [_P, _I, _P, _I, _I, _I, _P, _INT, _I, _P, _S, _P]),
-    "mce_bwd_train_dweight": (_INT, [_P, _I, _P, _I, _I, _I, _P, _I, _P, _P, _S, _P]),
-    "mce_bwd_train": (_INT, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P, _S, _P]),
-    "mce_fwd_train_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _P, _P, _P, _P, _P, _S,
-                                    _P]),
-    "mce_bwd_train_dcval": (_INT, [_P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _P, _P, _S, _P]),
-    "mce_train_flagged": (_INT, [_P, _I, _I, _I, _P, _P]),
+    "mce_train_ws_bytes": (_S, [_I, _I, _I, _I]),
+    "mce_train_block_rows": (_I, [_I, _I, _I, _I]),
+    "mce_fwd_train": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _INT, _P, _P, _P, _P, _P, _P, _INT,
+                             _I, _P, _I, _P, _P, _S, _P]),
+    "mce_fwd_train_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _I, _INT, _P, _P, _P, _P,
+                                    _P, _INT, _I, _P, _I, _P, _P, _S, _P]),
+    "mce_bwd_train": (_INT, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _INT, _I, _P, _I, _P, _P, _P, _S, _P]),
+    "mce_bwd_train_dcval": (_INT, [_P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _S, _P]),
+    "mce_train_flagged": (_INT, [_P, _I, _I, _I, _I, _P, _P]),
     "mce_train_set_threshold": (None, [ctypes.c_float]),
+    "mce_prof_start": (_INT, []),
+    "mce_prof_stop": (_INT, [_P, _P, _INT]),
     # include/mce_induct.h
     "mce_induct": (_INT, [_P, _I, _I, _INT, _INT, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "mce_induct_max_len": (_INT, []),

@@ -28,7 +28,10 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <algorithm>
+#include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "../../include/mce.h"
 
@@ -834,6 +837,53 @@ __global__ __launch_bounds__(256) void k_fill_f32(float* __restrict__ p, int64_t
   if (i < n) p[i] = v;
 }
 
+// p[r * ld + c] = v for r < rows, c < cols.
+__global__ __launch_bounds__(256) void k_fill2d_f32(float* __restrict__ p, int64_t ld, int64_t rows, int64_t cols,
+                                                    float v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < rows * cols) p[(i / cols) * ld + i % cols] = v;
+}
+
+// dst[r, c] = go[0] * src[r, c] for r < rows, c < cols (cols % 8 == 0, strides multiples of 8 elements), bf16 (BF16)
+// or fp32 values, 8 per thread; dst may be src.
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_scale_rows(const void* src, int64_t lds, void* dst, int64_t ldd,
+                                                    int64_t rows, int64_t cols, const float* __restrict__ go) {
+  const int64_t per = cols / 8, i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * per) return;
+  const int64_t r = i / per, c = (i % per) * 8;
+  const float g = go[0];
+  if constexpr (BF16) {
+    u16x8 v = *reinterpret_cast<const u16x8*>(reinterpret_cast<const uint16_t*>(src) + r * lds + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (uint16_t)(pack_bf16x2(g * bf16_to_f32(v[e]), 0.f) & 0xFFFFu);
+    *reinterpret_cast<u16x8*>(reinterpret_cast<uint16_t*>(dst) + r * ldd + c) = v;
+  } else {
+    const float4* sp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(src) + r * lds + c);
+    float4 a = sp[0], b = sp[1];
+    a.x *= g; a.y *= g; a.z *= g; a.w *= g;
+    b.x *= g; b.y *= g; b.z *= g; b.w *= g;
+    float4* dp = reinterpret_cast<float4*>(reinterpret_cast<float*>(dst) + r * ldd + c);
+    dp[0] = a;
+    dp[1] = b;
+  }
+}
+
+// out[0] = sum of the `count` ints p[0 .. count-1] (one block).
+__global__ __launch_bounds__(256) void k_sum_i32(const int* __restrict__ p, int64_t count, int* __restrict__ out) {
+  __shared__ int red[256];
+  const int t = threadIdx.x;
+  int s = 0;
+  for (int64_t i = t; i < count; i += 256) s += p[i];
+  red[t] = s;
+  __syncthreads();
+  for (int k = 128; k > 0; k >>= 1) {
+    if (t < k) red[t] += red[t + k];
+    __syncthreads();
+  }
+  if (t == 0) out[0] = red[0];
+}
+
 // Deterministic sum of `count` partials into out[0] (one block).
 __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int64_t count, float* __restrict__ out) {
   __shared__ float red[256];
@@ -1087,9 +1137,10 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 // dBias[v] = sum over the `rows` partial rows of column v (two per row tile: one per wave column; ldp, the row
 // stride, is a multiple of 64). A block covers 64 columns: thread t sums columns 4*(t%16) .. +3 over the rows
 // t/16, t/16 + 16, ... with 16-byte loads, and the 16 row-group sums are added in a fixed order, so the result is
-// deterministic.
+// deterministic; plus cin[v] (null: none; it may be dbias itself), times go[0] (1 when null).
 __global__ __launch_bounds__(256) void k_dbias_reduce(const float* __restrict__ part, int rows, int64_t ldp,
-                                                      int64_t V, float* __restrict__ dbias) {
+                                                      int64_t V, float* dbias, const float* __restrict__ go = nullptr,
+                                                      const float* cin = nullptr) {
   __shared__ float4 red[16][16];
   const int c4 = threadIdx.x & 15, g = threadIdx.x >> 4;
   const int64_t v = (int64_t)blockIdx.x * 64 + c4 * 4;
@@ -1112,7 +1163,7 @@ __global__ __launch_bounds__(256) void k_dbias_reduce(const float* __restrict__ 
       tot += e == 0 ? x.x : e == 1 ? x.y : e == 2 ? x.z : x.w;
     }
     const int64_t vo = (int64_t)blockIdx.x * 64 + threadIdx.x;
-    if (vo < V) dbias[vo] = tot;
+    if (vo < V) dbias[vo] = (go != nullptr ? go[0] : 1.f) * (tot + (cin != nullptr ? cin[vo] : 0.f));
   }
 }
 
@@ -1150,15 +1201,15 @@ __device__ __forceinline__ int64_t cm_index(int64_t m, int64_t k, int64_t Mp) {
 __device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xFFFFu); }
 
 // e_n per row from the two half-tile partials of vocabulary tile 0 (part_m / part_s rows 0 and 1) and the target
-// logit when the target lies outside tile 0; also clears the flags and the flagged-row counter.
+// logit when the target lies outside tile 0; also clears the flags and the ncount flagged-row counters.
 __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_m, const float* __restrict__ part_s,
                                                  const float* __restrict__ xy, const int64_t* __restrict__ y,
                                                  const int64_t* __restrict__ cand, const float* __restrict__ cval,
                                                  const float* __restrict__ xc, int kc, int64_t Vreal, int64_t N,
                                                  int64_t Np, float* __restrict__ lse_est, int* __restrict__ flag,
-                                                 int* __restrict__ flag_count) {
+                                                 int* __restrict__ counts, int ncount) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (n == 0) *flag_count = 0;
+  if (n < ncount) counts[n] = 0;
   if (n >= Np) return;
   flag[n] = 0;
   if (n >= N) {
@@ -1488,8 +1539,9 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Plain GEMM C[M, Nc] = A . B^T with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
-// nk_total K stages; with rscale, row i of C is multiplied by go[0] * rscale[i] first. DB > 0 (= fold_nr(tiles_n)):
+// Plain GEMM C[M, Nc] = s_i (A . B^T + Cin) with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
+// nk_total K stages: s_i = go[0] * rscale[i] (1 for a null go or rscale), Cin an fp32 matrix with C's row stride
+// (null: none; fp32 output only, and it may be C itself, an accumulation). DB > 0 (= fold_nr(tiles_n)):
 // block of tile (tm, tn < 8) also forms sum_k A(m, k) u(k) (u bf16 over the K positions) for the rows m of its
 // 32-row groups tn, tn + tiles_n, .. (DB of them), over its K range: DB 32-value partials per block (k_dbias_tiles
 // adds them up). The first `full` blocks each compute one whole tile (tiles 0 .. full-1 in the XCD-grouped
@@ -1499,9 +1551,9 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 template <bool OUT_BF16, bool KF, bool APC, int DB>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
-            int full, int P, void* __restrict__ C, int64_t ldc, float* __restrict__ part,
-            const float* __restrict__ rscale, const float* __restrict__ go, const uint16_t* __restrict__ u,
-            float* __restrict__ upart) {
+            int full, int P, void* C, int64_t ldc, float* __restrict__ part,
+            const float* __restrict__ rscale, const float* __restrict__ go, const float* cin,
+            const uint16_t* __restrict__ u, float* __restrict__ upart) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (DB > 0 ? 2048 : 0)];
   const int b = (int)blockIdx.x;
   int lin, s0 = 0, nk = nk_total, slot = -1;
@@ -1559,34 +1611,72 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
     return;
   }
   const float gs = go != nullptr ? go[0] : 1.f;
+  // The tile's 256 row scales go through LDS (free after gemm_tile's final barrier): one load per thread, so no
+  // global load sits between the stores below -- a load there would wait for the earlier stores too (the vector
+  // memory counter covers both) and expose the memory latency once per row.
+  float* rs = reinterpret_cast<float*>(lds + 64 * 1024);
+  if (rscale != nullptr) {
+    const int64_t i = m0 + t;
+    rs[t] = i < M ? gs * rscale[i] : 0.f;
+    __syncthreads();
+  }
+  // two halves of the wave's rows (M-subtiles 2mh, 2mh + 1); with Cin, all 128 of a half's Cin values are loaded
+  // before any of them is stored (Cin may be C itself, so a load may not move past an earlier store)
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mh = 0; mh < 2; ++mh) {
+    float cv[2][16][4];
+    if constexpr (!OUT_BF16) {
+      if (cin != nullptr) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t i = m0 + wm * 128 + acc_row(mi, r, lh);
-      if (i >= M) continue;
-      const float sc = rscale != nullptr ? gs * rscale[i] : 1.f;
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int nj = 0; nj < 4; ++nj) {
-        const int64_t j = n0 + wn * 128 + nj * 32 + lr;
-        if (j < Nc) {
-          const float o = rscale != nullptr ? sc * acc[mi][nj][r] : acc[mi][nj][r];
-          if constexpr (OUT_BF16)
-            reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)o;
-          else
-            reinterpret_cast<float*>(C)[i * ldc + j] = o;
-        }
+          for (int r = 0; r < 16; ++r) {
+            const int64_t i = m0 + wm * 128 + acc_row(2 * mh + q, r, lh);
+#pragma unroll
+            for (int nj = 0; nj < 4; ++nj) {
+              const int64_t j = n0 + wn * 128 + nj * 32 + lr;
+              cv[q][r][nj] = (i < M && j < Nc) ? __builtin_nontemporal_load(cin + i * ldc + j) : 0.f;
+            }
+          }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+#pragma unroll
+            for (int nj = 0; nj < 4; ++nj) cv[q][r][nj] = 0.f;
       }
     }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int mi = 2 * mh + q;
+        const int64_t i = m0 + wm * 128 + acc_row(mi, r, lh);
+        if (i >= M) continue;
+        const float sc = rscale != nullptr ? rs[wm * 128 + acc_row(mi, r, lh)] : gs;
+#pragma unroll
+        for (int nj = 0; nj < 4; ++nj) {
+          const int64_t j = n0 + wn * 128 + nj * 32 + lr;
+          if (j < Nc) {
+            if constexpr (OUT_BF16)
+              reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)(sc * acc[mi][nj][r]);
+            else
+              reinterpret_cast<float*>(C)[i * ldc + j] = sc * (acc[mi][nj][r] + cv[q][r][nj]);
+          }
+        }
+      }
+  }
 }
 
-// Sum of the P K-slices of each split tail tile into C (fixed order p = 0..P-1). Block (group of 4 rows, tile r);
+// Sum of the P K-slices of each split tail tile into C with k_gemm's epilogue (row scale, Cin) (fixed order
+// p = 0..P-1). Block (group of 4 rows, tile r);
 // thread t sums columns 4*(t%64) .. +3 of row 4*blockIdx.x + t/64 with 16-byte loads.
 template <bool OUT_BF16>
 __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ part, int P, int full, int tiles_m,
                                                      int tiles_n, int group, int64_t M, int64_t Nc,
-                                                     void* __restrict__ C, int64_t ldc,
-                                                     const float* __restrict__ rscale, const float* __restrict__ go) {
+                                                     void* C, int64_t ldc, const float* __restrict__ rscale,
+                                                     const float* __restrict__ go, const float* cin) {
   const int r = (int)blockIdx.y;
   int tm, tn;
   tile_of(full + r, tiles_m, tiles_n, group, tm, tn);
@@ -1601,31 +1691,40 @@ __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ p
   }
   const int64_t i = (int64_t)tm * BM + il;
   if (i >= M) return;
-  const float sc = rscale != nullptr ? (go != nullptr ? go[0] : 1.f) * rscale[i] : 1.f;
-  const float o[4] = {sc * s.x, sc * s.y, sc * s.z, sc * s.w};
+  const float gs = go != nullptr ? go[0] : 1.f;
+  const float sc = rscale != nullptr ? gs * rscale[i] : gs;
+  const float o[4] = {s.x, s.y, s.z, s.w};
+  float c[4] = {0.f, 0.f, 0.f, 0.f};  // Cin loaded before the stores (it may be C itself)
+  if (!OUT_BF16 && cin != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t j = (int64_t)tn * BN + jl + e;
+      if (j < Nc) c[e] = cin[i * ldc + j];
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t j = (int64_t)tn * BN + jl + e;
     if (j < Nc) {
       if constexpr (OUT_BF16)
-        reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)o[e];
+        reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)(sc * o[e]);
       else
-        reinterpret_cast<float*>(C)[i * ldc + j] = o[e];
+        reinterpret_cast<float*>(C)[i * ldc + j] = sc * (o[e] + c[e]);
     }
   }
 }
 
 // dBias of the training path from the dW blocks' dot-product partials (k_gemm<.., DB>): row group rg = (v%256)/32
 // of tile row v/256 belongs to tile column tn = rg % tiles_n as its group j = rg / tiles_n; dbias[v] = that
-// partial at row v%32 -- or, for a tile of the split tail, the sum of its P K-slice partials in a fixed order. One
-// thread per v.
+// partial at row v%32 -- or, for a tile of the split tail, the sum of its P K-slice partials in a fixed order --
+// plus cin[v] (null: none; it may be dbias itself, an accumulation), times go[0] (1 when null). One thread per v.
 __device__ __forceinline__ int lin_of(int tm, int tn, int tiles_m, int tiles_n, int group) {
   const int g = tm / group, first = g * group, gsize = min(tiles_m - first, group);
   return g * group * tiles_n + tn * gsize + (tm - first);
 }
 __global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ upart, int tiles_m, int tiles_n,
                                                      int nr, int group, int full, int P, int64_t V,
-                                                     float* __restrict__ dbias) {
+                                                     const float* __restrict__ go, const float* cin, float* dbias) {
   const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (v >= V) return;
   const int tm = (int)(v / BM), rg = (int)((v % BM) / 32), m = (int)(v % 32);
@@ -1638,7 +1737,7 @@ __global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ u
   } else {
     for (int p = 0; p < P; ++p) s += upart[((T + (int64_t)(lin - full) * P + p) * nr + j) * 32 + m];
   }
-  dbias[v] = s;
+  dbias[v] = (go != nullptr ? go[0] : 1.f) * (s + (cin != nullptr ? cin[v] : 0.f));
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1723,19 +1822,77 @@ int check_common(const void* H, int64_t ldh, const void* W, int64_t ldw, int64_t
 
 int check_bias(const float* bias) { return (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 3)) ? MCE_EALIGN : MCE_OK; }
 
-// C = A . B^T over nk stages with the tile grid of k_gemm. When the tiles leave a partial last wave, the R tail
-// tiles are split into P = CUs / R K-slices (at least 2 stages each) so the last wave fills the GPU.
+// Kernel-class timing for benchmarks (mce_prof_start / mce_prof_stop): while enabled, a pair of HIP events is
+// recorded on the launch stream around every launch of the classes below.
+enum { PROF_FWD_TRAIN = 0, PROF_FWD_TILES = 1, PROF_BWD_GRAD = 2, PROF_GEMM_DH = 3, PROF_GEMM_DW = 4, PROF_NONE = 5,
+       PROF_CLASSES = 5 };
+struct ProfRec {
+  int cls;
+  hipEvent_t e0, e1;
+};
+std::atomic<bool> g_prof_on{false};
+std::mutex g_prof_mu;
+std::vector<ProfRec> g_prof_recs;
+std::vector<hipEvent_t> g_prof_pool;
+
+hipEvent_t prof_event() {  // with g_prof_mu held
+  if (!g_prof_pool.empty()) {
+    hipEvent_t e = g_prof_pool.back();
+    g_prof_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
+
+class ProfScope {
+ public:
+  ProfScope(int cls, hipStream_t st) : cls_(cls), st_(st) {
+    if (cls_ >= PROF_CLASSES || !g_prof_on.load(std::memory_order_relaxed)) return;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    e0_ = prof_event();
+    e1_ = prof_event();
+    if (e0_ == nullptr || e1_ == nullptr || hipEventRecord(e0_, st_) != hipSuccess) e0_ = nullptr;
+  }
+  ~ProfScope() { end(); }
+  // records the closing event now (later calls and the destructor do nothing)
+  void end() {
+    if (e0_ == nullptr) return;
+    const bool ok = hipEventRecord(e1_, st_) == hipSuccess;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    if (ok) {
+      g_prof_recs.push_back({cls_, e0_, e1_});
+    } else {
+      g_prof_pool.push_back(e0_);
+      g_prof_pool.push_back(e1_);
+    }
+    e0_ = nullptr;
+  }
+  ProfScope(const ProfScope&) = delete;
+  ProfScope& operator=(const ProfScope&) = delete;
+
+ private:
+  int cls_;
+  hipStream_t st_;
+  hipEvent_t e0_ = nullptr, e1_ = nullptr;
+};
+
+// C = s_i (A . B^T + Cin) over nk stages with the tile grid of k_gemm (s_i, Cin as there). When the tiles leave a
+// partial last wave (or do not fill the GPU once), the R tail tiles are split into P = CUs / R K-slices (at least 2
+// stages each) so the last wave fills the GPU.
 int launch_status();
 template <bool OUT_BF16>
 int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t Nc, int group, void* C, int64_t ldc,
                 float* part, hipStream_t st, const float* rscale = nullptr, const float* go = nullptr,
-                const uint16_t* u = nullptr, float* upart = nullptr, int* p_out = nullptr, int* full_out = nullptr) {
+                const float* cin = nullptr, const uint16_t* u = nullptr, float* upart = nullptr,
+                int* p_out = nullptr, int* full_out = nullptr, int pcls = PROF_NONE) {
   const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nc, BN), T = tiles_m * tiles_n;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                                hipSuccess || cus <= 0)
     cus = 256;
-  const int R = T > cus ? T % cus : 0;
+  if (OUT_BF16 && cin != nullptr) return MCE_EINVAL;
+  const int R = T % cus;
   int P = R ? cus / R : 1;
   if (P > nk / 2) P = nk / 2;
   if (R && P > TAIL_SLOTS / R) P = TAIL_SLOTS / R;
@@ -1746,17 +1903,16 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (B.cm) return MCE_EINVAL;  // only the A operand may be in the piece layout
   if (p_out) *p_out = P;
   if (full_out) *full_out = full;
+  // dot products with u: only for an A operand in the piece layout (G^T), fp32 output; with more than one row
+  // group per tile only for whole K stages
+  const int nr = fold_nr(tiles_n);
+  if (u != nullptr && (OUT_BF16 || !A.cm || upart == nullptr || (nr > 1 && !kf))) return MCE_EINVAL;
+  ProfScope prof(pcls, st);
   if (u != nullptr) {
-    // dot products with u: only for an A operand in the piece layout (G^T), fp32 output; with more than one row
-    // group per tile only for whole K stages
-    const int nr = fold_nr(tiles_n);
-    if constexpr (OUT_BF16) {
-      return MCE_EINVAL;
-    } else {
-      if (!A.cm || upart == nullptr || (nr > 1 && !kf)) return MCE_EINVAL;
+    if constexpr (!OUT_BF16) {
 #define MCE_GEMM_DB(KF_, NR_)                                                                                \
   hipLaunchKernelGGL((k_gemm<false, KF_, true, NR_>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, \
-                     tiles_n, group, full, P, C, ldc, part, rscale, go, u, upart)
+                     tiles_n, group, full, P, C, ldc, part, rscale, go, cin, u, upart)
       if (!kf)
         MCE_GEMM_DB(false, 1);
       else if (nr == 1)
@@ -1774,22 +1930,23 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   } else if (A.cm) {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
   } else {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
   }
+  prof.end();
   int rc = launch_status();
   if (rc || full == T) return rc;
   hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 4, T - full), dim3(256), 0, st, part, P, full, tiles_m,
-                     tiles_n, group, M, Nc, C, ldc, rscale, go);
+                     tiles_n, group, M, Nc, C, ldc, rscale, go, cin);
   return launch_status();
 }
 
@@ -1820,12 +1977,15 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
                      kc, N, K, V_real, xy, w.xc);
   if ((rc = launch_status())) return rc;
-  if (K % BK == 0)
-    hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
-                       tn, w.part_m, w.part_s);
-  else
-    hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
-                       tn, w.part_m, w.part_s);
+  {
+    ProfScope prof(PROF_FWD_TILES, st);
+    if (K % BK == 0)
+      hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
+                         tn, w.part_m, w.part_s);
+    else
+      hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
+                         tn, w.part_m, w.part_s);
+  }
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, cand, cval,
                      w.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, loss_part);
@@ -1872,7 +2032,7 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
   if (go == nullptr && ycoef == nullptr) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
-    if (dBias) (void)hipMemsetAsync(dBias, 0, sizeof(float) * V, st);
+    if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
     return launch_status();
   }
   if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows)) return MCE_EINVAL;
@@ -1891,14 +2051,17 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
                        lse_rows, wgt_rows, go, N, V_real, w.fix_col, w.fix_val, dCval);
     if ((rc = launch_status())) return rc;
   }
-  if (K % BK == 0)
-    hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                       lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
-                       dBias ? w.dbias_part : nullptr);
-  else
-    hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                       lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
-                       dBias ? w.dbias_part : nullptr);
+  {
+    ProfScope prof(PROF_BWD_GRAD, st);
+    if (K % BK == 0)
+      hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
+                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                         dBias ? w.dbias_part : nullptr);
+    else
+      hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
+                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                         dBias ? w.dbias_part : nullptr);
+  }
   if ((rc = launch_status())) return rc;
   if (dBias) {
     hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, 2 * tn, w.vp, V,
@@ -1912,33 +2075,69 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
   return MCE_OK;
 }
 
-// Training-path workspace: the backward workspace (G and Gt hold E', the transposed copies, partials), the
-// forward workspace after it, then e_n, a_n, go*a_n in bf16 (kperm order) (all [Np]), the dW blocks' dBias
-// partials, the flags and the flagged-row list ([Np]), and the counter.
+// Training-path workspace. The rows are processed in blocks of `nb` rows (a multiple of 256; the last block may be
+// shorter): per block E' in G / Gt (tile-blocked, the block's rows padded to a multiple of 256), the row-scaled
+// H^T copy and go*a in bf16 (kperm order), the half-tile partials and the flagged-row list, all reused block after
+// block (the last block's stay for the backward); once per call W^T (for dH), the first vocabulary tile's partials,
+// the target / candidate logits, e_n, a_n, the flags and the per-block flagged-row counts over all rows, the loss
+// partials, the dW blocks' dBias partials, the K-split tail tiles and the dBias GEMV partials.
 struct TrainWs {
-  BwdWs b;
-  FwdWs f;
-  float *lse_est, *arow, *upart;
-  uint16_t* uperm;
-  int *flag, *flag_list, *flag_count;
+  int64_t np, vp, nb, nblk;
+  uint16_t *G, *Gt, *Ht, *uperm, *Wt;
+  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *loss_part, *lse_est, *arow, *upart, *part, *dbias_part;
+  int *flag, *flag_list, *counts;
   size_t bytes;
 };
-TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
+constexpr int DBIAS_SPLITS = 8;
+// Memory for the G / G^T pair of one row block when the caller leaves the block size to the library: 2 GiB, i.e.
+// 8192 rows at V = 50304 and 4096 rows at V = 131072.
+constexpr int64_t TRAIN_BLOCK_BUDGET = int64_t(2) << 30;
+
+// Rows per block: the requested count (0: the largest that keeps G / G^T within TRAIN_BLOCK_BUDGET) rounded up to
+// a multiple of 256, then evened out over the blocks it takes.
+int64_t train_block_rows(int64_t N, int64_t V, int64_t req) {
+  const int64_t np = cdiv(N, BLK) * BLK, vp = cdiv(V, BLK) * BLK;
+  int64_t cap = req > 0 ? cdiv(req, BLK) * BLK : TRAIN_BLOCK_BUDGET / (4 * vp) / BLK * BLK;
+  if (cap < BLK) cap = BLK;
+  if (cap >= np) return np > 0 ? np : BLK;
+  return cdiv(cdiv(np, cdiv(np, cap)), BLK) * BLK;
+}
+
+TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req) {
   TrainWs w{};
-  w.b = bwd_ws_layout(base, N, K, V);
-  size_t off = align256(w.b.bytes);
-  w.f = fwd_ws_layout(base == nullptr ? nullptr : base + off, N, V);
-  off = align256(off + w.f.bytes);
-  const int64_t np = w.b.np;
-  w.lse_est = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
-  w.arow = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * np);
-  w.uperm = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * np);
-  // dW blocks' dBias partials: 32 values per tile of the dW grid and per tail K slice
-  w.upart = reinterpret_cast<float*>(base + off);
-  off = align256(off + sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.b.vp / BM) * cdiv(K, BN) + TAIL_SLOTS));
-  w.flag = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
-  w.flag_list = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * np);
-  w.flag_count = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
+  w.np = cdiv(N, BLK) * BLK;
+  w.vp = cdiv(V, BLK) * BLK;
+  w.nb = train_block_rows(N, V, req);
+  w.nblk = cdiv(N, w.nb);
+  const int64_t T = 2 * (w.vp / BM), np = w.np > 0 ? w.np : BLK, nb = w.nb;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base == nullptr ? nullptr : base + off;
+    off = align256(off + bytes);
+    return p;
+  };
+  w.G = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * nb));
+  w.Gt = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * nb));
+  w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb * K));
+  w.uperm = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb));
+  w.part_m = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
+  w.part_s = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
+  w.flag_list = reinterpret_cast<int*>(take(sizeof(int) * nb));
+  w.Wt = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * K));
+  w.p0m = reinterpret_cast<float*>(take(sizeof(float) * 2 * np));
+  w.p0s = reinterpret_cast<float*>(take(sizeof(float) * 2 * np));
+  w.xy = reinterpret_cast<float*>(take(sizeof(float) * np));
+  w.xc = reinterpret_cast<float*>(take(sizeof(float) * np * MAX_KC));
+  w.loss_part = reinterpret_cast<float*>(take(sizeof(float) * cdiv(np, 32)));
+  w.lse_est = reinterpret_cast<float*>(take(sizeof(float) * np));
+  w.arow = reinterpret_cast<float*>(take(sizeof(float) * np));
+  w.flag = reinterpret_cast<int*>(take(sizeof(int) * np));
+  w.counts = reinterpret_cast<int*>(take(sizeof(int) * (np / BLK)));
+  // dW blocks' dBias partials: 32 values per row group, tile of the dW grid and tail K slice
+  w.upart = reinterpret_cast<float*>(
+      take(sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.vp / BM) * cdiv(K, BN) + TAIL_SLOTS)));
+  w.part = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * BM * BN));
+  w.dbias_part = reinterpret_cast<float*>(take(sizeof(float) * DBIAS_SPLITS * w.vp));
   w.bytes = off;
   return w;
 }
@@ -1946,131 +2145,198 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
 float g_train_s_max = TRAIN_S_MAX;
 constexpr int REPAIR_BLOCKS = 1024;
 
-// Forward of the one-pass training path (mixture or plain cross-entropy, no sparse bias): the per-row outputs of
-// fwd_impl plus E' in the workspace's G / Gt and a_n.
+template <typename T>
+inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
+
+// The gradient contractions of row block b: dH rows = s * a_n (E' W) into dH (bf16 or fp32, row stride lddh);
+// dW = s (E'^T (a . H) + dW_in) and dBias = s (E'^T a + dBias_in), with s = go[0] (1 when go is null); any output may
+// be null; dW_in / dBias_in may be null (none) or equal to the outputs (an accumulation).
+int train_block_grads(const TrainWs& w, int64_t b, const uint16_t* H, int64_t ldh, int64_t N, int64_t K,
+                      int64_t V, const float* go, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
+                      const float* dW_in, float* dBias, const float* dBias_in, hipStream_t st) {
+  int rc;
+  const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
+  if (dH != nullptr) {
+    const Operand Aop{w.G, 0, rows, w.vp, rp * BLK, 1};
+    const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
+    const int nk = (int)(w.vp / BK);
+    rc = dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, rows, K, 4, reinterpret_cast<uint16_t*>(dH) + row0 * lddh, lddh,
+                                     w.part, st, w.arow + row0, go, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                     PROF_GEMM_DH)
+                 : launch_gemm<false>(Aop, Bop, nk, rows, K, 4, reinterpret_cast<float*>(dH) + row0 * lddh, lddh,
+                                      w.part, st, w.arow + row0, go, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                      PROF_GEMM_DH);
+    if (rc) return rc;
+  }
+  if (dW == nullptr && dBias == nullptr) return MCE_OK;
+  if (dW != nullptr) {
+    // H^T of the block scaled by a (and, for dBias, a itself in bf16); dW = E'^T (a . H), and the dW tiles also form
+    // the dBias partials sum_n E'[n, v] a_n, each over its share of the K stages (k_dbias_tiles adds them)
+    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(rp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st,
+                       H + row0 * ldh, ldh, rows, K, w.Ht, w.arow + row0, nullptr, dBias ? w.uperm : nullptr);
+    if ((rc = launch_status())) return rc;
+    const Operand Aop{w.Gt, 0, V, rp, w.vp * BLK, 1};
+    const Operand Bop{w.Ht, BLK, K, rp, K * BLK, 0};
+    int P = 1, full = 0;
+    if ((rc = launch_gemm<false>(Aop, Bop, (int)(rp / BK), V, K, 4, dW, lddw, w.part, st, nullptr, go, dW_in,
+                                 dBias ? w.uperm : nullptr, w.upart, &P, &full, PROF_GEMM_DW)))
+      return rc;
+    if (dBias == nullptr) return MCE_OK;
+    hipLaunchKernelGGL(k_dbias_tiles, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.upart, (int)cdiv(V, BM),
+                       (int)cdiv(K, BN), fold_nr(cdiv(K, BN)), 4, full, P, V, go, dBias_in, dBias);
+    return launch_status();
+  }
+  // dBias without dW: a pass over the block's G^T
+  const int nt = (int)(rp / BM);
+  const int per = (int)cdiv(nt, DBIAS_SPLITS);
+  const int splits = (int)cdiv(nt, per);
+  hipLaunchKernelGGL(k_dbias_gemv, dim3((unsigned)(w.vp / BM), (unsigned)splits), dim3(256), 0, st, w.Gt,
+                     w.arow + row0, nullptr, rp, w.vp, per, w.dbias_part);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, splits, w.vp, V,
+                     dBias, go, dBias_in);
+  return launch_status();
+}
+
+// Forward of the one-pass training path (mixture or plain cross-entropy, optionally a sparse bias), block by block:
+// the per-row outputs of fwd_impl; E' and a_n of each block; for every block but the last, its gradient
+// contractions with go = 1 into the partial sums dH_part (its rows), dW_part and dBias_part (the first block
+// writes them, the later ones accumulate). The last block's contractions run in bwd_train_impl. want: MCE_GRAD_*.
 int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                    const int64_t* y, const float* gate, const float* hit, const int64_t* cand, const float* cval,
-                   int kc, int64_t N, int64_t K, int64_t V, int64_t V_real, float* loss_rows, float* lse_rows,
-                   float* wgt_rows, float* dgr_rows, float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
+                   int kc, int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows, int want,
+                   float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
+                   void* dH_part, int dh_bf16, int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part,
+                   void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (!rc) rc = check_bias(bias);
   if (!rc) rc = check_sparse(cand, cval, kc);
   if (!rc && kc > 0 && gate != nullptr) rc = MCE_EINVAL;  // the sparse bias is for plain cross-entropy
   if (rc) return rc;
-  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr)) return MCE_EINVAL;
+  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~7)) return MCE_EINVAL;
+  if ((want & MCE_GRAD_BIAS) && bias == nullptr) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
-    (void)hipMemsetAsync(loss_sum, 0, sizeof(float), st);
+    hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, loss_sum, (int64_t)1, 0.f);
     return launch_status();
   }
   if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
-  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V, block_rows);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
+  const bool more = w.nblk > 1;  // blocks before the last one write the partial sums
+  if (more && (((want & MCE_GRAD_H) && (!dH_part || lddh < K)) || ((want & MCE_GRAD_W) && (!dW_part || lddw < K)) ||
+               ((want & MCE_GRAD_BIAS) && !dBias_part)))
+    return MCE_EINVAL;
+  const int tv = (int)(w.vp / BM), tn = (int)cdiv(N, BN);
+  const Operand Wop{W, ldw, V, K, 0};
   const bool kf = K % BK == 0;
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand,
-                     cval, kc, N, K, V_real, w.f.xy, w.f.xc);
+                     cval, kc, N, K, V_real, w.xy, w.xc);
   if ((rc = launch_status())) return rc;
-  // e_n: the first vocabulary tile (one tile row of k_fwd_tiles) and the target logit
-  if (kf)
-    hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
-                       w.f.part_m, w.f.part_s);
-  else
-    hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
-                       w.f.part_m, w.f.part_s);
+  {
+    // e_n: the first vocabulary tile (one tile row of k_fwd_tiles over all rows) and the target logit
+    const Operand Hop{H, ldh, N, K, 0};
+    if (kf)
+      hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
+                         w.p0m, w.p0s);
+    else
+      hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
+                         w.p0m, w.p0s);
+    if ((rc = launch_status())) return rc;
+  }
+  hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, cval,
+                     w.xc, kc, V_real, N, w.np, w.lse_est, w.flag, w.counts, (int)(w.np / BLK));
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, w.f.part_m, w.f.part_s, w.f.xy,
-                     y, cand, cval, w.f.xc, kc, V_real, N, w.b.np, w.lse_est, w.flag, w.flag_count);
-  if ((rc = launch_status())) return rc;
-  if (kf)
-    hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est, N,
-                       w.b.np, V, w.b.vp, V_real, tv, tn, g_train_s_max, w.b.G, w.b.Gt, w.f.part_m, w.f.part_s,
-                       w.flag);
-  else
-    hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est, N,
-                       w.b.np, V, w.b.vp, V_real, tv, tn, g_train_s_max, w.b.G, w.b.Gt, w.f.part_m, w.f.part_s,
-                       w.flag);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.f.part_m, w.f.part_s, w.f.xy,
-                     cand, cval, w.f.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows,
-                     w.f.loss_part);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_train_rows, dim3((unsigned)cdiv(w.b.np, 256)), dim3(256), 0, st, y, w.f.xy, cand, cval,
-                     w.f.xc, kc, w.lse_est,
-                     lse_rows, wgt_rows, w.flag, N, w.b.np, w.b.vp, V_real, w.arow, w.flag_count, w.flag_list, w.b.G,
-                     w.b.Gt);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval, kc,
-                     lse_rows, wgt_rows, K, V, w.b.vp, V_real, w.b.np, w.flag_count, w.flag_list, w.b.G, w.b.Gt);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.f.loss_part, (int64_t)cdiv(N, 32), loss_sum);
+  if (want & MCE_GRAD_H) {
+    // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V
+    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
+                       ldw, V, K, w.Wt, nullptr, nullptr, nullptr);
+    if ((rc = launch_status())) return rc;
+  }
+  for (int64_t b = 0; b < w.nblk; ++b) {
+    const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
+    const int tnb = (int)(rp / BN);
+    const Operand Hop{H + row0 * ldh, ldh, rows, K, 0};
+    {
+      ProfScope prof(PROF_FWD_TRAIN, st);
+      if (kf)
+        hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est + row0,
+                           rows, rp, V, w.vp, V_real, tv, tnb, g_train_s_max, w.G, w.Gt, w.part_m, w.part_s,
+                           w.flag + row0);
+      else
+        hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias,
+                           w.lse_est + row0, rows, rp, V, w.vp, V_real, tv, tnb, g_train_s_max, w.G, w.Gt, w.part_m,
+                           w.part_s, w.flag + row0);
+    }
+    if ((rc = launch_status())) return rc;
+    hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(rows, 32)), dim3(256), 0, st, w.part_m, w.part_s,
+                       w.xy + row0, at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, V_real,
+                       at(gate, row0), at(hit, row0), rows, 2 * tv, loss_rows + row0, lse_rows + row0,
+                       wgt_rows + row0, at(dgr_rows, row0), w.loss_part + row0 / 32);
+    if ((rc = launch_status())) return rc;
+    hipLaunchKernelGGL(k_train_rows, dim3((unsigned)(rp / 256)), dim3(256), 0, st, y + row0, w.xy + row0,
+                       at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, w.lse_est + row0,
+                       lse_rows + row0, wgt_rows + row0, w.flag + row0, rows, rp, w.vp, V_real, w.arow + row0,
+                       w.counts + b, w.flag_list, w.G, w.Gt);
+    if ((rc = launch_status())) return rc;
+    hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, W, ldw, bias, y + row0,
+                       at(cand, row0 * kc), at(cval, row0 * kc), kc, lse_rows + row0, wgt_rows + row0, K, V, w.vp,
+                       V_real, rp, w.counts + b, w.flag_list, w.G, w.Gt);
+    if ((rc = launch_status())) return rc;
+    if (b + 1 < w.nblk) {
+      const bool first = b == 0;
+      if ((rc = train_block_grads(w, b, H, ldh, N, K, V, nullptr, (want & MCE_GRAD_H) ? dH_part : nullptr, dh_bf16,
+                                  lddh, (want & MCE_GRAD_W) ? dW_part : nullptr, lddw, first ? nullptr : dW_part,
+                                  (want & MCE_GRAD_BIAS) ? dBias_part : nullptr, first ? nullptr : dBias_part, st)))
+        return rc;
+    }
+  }
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)cdiv(N, 32), loss_sum);
   return launch_status();
 }
 
-// dH = go a . (E' W) of the training path.
-int bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V, void* dH,
-                      int dh_bf16, int64_t lddh, void* ws, size_t ws_bytes, hipStream_t st) {
-  int rc = check_common(W, ldw, W, ldw, N, K, V, V);
-  if (rc) return rc;
-  if (N == 0) return MCE_OK;
-  if (!dH || !ws || !go || lddh < K) return MCE_EINVAL;
-  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
-  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.b.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
-                     ldw, V, K, w.b.Wt, nullptr, nullptr);
-  if ((rc = launch_status())) return rc;
-  const Operand Aop{w.b.G, 0, N, w.b.vp, w.b.np * BLK, 1};
-  const Operand Bop{w.b.Wt, BLK, K, w.b.vp, K * BLK};
-  const int nk = (int)(w.b.vp / BK);
-  return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.b.part, st, w.arow, go)
-                 : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.b.part, st, w.arow, go);
-}
-
-// dW = E'^T (go a . H) and dBias = E'^T (go a) of the training path (either output may be null).
-constexpr int DBIAS_SPLITS = 8;
-int bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N, int64_t K, int64_t V, float* dW,
-                      int64_t lddw, float* dBias, void* ws, size_t ws_bytes, hipStream_t st) {
+// Backward of the one-pass training path: the last block's contractions with go, added to the partial sums of the
+// earlier blocks (which are scaled by go): dH = go * [dH_part rows; last block], dW = go (dW_part + last block),
+// dBias likewise; dGate = go * dgr. Any output may be null; the partial inputs are needed (and may equal the
+// outputs) when the call has more than one block.
+int bwd_train_impl(const uint16_t* H, int64_t ldh, const float* go, const float* dgr_rows, int64_t N, int64_t K,
+                   int64_t V, int64_t block_rows, const void* dH_part, const float* dW_part,
+                   const float* dBias_part, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
+                   float* dBias, float* dGate, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = check_common(H, ldh, H, ldh, N, K, V, V);
   if (rc) return rc;
-  if (dW && lddw < K) return MCE_EINVAL;
+  if (block_rows < 0 || (dH && lddh < K) || (dW && lddw < K)) return MCE_EINVAL;
+  if ((dH || dW || dBias || dGate) && go == nullptr) return MCE_EINVAL;
   if (N == 0) {
-    if (dW) (void)hipMemset2DAsync(dW, sizeof(float) * lddw, 0, sizeof(float) * K, V, st);
-    if (dBias) (void)hipMemsetAsync(dBias, 0, sizeof(float) * V, st);
+    if (dW) {
+      hipLaunchKernelGGL(k_fill2d_f32, dim3((unsigned)cdiv(V * K, 256)), dim3(256), 0, st, dW, lddw, V, K, 0.f);
+      if ((rc = launch_status())) return rc;
+    }
+    if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
     return launch_status();
   }
-  if (!ws || !go) return MCE_EINVAL;
-  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (!ws) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V, block_rows);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  if (dW) {
-    // H^T scaled by go*a (and, for dBias, go*a itself in bf16); dW = E'^T (go a . H), and the blocks also form
-    // the dBias partials sum_n E'[n, v] go a_n, each over its share of the K stages (k_dbias_tiles adds them)
-    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.b.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st,
-                       H, ldh, N, K, w.b.Ht, w.arow, go, dBias ? w.uperm : nullptr);
+  const int64_t b = w.nblk - 1, row0 = b * w.nb;
+  if (row0 > 0 && ((dH && !dH_part) || (dW && !dW_part) || (dBias && !dBias_part))) return MCE_EINVAL;
+  if (dH && row0 > 0) {
+    const int64_t items = row0 * (K / 8);
+    if (dh_bf16)
+      hipLaunchKernelGGL(k_scale_rows<true>, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, st, dH_part, lddh, dH,
+                         lddh, row0, K, go);
+    else
+      hipLaunchKernelGGL(k_scale_rows<false>, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, st, dH_part, lddh, dH,
+                         lddh, row0, K, go);
     if ((rc = launch_status())) return rc;
-    const Operand Aop{w.b.Gt, 0, V, w.b.np, w.b.vp * BLK, 1};
-    const Operand Bop{w.b.Ht, BLK, K, w.b.np, K * BLK, 0};
-    int P = 1, full = 0;
-    const bool fold = dBias != nullptr;  // the dW tiles form dBias
-    if ((rc = launch_gemm<false>(Aop, Bop, (int)(w.b.np / BK), V, K, 4, dW, lddw, w.b.part, st, nullptr, nullptr,
-                                 fold ? w.uperm : nullptr, w.upart, &P, &full)))
-      return rc;
-    if (fold) {
-      hipLaunchKernelGGL(k_dbias_tiles, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.upart, (int)cdiv(V, BM),
-                         (int)cdiv(K, BN), fold_nr(cdiv(K, BN)), 4, full, P, V, dBias);
-      return launch_status();
-    }
   }
-  if (dBias) {  // dBias without dW: a pass over G^T
-    const int nt = (int)(w.b.np / BM);
-    const int per = (int)cdiv(nt, DBIAS_SPLITS);
-    const int splits = (int)cdiv(nt, per);
-    hipLaunchKernelGGL(k_dbias_gemv, dim3((unsigned)(w.b.vp / BM), (unsigned)splits), dim3(256), 0, st, w.b.Gt,
-                       w.arow, go, w.b.np, w.b.vp, per, w.b.dbias_part);
-    if ((rc = launch_status())) return rc;
-    hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.b.dbias_part, splits, w.b.vp,
-                       V, dBias);
-    if ((rc = launch_status())) return rc;
+  if ((rc = train_block_grads(w, b, H, ldh, N, K, V, go, dH, dh_bf16, lddh, dW, lddw, row0 > 0 ? dW_part : nullptr,
+                              dBias, row0 > 0 ? dBias_part : nullptr, st)))
+    return rc;
+  if (dGate) {
+    if (!dgr_rows) return MCE_EINVAL;
+    hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
+    return launch_status();
   }
   return MCE_OK;
 }
@@ -2236,8 +2502,10 @@ int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_
   const Operand Aop{w.G, 0, N, w.vp, w.np * BLK, 1};
   const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
   const int nk = (int)(w.vp / BK);
-  return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st)
-                 : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st);
+  return dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st, nullptr, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, nullptr, PROF_GEMM_DH)
+                 : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st, nullptr, nullptr, nullptr, nullptr,
+                                      nullptr, nullptr, nullptr, PROF_GEMM_DH);
 }
 
 int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_t V, float* dW, int64_t lddw,
@@ -2247,7 +2515,7 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
   if (!dW || lddw < K) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
-    (void)hipMemset2DAsync(dW, sizeof(float) * lddw, 0, sizeof(float) * K, V, st);
+    hipLaunchKernelGGL(k_fill2d_f32, dim3((unsigned)cdiv(V * K, 256)), dim3(256), 0, st, dW, lddw, V, K, 0.f);
     return launch_status();
   }
   if (!ws) return MCE_EINVAL;
@@ -2261,7 +2529,8 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
   // 32-wide groups' halves, and Gt's and Ht's columns N..Np-1 are zero
   const Operand Aop{w.Gt, 0, V, w.np, w.vp * BLK, 1};
   const Operand Bop{w.Ht, BLK, K, w.np, K * BLK, 0};
-  return launch_gemm<false>(Aop, Bop, (int)(w.np / BK), V, K, 4, dW, lddw, w.part, st);
+  return launch_gemm<false>(Aop, Bop, (int)(w.np / BK), V, K, 4, dW, lddw, w.part, st, nullptr, nullptr, nullptr,
+                            nullptr, nullptr, nullptr, nullptr, PROF_GEMM_DW);
 }
 
 int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
@@ -2276,73 +2545,102 @@ int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
   return MCE_OK;
 }
 
-size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V) {
-  if (N < 0 || V <= 0 || K <= 0) return 0;
-  return train_ws_layout(nullptr, N, K, V).bytes;
+size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V, int64_t block_rows) {
+  if (N < 0 || V <= 0 || K <= 0 || block_rows < 0) return 0;
+  return train_ws_layout(nullptr, N, K, V, block_rows).bytes;
+}
+
+int64_t mce_train_block_rows(int64_t N, int64_t K, int64_t V, int64_t block_rows) {
+  (void)K;
+  if (N < 0 || V <= 0 || block_rows < 0) return 0;
+  return train_block_rows(N, V, block_rows);
 }
 
 int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                   const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
-                  int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows,
-                  float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
-  return fwd_train_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, loss_rows, lse_rows,
-                        wgt_rows, dgr_rows, loss_sum, ws, ws_bytes, stream);
+                  int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows, float* wgt_rows,
+                  float* dgr_rows, float* loss_sum, void* dH_part, int dh_bf16, int64_t lddh, float* dW_part,
+                  int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes, void* stream) {
+  return fwd_train_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, block_rows, want,
+                        loss_rows, lse_rows, wgt_rows, dgr_rows, loss_sum, dH_part, dh_bf16, lddh, dW_part, lddw,
+                        dBias_part, ws, ws_bytes, stream);
 }
 
 int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                          const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K,
-                         int64_t V, int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows,
-                         float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
-  return fwd_train_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, cand, cval, kc, N, K, V, V_real, loss_rows,
-                        lse_rows, wgt_rows, nullptr, loss_sum, ws, ws_bytes, stream);
+                         int64_t V, int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows,
+                         float* wgt_rows, float* loss_sum, void* dH_part, int dh_bf16, int64_t lddh, float* dW_part,
+                         int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes, void* stream) {
+  return fwd_train_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, cand, cval, kc, N, K, V, V_real, block_rows, want,
+                        loss_rows, lse_rows, wgt_rows, nullptr, loss_sum, dH_part, dh_bf16, lddh, dW_part, lddw,
+                        dBias_part, ws, ws_bytes, stream);
+}
+
+int mce_bwd_train(const uint16_t* H, int64_t ldh, const float* go, const float* dgr_rows, int64_t N, int64_t K,
+                  int64_t V, int64_t block_rows, const void* dH_part, const float* dW_part, const float* dBias_part,
+                  void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw, float* dBias, float* dGate, void* ws,
+                  size_t ws_bytes, void* stream) {
+  return bwd_train_impl(H, ldh, go, dgr_rows, N, K, V, block_rows, dH_part, dW_part, dBias_part, dH, dh_bf16, lddh,
+                        dW, lddw, dBias, dGate, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
                         const float* wgt_rows, const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real,
-                        float* dCval, void* ws, size_t ws_bytes, void* stream) {
+                        int64_t block_rows, float* dCval, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_sparse(cand, cval, kc);
   if (rc) return rc;
-  if (N < 0 || K <= 0 || V <= 0 || V_real < 0 || V_real > V) return MCE_EINVAL;
+  if (N < 0 || K <= 0 || V <= 0 || V_real < 0 || V_real > V || block_rows < 0) return MCE_EINVAL;
   if (N == 0 || kc == 0) return MCE_OK;
   if (!y || !lse_rows || !wgt_rows || !go || !dCval || !ws) return MCE_EINVAL;
-  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V, block_rows);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
-                     y, cand, cval, kc, w.f.xy, w.f.xc, lse_rows, wgt_rows, go, N, V_real, nullptr, nullptr, dCval);
+                     y, cand, cval, kc, w.xy, w.xc, lse_rows, wgt_rows, go, N, V_real, nullptr, nullptr, dCval);
   return launch_status();
 }
 
-int mce_bwd_train_dhidden(const uint16_t* W, int64_t ldw, const float* go, int64_t N, int64_t K, int64_t V, void* dH,
-                          int dh_bf16, int64_t lddh, void* ws, size_t ws_bytes, void* stream) {
-  return bwd_train_dhidden(W, ldw, go, N, K, V, dH, dh_bf16, lddh, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, int* out, void* stream) {
+  if (ws == nullptr || out == nullptr || N <= 0 || K <= 0 || V <= 0 || block_rows < 0) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(const_cast<void*>(ws)), N, K, V, block_rows);
+  hipLaunchKernelGGL(k_sum_i32, dim3(1), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), w.counts, w.nblk, out);
+  return launch_status();
 }
 
-int mce_bwd_train_dweight(const uint16_t* H, int64_t ldh, const float* go, int64_t N, int64_t K, int64_t V, float* dW,
-                          int64_t lddw, float* dBias, void* ws, size_t ws_bytes, void* stream) {
-  return bwd_train_dweight(H, ldh, go, N, K, V, dW, lddw, dBias, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
-}
-
-int mce_bwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* go,
-                  const float* dgr_rows, int64_t N, int64_t K, int64_t V, void* dH, int dh_bf16, int64_t lddh,
-                  float* dW, int64_t lddw, float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream) {
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  int rc;
-  if (dH && (rc = bwd_train_dhidden(W, ldw, go, N, K, V, dH, dh_bf16, lddh, ws, ws_bytes, st))) return rc;
-  if ((dW || dBias) && (rc = bwd_train_dweight(H, ldh, go, N, K, V, dW, lddw, dBias, ws, ws_bytes, st))) return rc;
-  if (dGate && N > 0) {
-    if (!dgr_rows || !go) return MCE_EINVAL;
-    hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
-    return launch_status();
+int mce_prof_start(void) {
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  for (const ProfRec& r : g_prof_recs) {
+    g_prof_pool.push_back(r.e0);
+    g_prof_pool.push_back(r.e1);
   }
+  g_prof_recs.clear();
+  g_prof_on.store(true);
   return MCE_OK;
 }
 
-int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int* out, void* stream) {
-  if (ws == nullptr || out == nullptr || N <= 0 || K <= 0 || V <= 0) return MCE_EINVAL;
-  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(const_cast<void*>(ws)), N, K, V);
-  (void)hipMemcpyAsync(out, w.flag_count, sizeof(int), hipMemcpyDeviceToDevice,
-                       reinterpret_cast<hipStream_t>(stream));
-  return launch_status();
+int mce_prof_stop(double* ms, int64_t* launches, int nclass) {
+  g_prof_on.store(false);
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  for (int c = 0; c < nclass; ++c) {
+    if (ms) ms[c] = 0.0;
+    if (launches) launches[c] = 0;
+  }
+  int rc = MCE_OK;
+  for (const ProfRec& r : g_prof_recs) {
+    float t = 0.f;
+    const hipError_t e = hipEventSynchronize(r.e1);
+    const hipError_t e2 = e == hipSuccess ? hipEventElapsedTime(&t, r.e0, r.e1) : e;
+    if (e2 != hipSuccess) {
+      g_last_hip_error = (int)e2;
+      rc = MCE_ELAUNCH;
+    } else if (r.cls < nclass) {
+      if (ms) ms[r.cls] += t;
+      if (launches) launches[r.cls] += 1;
+    }
+    g_prof_pool.push_back(r.e0);
+    g_prof_pool.push_back(r.e1);
+  }
+  g_prof_recs.clear();
+  return rc;
 }
 
 void mce_train_set_threshold(float s_max) { g_train_s_max = s_max > 0.f ? s_max : TRAIN_S_MAX; }

@@ -7,14 +7,17 @@ w, gate and the sparse values b in their own dtypes; None for y, hit, cand and c
 current stream; there is no other code path, and a tensor that is not on a GPU raises.
 
 When any input needs a gradient, the forward runs the one-pass training path (mce_fwd_train, or
-mce_fwd_train_sparse with a sparse bias): like the reference (fused_ops.py:148-155) it forms the logits gradient
-during the forward, as a bf16 N x V buffer of exp(x - e_n) with one per-row factor left to the backward, and never
-stores the logits; the backward then runs only the dH and dW contractions (and the candidates' gradient from the
-per-row state). Otherwise -- no gradient needed, or RECOMPUTE set (environment MEMARCH_AMD_RECOMPUTE=1) -- the
-forward computes only the per-row statistics and the
-backward recomputes the logits tile by tile to form the gradient. `chunk` is accepted and ignored (tiling is
-internal). Logits are fp32 in both paths (never rounded to bf16), and rows with P below the 1e-30 clamp get zero
-gradient, as the reference's eager formula does (full2.py:1925-1929).
+mce_fwd_train_sparse with a sparse bias): like the reference (fused_ops.py:148-155) it forms the gradients during
+the forward, row block by row block, never storing the logits: each block's logits gradient exists only as a bf16
+block x V buffer of exp(x - e_n) with one per-row factor applied in the contractions, and every block but the last
+adds its dH rows, dW and dBias to partial sums (for go = 1); the backward runs the last block's contractions with
+go, adds the partial sums in their epilogues and scales the earlier dH rows (and forms the candidates' gradient
+from the per-row state). The rows per block come from the library (a 2 GiB bound on the block's buffer, or
+BLOCK_ROWS, environment MEMARCH_AMD_BLOCK_ROWS); `chunk` is accepted and ignored. Otherwise -- no gradient needed,
+or RECOMPUTE set (environment MEMARCH_AMD_RECOMPUTE=1) -- the forward computes only the per-row statistics and the
+backward recomputes the logits tile by tile to form the gradient. Logits are fp32 in both paths (never rounded to
+bf16), and rows with P below the 1e-30 clamp get zero gradient, as the reference's eager formula does
+(full2.py:1925-1929).
 """
 import os
 
@@ -25,6 +28,8 @@ from . import _lib
 _BF16 = torch.bfloat16
 MAX_KC = 8   # sparse candidates per row of linear_ce_sparse (the library's limit)
 RECOMPUTE = os.environ.get("MEMARCH_AMD_RECOMPUTE", "0") == "1"   # True: the two-pass (recompute) backward
+BLOCK_ROWS = int(os.environ.get("MEMARCH_AMD_BLOCK_ROWS", "0"))   # rows per block of the one-pass path (0: library)
+GRAD_H, GRAD_W, GRAD_BIAS = 1, 2, 4   # MCE_GRAD_* of include/mce.h
 
 
 def _stream(dev):
@@ -75,10 +80,11 @@ def _check_sparse(cand, cval, n, gate):
     return kc
 
 
-def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=False):
+def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=False, want=0):
     """Validates the inputs, prepares the bf16 operands and runs mce_fwd (or mce_fwd_sparse when a sparse bias
-    cand/cval [N, k] is given, or mce_fwd_train for train=True) on the current stream. Returns (operands, per-row
-    outputs, loss_sum, meta, training workspace or None)."""
+    cand/cval [N, k] is given, or for train=True the one-pass mce_fwd_train / mce_fwd_train_sparse, forming the
+    gradients `want` names, GRAD_* bits) on the current stream. Returns (operands, per-row outputs, loss_sum, meta, training state or
+    None); the training state holds the workspace and the partial sums of the gradients the backward completes."""
     if h.dim() != 2 or w.dim() != 2 or h.shape[1] != w.shape[1]:
         raise ValueError(f"h {tuple(h.shape)} and w {tuple(w.shape)} must be [N, K] and [V, K]")
     n, k = h.shape
@@ -108,19 +114,35 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
     loss_sum = torch.empty((), **f32)
     lib = _lib.load()
     if train:
-        ws_bytes = lib.mce_train_ws_bytes(n, kp, v)
+        if bf is None:
+            want &= ~GRAD_BIAS
+        ws_bytes = lib.mce_train_ws_bytes(n, kp, v, BLOCK_ROWS)
         tws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        nb = lib.mce_train_block_rows(n, kp, v, BLOCK_ROWS)
+        r = (max(n, 1) + nb - 1) // nb * nb - nb   # rows of the blocks before the last: the partial sums' rows
+        dh_bf16 = h.dtype == _BF16
+        parts = dict(dh=None, dw=None, dbias=None)
+        if r > 0:
+            if want & GRAD_H:
+                parts["dh"] = torch.empty(r, kp, dtype=_BF16 if dh_bf16 else torch.float32, device=dev)
+            if want & GRAD_W:
+                parts["dw"] = torch.empty(v, kp, **f32)
+            if want & GRAD_BIAS:
+                parts["dbias"] = torch.empty(v, **f32)
+        pd, pw, pb = (_ptr(parts[x]) for x in ("dh", "dw", "dbias"))
         if kc:
             _lib.call("mce_fwd_train_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
-                      _ptr(cand64), _ptr(cval32), kc, n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt),
-                      _ptr(loss_sum), _ptr(tws), ws_bytes, _stream(dev))
+                      _ptr(cand64), _ptr(cval32), kc, n, kp, v, v_real, BLOCK_ROWS, want, _ptr(loss_rows), _ptr(lse),
+                      _ptr(wgt), _ptr(loss_sum), pd, int(dh_bf16), kp, pw, kp, pb, _ptr(tws), ws_bytes,
+                      _stream(dev))
             dgr.zero_()
         else:
             _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
-                      _ptr(hf), n, kp, v, v_real, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(loss_sum),
-                      _ptr(tws), ws_bytes, _stream(dev))
+                      _ptr(hf), n, kp, v, v_real, BLOCK_ROWS, want, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr),
+                      _ptr(loss_sum), pd, int(dh_bf16), kp, pw, kp, pb, _ptr(tws), ws_bytes, _stream(dev))
         rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
-        return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real), tws
+        state = dict(ws=tws, want=want, block_rows=BLOCK_ROWS, dh_bf16=dh_bf16, **parts)
+        return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real), state
     ws_bytes = lib.mce_fwd_ws_bytes(n, kp, v)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     if cand64 is not None:
@@ -138,10 +160,18 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
 
 def _forward(ctx, h, w, bias, y, gate, hit, v_real, cand=None, cval=None):
     train = ctx is not None and any(ctx.needs_input_grad) and not RECOMPUTE
-    (hd, wd, bf, y64, c64, cv32), rows, loss_sum, meta, tws = _fwd_launch(h, w, bias, y, gate, hit, v_real, cand,
-                                                                          cval, train)
-    ctx.save_for_backward(hd, wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"], c64, cv32)
-    ctx.train_ws = tws   # the one-pass path's E' and row factors, read by the backward (None: recompute)
+    want = 0
+    if train:
+        # the contractions for h, w and the bias; dgate and dcval come from the per-row state
+        need = ctx.needs_input_grad
+        want = (GRAD_H if need[0] else 0) | (GRAD_W if need[1] else 0) | (GRAD_BIAS if bias is not None and need[2]
+                                                                          else 0)
+    (hd, wd, bf, y64, c64, cv32), rows, loss_sum, meta, state = _fwd_launch(h, w, bias, y, gate, hit, v_real, cand,
+                                                                            cval, train, want)
+    # the one-pass backward needs no W (its W^T copy is in the workspace)
+    ctx.save_for_backward(hd, None if state is not None else wd, bf, y64, rows["lse"], rows["wgt"], rows["dgr"], c64,
+                          cv32)
+    ctx.train = state   # the one-pass path's workspace and partial sums, read by the backward (None: recompute)
     ctx.meta = meta
     ctx.dtypes = (h.dtype, w.dtype, None if gate is None else gate.dtype, None if bias is None else bias.dtype,
                   None if cval is None else cval.dtype)
@@ -178,28 +208,27 @@ def _backward(ctx, go, need_h, need_w, need_b, need_g, need_c=False):
     dbias = torch.empty(v, **f32) if (need_b and bf is not None) else None
     dcval = torch.empty(c64.shape, **f32) if (need_c and c64 is not None) else None
     dh = dw = None
-    tws = getattr(ctx, "train_ws", None)
-    if tws is not None:
+    state = getattr(ctx, "train", None)
+    if state is not None:
         st = _stream(dev)
+        tws, want = state["ws"], state["want"]
         nb = tws.numel()
+        need_h, need_w = need_h and bool(want & GRAD_H), need_w and bool(want & GRAD_W)
+        if dbias is not None and not want & GRAD_BIAS:
+            dbias = None
+        dhf = torch.empty(n, kp, dtype=_BF16 if state["dh_bf16"] else torch.float32, device=dev) if need_h else None
+        dwf = torch.empty(v, kp, **f32) if need_w else None
+        _lib.call("mce_bwd_train", _ptr(hd), hd.stride(0), _ptr(go32), _ptr(dgr), n, kp, v, state["block_rows"],
+                  _ptr(state["dh"]) if need_h else None, _ptr(state["dw"]) if need_w else None,
+                  _ptr(state["dbias"]) if dbias is not None else None, _ptr(dhf), int(state["dh_bf16"]), kp,
+                  _ptr(dwf), kp, _ptr(dbias), _ptr(dgate), _ptr(tws), nb, st)
         if need_h:
-            out_bf16 = hdt == _BF16
-            dh = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev)
-            _lib.call("mce_bwd_train_dhidden", _ptr(wd), wd.stride(0), _ptr(go32), n, kp, v, _ptr(dh), int(out_bf16),
-                      dh.stride(0), _ptr(tws), nb, st)
-            dh = dh[:, :k].to(hdt)
-        if need_w or dbias is not None:
-            dwf = torch.empty(v, kp, **f32) if need_w else None
-            _lib.call("mce_bwd_train_dweight", _ptr(hd), hd.stride(0), _ptr(go32), n, kp, v, _ptr(dwf),
-                      kp if dwf is None else dwf.stride(0), _ptr(dbias), _ptr(tws), nb, st)
-            if need_w:
-                dw = dwf[:, :k].to(wdt)
-        if dgate is not None:
-            _lib.call("mce_bwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(go32), _ptr(dgr), n, kp,
-                      v, None, 0, kp, None, kp, None, _ptr(dgate), _ptr(tws), nb, st)
+            dh = dhf[:, :k].to(hdt)
+        if need_w:
+            dw = dwf[:, :k].to(wdt)
         if dcval is not None:
             _lib.call("mce_bwd_train_dcval", _ptr(y64), _ptr(c64), _ptr(cv32), c64.shape[1], _ptr(lse), _ptr(wgt),
-                      _ptr(go32), n, kp, v, v_real, _ptr(dcval), _ptr(tws), nb, st)
+                      _ptr(go32), n, kp, v, v_real, state["block_rows"], _ptr(dcval), _ptr(tws), nb, st)
     elif need_h or need_w or need_g or dbias is not None or dcval is not None:
         lib = _lib.load()
         ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)

@@ -85,10 +85,12 @@ def assert_parity(got, fwd, bwd, what=""):
     return errs
 
 
-def capi_train(case, go=1.0, s_max=None, dev="cuda"):
+def capi_train(case, go=1.0, s_max=None, dev="cuda", block_rows=0):
     """The one-pass training path through the C ABI directly (mce_fwd_train, mce_bwd_train) on bf16 copies of the
-    case's operands; s_max sets the fallback bound (mce_train_set_threshold) for this call only. Returns numpy
-    results and the number of rows written by the exact fallback pass."""
+    case's operands, in row blocks of `block_rows` (0: the library's choice); s_max sets the fallback bound
+    (mce_train_set_threshold) for this call only. The backward runs twice: the second must reproduce the first
+    bit for bit (it reads the forward's partial sums without changing them). Returns numpy results, the number of
+    rows written by the exact fallback pass and the number of blocks."""
     from memarch_amd import _lib
     lib = _lib.load()
     n, k = case["h"].shape
@@ -102,29 +104,43 @@ def capi_train(case, go=1.0, s_max=None, dev="cuda"):
     f32 = dict(dtype=torch.float32, device=dev)
     loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
     loss_sum = torch.empty((), **f32)
-    nb = lib.mce_train_ws_bytes(n, k, v)
+    nb = lib.mce_train_ws_bytes(n, k, v, block_rows)
     ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    rows = lib.mce_train_block_rows(n, k, v, block_rows)
+    blocks = -(-n // rows)
+    r = (blocks - 1) * rows
+    want = 1 | 2 | (4 if b is not None else 0)
+    dh_part = torch.empty(r, k, dtype=torch.bfloat16, device=dev) if r else None
+    dw_part = torch.empty(v, k, **f32) if r else None
+    db_part = torch.empty(v, **f32) if r and b is not None else None
     st = torch.cuda.current_stream().cuda_stream
     p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     if s_max is not None:
         lib.mce_train_set_threshold(float(s_max))
     try:
         _lib.call("mce_fwd_train", p(h), k, p(w), k, p(b), p(y), p(gate), p(hit), n, k, v, case["v_real"],
-                  p(loss_rows), p(lse), p(wgt), p(dgr), p(loss_sum), p(ws), nb, st)
+                  block_rows, want, p(loss_rows), p(lse), p(wgt), p(dgr), p(loss_sum), p(dh_part), 1, k, p(dw_part),
+                  k, p(db_part), p(ws), nb, st)
     finally:
         if s_max is not None:
             lib.mce_train_set_threshold(0.0)
     flagged = torch.zeros(1, dtype=torch.int32, device=dev)
-    _lib.call("mce_train_flagged", p(ws), n, k, v, p(flagged), st)
+    _lib.call("mce_train_flagged", p(ws), n, k, v, block_rows, p(flagged), st)
     go_t = torch.full((), go, **f32)
-    dh = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
-    dw = torch.empty(v, k, **f32)
-    dbias = torch.empty(v, **f32) if b is not None else None
-    dgate = torch.empty(n, **f32)
-    _lib.call("mce_bwd_train", p(h), k, p(w), k, p(go_t), p(dgr), n, k, v, p(dh), 1, k, p(dw), k, p(dbias),
-              p(dgate), p(ws), nb, st)
+    outs = []
+    for _ in range(2):
+        dh = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+        dw = torch.empty(v, k, **f32)
+        dbias = torch.empty(v, **f32) if b is not None else None
+        dgate = torch.empty(n, **f32)
+        _lib.call("mce_bwd_train", p(h), k, p(go_t), p(dgr), n, k, v, block_rows, p(dh_part), p(dw_part),
+                  p(db_part), p(dh), 1, k, p(dw), k, p(dbias), p(dgate), p(ws), nb, st)
+        outs.append((dh, dw, dbias, dgate))
     torch.cuda.synchronize()
+    for a, c in zip(outs[0], outs[1]):
+        assert a is None or torch.equal(a, c), "a second backward of the same forward differs"
+    dh, dw, dbias, dgate = outs[0]
     out = dict(loss=float(loss_sum) * go, dh=dh.float().cpu().numpy(), dw=dw.cpu().numpy(),
                dgate=dgate.cpu().numpy(), dbias=None if dbias is None else dbias.cpu().numpy(),
-               lse=lse.cpu().double().numpy(), flagged=int(flagged.item()))
+               lse=lse.cpu().double().numpy(), flagged=int(flagged.item()), blocks=blocks)
     return out

@@ -1,5 +1,7 @@
 """GPU parity of the one-pass training path (mce_fwd_train / mce_bwd_train), which forms the logits gradient in
-the forward from a per-row lower bound e_n of the lse, against the CPU oracle; the exact fallback for rows whose
+the forward from a per-row lower bound e_n of the lse, row block by row block (every block but the last adds its
+gradients to partial sums in the forward; the backward completes the last block and the sums), against the CPU
+oracle, with one block and with several (block_rows = 256, a ragged last block); the exact fallback for rows whose
 logits exceed e_n too far for the exponent range, forced from the host (a lowered bound) and by real inputs; and
 the two-pass (recompute) backward through the same autograd surface.
 
@@ -48,13 +50,37 @@ def test_capi_parity(shape):
     assert_parity(got, dict(fwd, loss_sum=fwd["loss_sum"] * go), bwd, f"train {shape}")
 
 
+BLOCK_SHAPES = [
+    # several 256-row blocks, the last one ragged: (N, K, V, v_real, bias)
+    (777, 520, 2051, 2000, True),      # 4 blocks (256, 256, 256, 9 rows)
+    (600, 2048, 9000, 8990, True),     # 3 blocks, dBias in the dW tiles, K-split dW tail in every block
+    (1000, 1024, 5000, 4990, True),    # 4 blocks, 2 row groups of dBias per dW tile
+    (513, 128, 700, None, False),      # 3 blocks, the last with one row; no bias (the folded layout)
+    (512, 256, 1000, 990, True),       # 2 whole blocks
+]
+
+
+@pytest.mark.parametrize("shape", BLOCK_SHAPES, ids=lambda s: "N{}_K{}_V{}_vr{}_b{}".format(*s))
+def test_capi_parity_blocks(shape):
+    N, K, V, vr, bias = shape
+    print(f"case {shape}, 256-row blocks", flush=True)
+    case = random_case(N, K, V, vr, bias, seed=N + K + V + 3)
+    go = 1.0 / N
+    got = capi_train(case, go=go, block_rows=256)
+    assert got["blocks"] == -(-N // 256) > 1
+    fwd, bwd = oracle_of(case, go=go)
+    assert got["flagged"] == 0
+    assert_parity(got, dict(fwd, loss_sum=fwd["loss_sum"] * go), bwd, f"train {shape} blocks")
+
+
 @pytest.mark.parametrize("shape", SHAPES[1:4], ids=lambda s: "N{}_K{}_V{}".format(*s[:3]))
-def test_forced_fallback_every_row(shape):
+@pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
+def test_forced_fallback_every_row(shape, block_rows):
     """A bound of 1e-30 on the half-tile sums flags every row: all E' rows come from the exact fallback pass."""
     N, K, V, vr, bias = shape
-    print(f"case {shape}", flush=True)
+    print(f"case {shape} block_rows={block_rows}", flush=True)
     case = random_case(N, K, V, vr, bias, seed=N + 5)
-    got = capi_train(case, s_max=1e-30)
+    got = capi_train(case, s_max=1e-30, block_rows=block_rows)
     fwd, bwd = oracle_of(case)
     assert got["flagged"] == N
     assert_parity(got, fwd, bwd, f"forced fallback {shape}")
@@ -87,9 +113,10 @@ def _peaked_case(n=600, k=128, v=1500, rows=(3, 4, 100, 255, 256, 599), seed=17)
     return case, len(rows)
 
 
-def test_natural_fallback_rows():
+@pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
+def test_natural_fallback_rows(block_rows):
     case, nflag = _peaked_case()
-    got = capi_train(case)
+    got = capi_train(case, block_rows=block_rows)
     fwd, bwd = oracle_of(case)
     assert got["flagged"] == nflag
     assert_parity(got, fwd, bwd, "natural fallback")
@@ -133,9 +160,23 @@ def test_paths_agree():
         assert d <= 1e-2, (key, d)
 
 
-def test_backward_twice_with_retain_graph():
+@pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
+def test_autograd_blocks(block_rows, monkeypatch):
+    """The autograd surface with the library's block choice and with 256-row blocks (3 blocks), fp32 and bf16 h."""
     from memarch_amd import fused_ops
-    case = random_case(300, 256, 1000, None, True, seed=41)
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", block_rows)
+    case = random_case(700, 384, 3000, 2990, True, seed=51)
+    for h_dtype in (torch.bfloat16, torch.float32):
+        got = gpu_run(case, go=1.0 / 700, h_dtype=h_dtype)
+        fwd, bwd = oracle_of(case, go=1.0 / 700)
+        assert_parity(got, fwd, bwd, f"autograd block_rows={block_rows} h={h_dtype}")
+
+
+@pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
+def test_backward_twice_with_retain_graph(block_rows, monkeypatch):
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", block_rows)
+    case = random_case(600, 256, 1000, None, True, seed=41)
     h = case["h"].cuda().bfloat16().requires_grad_()
     w = case["w"].cuda().requires_grad_()
     b = case["bias"].cuda().requires_grad_()
