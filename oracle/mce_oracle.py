@@ -17,6 +17,8 @@ Two independent restatements of the reference's eager formula (full2.py:1917-192
   Sparse bias (cand, cval [N, k]; `_LinearCESparse`, fused_ops.py:66-96, eager form full2.py:1920-1922):
   x[n, cand[n, j]] += cval[n, j] before everything else (repeated ids add up; ids outside [0, v_real) are
   ignored); dcval[n, j] = G[n, cand[n, j]].
+* `closed_form_torch`: the same closed form in torch, chunked, for whole-batch checks of the full-size
+  configurations on the GPU (fp32, TF32 off), where numpy in fp64 would take minutes.
 * `eager_ce_part`: the eager formula written with torch ops exactly as `_ce_part` composes them; torch
   autograd supplies its gradients, independently of the closed form above.
 * `lse_backward`: the (lse, x_y) gradient of `_ChunkCE` (full2.py:813-829): G = g_lse softmax + g_ly onehot,
@@ -139,6 +141,58 @@ def backward(h, w, y, gate, hit, bias=None, v_real=None, go=1.0, fwd=None, dtype
         dw += G.T @ hc
     dgate = go * fwd["dgr"]
     return dict(dh=dh, dw=dw, dbias=db, dgate=dgate, dcval=dc)
+
+
+def closed_form_torch(h, w, y, gate, hit, bias=None, v_real=None, go=1.0, chunk=2048):
+    """The closed form of `forward` / `backward` in torch, for whole-batch checks at sizes where numpy would take
+    minutes: fp32 (or fp64) tensors on any device, chunks of `chunk` rows, logits materialised one chunk at a time.
+    Returns dict(loss_rows, lse, wgt, dgr, dh, dw, dbias, dgate). Matmuls run at the inputs' precision; on a GPU the
+    caller turns TF32 off. Pinned against the numpy closed form in tests/test_oracle.py."""
+    import torch
+    N, K = h.shape
+    V = w.shape[0]
+    vr = V if v_real is None else v_real
+    dt = h.dtype
+    wt = w.t().contiguous()                      # [K, V]: no transposed view enters a matmul
+    cols = torch.arange(V, device=h.device)
+    mask = torch.where(cols < vr, 0.0, float("-inf")).to(dt)
+    b = mask if bias is None else bias.to(dt) + mask
+    out = {k: torch.empty(N, dtype=dt, device=h.device) for k in ("loss_rows", "lse", "wgt", "dgr")}
+    dh = torch.empty(N, K, dtype=dt, device=h.device)
+    dwt = torch.zeros(K, V, dtype=dt, device=h.device)   # dW^T, accumulated as (h^T) G
+    db = torch.zeros(V, dtype=dt, device=h.device)
+    for i in range(0, N, chunk):
+        hc = h[i:i + chunk]
+        yc = y[i:i + chunk]
+        x = hc @ wt + b
+        lse = torch.logsumexp(x, 1)
+        ok = (yc >= 0) & (yc < vr)
+        xy = torch.where(ok, x.gather(1, yc.clamp(0, V - 1)[:, None])[:, 0], torch.tensor(float("-inf"), dtype=dt,
+                                                                                          device=h.device))
+        py = torch.exp(xy - lse)
+        if gate is None:
+            loss = torch.where(ok, lse - torch.where(ok, xy, torch.zeros_like(xy)), torch.zeros_like(xy))
+            wgt = ok.to(dt)
+            dgr = torch.zeros_like(xy)
+        else:
+            g, ht = gate[i:i + chunk].to(dt), hit[i:i + chunk].to(dt)
+            P = (1 - g) * py + g * ht
+            clamped = ~(P >= CLAMP_P)
+            Pc = torch.where(clamped, torch.full_like(P, CLAMP_P), P)
+            loss = -torch.log(Pc)
+            wgt = torch.where(clamped, torch.zeros_like(P), (1 - g) * py / Pc)
+            dgr = torch.where(clamped, torch.zeros_like(P), (py - ht) / Pc)
+        G = torch.exp(x - lse[:, None])
+        rows = torch.nonzero(ok)[:, 0]
+        G[rows, yc[rows]] -= 1.0
+        G *= (go * wgt)[:, None]
+        db += G.sum(0)
+        dh[i:i + chunk] = G @ w
+        dwt += hc.t().contiguous() @ G
+        for k, v in (("loss_rows", loss), ("lse", lse), ("wgt", wgt), ("dgr", dgr)):
+            out[k][i:i + chunk] = v
+    out.update(dh=dh, dw=dwt.t().contiguous(), dbias=db, dgate=go * out["dgr"])
+    return out
 
 
 def eager_ce_part(hn, W, bias, y, c1, g):

@@ -211,3 +211,31 @@ def test_pins_catch_planted_mistakes(kind):
     caught = not (np.allclose(bad["dh"], dh, rtol=1e-6) and np.allclose(bad["dw"], dw, rtol=1e-6)
                   and np.allclose(bad["dbias"], db, rtol=1e-6, atol=1e-9))
     assert caught, kind
+
+
+@pytest.mark.parametrize("mode", ["mixture", "plain", "clamped"])
+def test_closed_form_torch_matches_numpy(mode):
+    """oracle.closed_form_torch (the whole-batch checker of the full-size GPU tests) equals the numpy closed form
+    in fp64, on a case with padded ids (v_real < V), out-of-range targets and rows several chunks apart."""
+    rng = np.random.default_rng(11)
+    N, K, V, vr = 70, 24, 90, 85
+    h = rng.standard_normal((N, K))
+    w = rng.standard_normal((V, K)) * (3.0 if mode == "clamped" else 0.3)
+    b = rng.standard_normal(V)
+    y = rng.integers(0, vr, N)
+    y[5] = vr + 2                      # an id past v_real: probability 0 (ignored in plain cross-entropy)
+    gate = None if mode == "plain" else 1 / (1 + np.exp(-rng.standard_normal(N)))
+    hit = None if mode == "plain" else (rng.random(N) < 0.3).astype(np.float64)
+    if mode == "clamped":
+        gate[:] = 0.0
+    go = 0.37
+    fwd = orc.forward(h, w, y, gate, hit, b, vr, np.float64)
+    bwd = orc.backward(h, w, y, gate, hit, b, vr, go, fwd, np.float64)
+    if mode == "clamped":
+        assert (~(fwd["P"] >= orc.CLAMP_P)).sum() > 0
+    t = lambda a: None if a is None else torch.from_numpy(np.asarray(a))  # noqa: E731
+    got = orc.closed_form_torch(t(h), t(w), t(y), t(gate), t(hit), t(b), vr, go, chunk=16)
+    for key, ref in (("loss_rows", fwd["loss_rows"]), ("lse", fwd["lse"]), ("wgt", fwd["wgt"]),
+                     ("dgr", fwd["dgr"]), ("dh", bwd["dh"]), ("dw", bwd["dw"]), ("dbias", bwd["dbias"]),
+                     ("dgate", bwd["dgate"])):
+        np.testing.assert_allclose(got[key].numpy(), ref, rtol=1e-10, atol=1e-12, err_msg=key)
