@@ -703,9 +703,11 @@ __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__
                                                     const float* __restrict__ bias, const int64_t* __restrict__ y,
                                                     const int64_t* __restrict__ cand, const float* __restrict__ cval,
                                                     int kc, int64_t N, int64_t K, int64_t Vreal,
-                                                    float* __restrict__ xy, float* __restrict__ xc) {
+                                                    float* __restrict__ xy, float* __restrict__ xc,
+                                                    int* __restrict__ zero = nullptr) {
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *zero = 0;  // k_fwd_merge's exact-row counter
   if (n >= N) return;
   const uint16_t* hr = H + n * ldh;
   const int64_t yn = y[n];
@@ -724,7 +726,11 @@ __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__
 // Merge of the T per-half-tile partials: lse, loss, wgt, dgr per row; one loss partial sum per block.
 // 32 rows per block, 8 threads per row (an online max / rescaled sum over every 8th partial), combined in LDS.
 // With a sparse bias (kc > 0) the tiles saw the logits without it: each distinct valid candidate c then moves
-// its term of the sum from exp(x_c) to exp(x_c + B_c), with the maximum raised first so no term overflows.
+// its term of the sum from exp(x_c) to exp(x_c + B_c), with the maximum raised first so no term overflows. The
+// term removed is computed from k_row_logits' x_c, which matches the tiles' own value only to fp32 rounding: where
+// negative biases remove nearly all of the sum (a candidate that dominates its row pushed far down), the two would
+// cancel each other and leave rounding noise, so a row whose corrected sum is not above 1/16 of the terms removed is
+// appended to exact_list (its lse, loss and wgt are then rewritten by k_exact_tiles / k_exact_rows).
 __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ part_m, const float* __restrict__ part_s,
                                                    const float* __restrict__ xy, const int64_t* __restrict__ cand,
                                                    const float* __restrict__ cval, const float* __restrict__ xc,
@@ -732,7 +738,8 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
                                                    const float* __restrict__ hit, int64_t N, int T,
                                                    float* __restrict__ loss_rows, float* __restrict__ lse_rows,
                                                    float* __restrict__ wgt_rows, float* __restrict__ dgr_rows,
-                                                   float* __restrict__ loss_part) {
+                                                   float* __restrict__ loss_part, int* __restrict__ exact_count,
+                                                   int* __restrict__ exact_list) {
   __shared__ float rm[8][32], rs[8][32], rl[32];
   const int t = threadIdx.x, r = t & 31, sl = t >> 5;
   const int64_t n = (int64_t)blockIdx.x * 32 + r;
@@ -786,13 +793,15 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
         for (int k = 0; k < kc; ++k)
           if (first_valid(cand, kc, n, k, Vreal))
             Mp = fmaxf(Mp, xc[n * kc + k] + sparse_bias(cand, cval, kc, n, cand[n * kc + k]));
-        float Sp = M == -INFINITY ? 0.f : S * expf(M - Mp);
+        float Sp = M == -INFINITY ? 0.f : S * expf(M - Mp), removed = 0.f;
         for (int k = 0; k < kc; ++k)
           if (first_valid(cand, kc, n, k, Vreal)) {
             const float x = xc[n * kc + k], B = sparse_bias(cand, cval, kc, n, cand[n * kc + k]);
             // exp(x + B - M') - exp(x - M'); expm1 keeps small |B| exact (and would overflow for large B)
             Sp += B < 20.f ? expf(x - Mp) * expm1f(B) : expf(x + B - Mp) - expf(x - Mp);
+            if (B < 0.f) removed += expf(x - Mp);
           }
+        if (exact_list != nullptr && !(Sp > 0.0625f * removed)) exact_list[atomicAdd(exact_count, 1)] = (int)n;
         M = Mp;
         S = Sp;
       }
@@ -897,6 +906,98 @@ __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int
     __syncthreads();
   }
   if (t == 0) out[0] = red[0];
+}
+
+// The exact lse of the rows k_fwd_merge listed (a sparse bias that removes nearly all of a row's sum): work item
+// i = (listed row list[i / tiles_v], vocabulary tile i % tiles_v), a grid-stride loop over the items. For the
+// item's 256 ids v (thread t: v = 256 (i % tiles_v) + t): x_v = b_v + h_n . w_v + the row's sparse bias on v (fp32
+// sums of the bf16 products; -inf for v >= V_real); the tile's (max, sum of exp(x - max)) go to
+// part_m / part_s[(i % tiles_v) * ld + i / tiles_v]. h_n is staged in LDS REPAIR_KC values at a time. It reads all
+// of W once per listed row, so it is a fallback, not a fast path.
+constexpr int REPAIR_KC = 16384;
+__global__ __launch_bounds__(256) void k_exact_tiles(const uint16_t* __restrict__ H, int64_t ldh,
+                                                     const uint16_t* __restrict__ W, int64_t ldw,
+                                                     const float* __restrict__ bias, const int64_t* __restrict__ cand,
+                                                     const float* __restrict__ cval, int kc, int64_t K, int64_t V,
+                                                     int64_t Vreal, int tiles_v, const int* __restrict__ count,
+                                                     const int* __restrict__ list, float* __restrict__ part_m,
+                                                     float* __restrict__ part_s, int64_t ld) {
+  __shared__ __attribute__((aligned(16))) uint16_t hs[REPAIR_KC];
+  __shared__ float red[2][8];
+  const int64_t items = (int64_t)(*count) * tiles_v;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int nkc = (int)((K + REPAIR_KC - 1) / REPAIR_KC);
+  for (int64_t i = blockIdx.x; i < items; i += gridDim.x) {
+    const int64_t j = i / tiles_v, tile = i % tiles_v;
+    const int64_t n = list[j];
+    const int64_t v = tile * BM + t;
+    float x = 0.f;
+    for (int c = 0; c < nkc; ++c) {
+      const int64_t k0 = (int64_t)c * REPAIR_KC;
+      const int kn = (int)((K - k0) < REPAIR_KC ? (K - k0) : REPAIR_KC);
+      __syncthreads();
+      for (int k = t * 8; k < kn; k += 256 * 8)
+        *reinterpret_cast<u16x8*>(hs + k) = *reinterpret_cast<const u16x8*>(H + n * ldh + k0 + k);
+      __syncthreads();
+      if (v < V) {
+        const uint16_t* wr = W + v * ldw + k0;
+        for (int k = 0; k < kn; k += 8) {
+          const u16x8 a = *reinterpret_cast<const u16x8*>(hs + k);
+          const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[e]), x);
+        }
+      }
+    }
+    x = v < Vreal ? x + (bias != nullptr ? bias[v] : 0.f) + sparse_bias(cand, cval, kc, n, v) : -INFINITY;
+    float m = x;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) red[0][wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float e = m == -INFINITY ? 0.f : expf(x - m);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) e += __shfl_xor(e, off);
+    if (lane == 0) red[1][wave] = e;
+    __syncthreads();
+    if (t == 0) {
+      part_m[tile * ld + j] = m;
+      part_s[tile * ld + j] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    }
+  }
+}
+
+// The listed rows' lse from k_exact_tiles' partials (tiles_v of them, row j at part_*[t * ld + j]) and their
+// plain cross-entropy loss and weight (the sparse bias comes with plain cross-entropy only): loss = lse - x_y,
+// wgt = 1, or 0 and 0 for a target outside [0, V_real) (xy = -inf). One thread per list entry.
+__global__ __launch_bounds__(256) void k_exact_rows(const int* __restrict__ count, const int* __restrict__ list,
+                                                    const float* __restrict__ part_m,
+                                                    const float* __restrict__ part_s, int64_t ld, int tiles_v,
+                                                    const float* __restrict__ xy, float* __restrict__ loss_rows,
+                                                    float* __restrict__ lse_rows, float* __restrict__ wgt_rows) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= *count) return;
+  float m = -INFINITY, s = 0.f;
+  for (int t = 0; t < tiles_v; ++t) {
+    const float mm = part_m[t * ld + j];
+    if (mm == -INFINITY) continue;
+    const float ss = part_s[t * ld + j];
+    if (mm > m) {
+      s = (m == -INFINITY ? 0.f : s * expf(m - mm)) + ss;
+      m = mm;
+    } else {
+      s += ss * expf(mm - m);
+    }
+  }
+  const int64_t n = list[j];
+  const float lse = m + logf(s);
+  const bool ok = xy[n] != -INFINITY;
+  lse_rows[n] = lse;
+  if (loss_rows != nullptr) {
+    loss_rows[n] = ok ? lse - xy[n] : 0.f;
+    wgt_rows[n] = ok ? 1.f : 0.f;
+  }
 }
 
 // Sparse fix-ups for k_bwd_grad, which writes go*wgt*exp(x - lse) from the logits without the sparse bias and
@@ -1383,7 +1484,6 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
 // -inf for v >= V_real), E'[n, v] = exp(x_v - lse_n) - [v = y_n] into G and Gt. h_n is staged in LDS 16384 values
 // at a time. This is the fallback for rows whose logits exceed e_n by about 44 or more, which the bound from the
 // first vocabulary tile and the target makes rare; it reads all of W once per flagged row.
-constexpr int REPAIR_KC = 16384;
 __global__ __launch_bounds__(256) void k_repair(const uint16_t* __restrict__ H, int64_t ldh,
                                                 const uint16_t* __restrict__ W, int64_t ldw,
                                                 const float* __restrict__ bias, const int64_t* __restrict__ y,
@@ -1752,11 +1852,12 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 struct FwdWs {
-  float *part_m, *part_s, *xy, *xc, *loss_part;
+  float *part_m, *part_s, *xy, *xc;
+  int *xcount, *xlist;
   size_t bytes;
 };
 // Forward workspace: per-half-tile (max, sum-exp) partials [2*tiles_v][N], target logits [N], candidate
-// logits [N][MAX_KC] (sparse bias only), loss partials.
+// logits [N][MAX_KC] (sparse bias only), the counter and list of the rows whose lse the exact pass rewrites.
 FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
   const int64_t T = 2 * cdiv(V, BM);
   FwdWs w{};
@@ -1765,7 +1866,8 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
   w.part_s = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N);
   w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * MAX_KC);
-  w.loss_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, 32));
+  w.xcount = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
+  w.xlist = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * N);
   w.bytes = off;
   return w;
 }
@@ -1965,17 +2067,33 @@ int check_sparse(const int64_t* cand, const float* cval, int kc) {
   return MCE_OK;
 }
 
-// The forward kernels: row logits (xy, and the candidate logits), tiles, merge. Outputs the merge does not
-// need to write may be null (loss_rows with wgt_rows, dgr_rows, loss_part).
+// The exact pass over the rows k_fwd_merge listed (count and list on the device): k_exact_tiles, k_exact_rows.
+// part_m / part_s (the merged partials, [>= tiles_v][N]) are reused as its scratch.
+constexpr int REPAIR_BLOCKS = 1024;
+int launch_exact(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                 const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K, int64_t V, int64_t V_real,
+                 int tv, const int* count, const int* list, float* part_m, float* part_s, const float* xy,
+                 float* loss_rows, float* lse_rows, float* wgt_rows, hipStream_t st) {
+  int rc;
+  hipLaunchKernelGGL(k_exact_tiles, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H, ldh, W, ldw, bias, cand, cval, kc, K, V,
+                     V_real, tv, count, list, part_m, part_s, N);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_exact_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, count, list, part_m, part_s, N, tv,
+                     xy, loss_rows, lse_rows, wgt_rows);
+  return launch_status();
+}
+
+// The forward kernels: row logits (xy, and the candidate logits), tiles, merge (and, with a sparse bias, the exact
+// pass). Outputs the merge does not need to write may be null (loss_rows with wgt_rows, dgr_rows).
 int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                const int64_t* y, const float* gate, const float* hit, const int64_t* cand, const float* cval, int kc,
                int64_t N, int64_t K, int64_t V, int64_t V_real, float* xy, float* loss_rows, float* lse_rows,
-               float* wgt_rows, float* dgr_rows, float* loss_part, hipStream_t st) {
+               float* wgt_rows, float* dgr_rows, hipStream_t st) {
   int rc;
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
-                     kc, N, K, V_real, xy, w.xc);
+                     kc, N, K, V_real, xy, w.xc, w.xcount);
   if ((rc = launch_status())) return rc;
   {
     ProfScope prof(PROF_FWD_TILES, st);
@@ -1988,8 +2106,12 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
   }
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, cand, cval,
-                     w.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, loss_part);
-  return launch_status();
+                     w.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, nullptr,
+                     kc > 0 ? w.xcount : nullptr, w.xlist);
+  if ((rc = launch_status())) return rc;
+  if (kc == 0) return MCE_OK;
+  return launch_exact(H, ldh, W, ldw, bias, cand, cval, kc, N, K, V, V_real, tv, w.xcount, w.xlist, w.part_m,
+                      w.part_s, xy, loss_rows, lse_rows, wgt_rows, st);
 }
 
 // Forward of every variant: gate and hit both given (mixture) or both null (plain cross-entropy); kc sparse
@@ -2012,9 +2134,9 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
   const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   if ((rc = fwd_launch(w, H, ldh, W, ldw, bias, y, gate, hit, cand, cval, kc, N, K, V, V_real, w.xy, loss_rows,
-                       lse_rows, wgt_rows, dgr_rows, w.loss_part, st)))
+                       lse_rows, wgt_rows, dgr_rows, st)))
     return rc;
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)cdiv(N, 32), loss_sum);
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, loss_rows, N, loss_sum);
   return launch_status();
 }
 
@@ -2084,8 +2206,8 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
 struct TrainWs {
   int64_t np, vp, nb, nblk;
   uint16_t *G, *Gt, *Ht, *uperm, *Wt;
-  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *loss_part, *lse_est, *arow, *upart, *part, *dbias_part;
-  int *flag, *flag_list, *counts;
+  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *lse_est, *arow, *upart, *part, *dbias_part;
+  int *flag, *flag_list, *counts, *xlist;
   size_t bytes;
 };
 constexpr int DBIAS_SPLITS = 8;
@@ -2128,11 +2250,13 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   w.p0s = reinterpret_cast<float*>(take(sizeof(float) * 2 * np));
   w.xy = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.xc = reinterpret_cast<float*>(take(sizeof(float) * np * MAX_KC));
-  w.loss_part = reinterpret_cast<float*>(take(sizeof(float) * cdiv(np, 32)));
   w.lse_est = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.arow = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.flag = reinterpret_cast<int*>(take(sizeof(int) * np));
-  w.counts = reinterpret_cast<int*>(take(sizeof(int) * (np / BLK)));
+  // per block: rows written by the exact E' pass (counts[b]), rows whose lse the exact pass rewrites
+  // (counts[np/256 + b]); the list of the latter, reused block after block
+  w.counts = reinterpret_cast<int*>(take(sizeof(int) * 2 * (np / BLK)));
+  w.xlist = reinterpret_cast<int*>(take(sizeof(int) * nb));
   // dW blocks' dBias partials: 32 values per row group, tile of the dW grid and tail K slice
   w.upart = reinterpret_cast<float*>(
       take(sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.vp / BM) * cdiv(K, BN) + TAIL_SLOTS)));
@@ -2143,7 +2267,6 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
 }
 
 float g_train_s_max = TRAIN_S_MAX;
-constexpr int REPAIR_BLOCKS = 1024;
 
 template <typename T>
 inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
@@ -2245,7 +2368,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
     if ((rc = launch_status())) return rc;
   }
   hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, cval,
-                     w.xc, kc, V_real, N, w.np, w.lse_est, w.flag, w.counts, (int)(w.np / BLK));
+                     w.xc, kc, V_real, N, w.np, w.lse_est, w.flag, w.counts, (int)(2 * w.np / BLK));
   if ((rc = launch_status())) return rc;
   if (want & MCE_GRAD_H) {
     // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V
@@ -2269,11 +2392,16 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
                            w.part_s, w.flag + row0);
     }
     if ((rc = launch_status())) return rc;
+    int* xcount = w.counts + w.np / BLK + b;
     hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(rows, 32)), dim3(256), 0, st, w.part_m, w.part_s,
                        w.xy + row0, at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, V_real,
                        at(gate, row0), at(hit, row0), rows, 2 * tv, loss_rows + row0, lse_rows + row0,
-                       wgt_rows + row0, at(dgr_rows, row0), w.loss_part + row0 / 32);
+                       wgt_rows + row0, at(dgr_rows, row0), nullptr, kc > 0 ? xcount : nullptr, w.xlist);
     if ((rc = launch_status())) return rc;
+    if (kc > 0 && (rc = launch_exact(H + row0 * ldh, ldh, W, ldw, bias, at(cand, row0 * kc), at(cval, row0 * kc), kc,
+                                     rows, K, V, V_real, tv, xcount, w.xlist, w.part_m, w.part_s, w.xy + row0,
+                                     loss_rows + row0, lse_rows + row0, wgt_rows + row0, st)))
+      return rc;
     hipLaunchKernelGGL(k_train_rows, dim3((unsigned)(rp / 256)), dim3(256), 0, st, y + row0, w.xy + row0,
                        at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, w.lse_est + row0,
                        lse_rows + row0, wgt_rows + row0, w.flag + row0, rows, rp, w.vp, V_real, w.arow + row0,
@@ -2291,7 +2419,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
         return rc;
     }
   }
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, w.loss_part, (int64_t)cdiv(N, 32), loss_sum);
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, loss_rows, N, loss_sum);
   return launch_status();
 }
 
@@ -2474,7 +2602,7 @@ int mce_lse_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, 
   const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   return fwd_launch(w, H, ldh, W, ldw, bias, y, nullptr, nullptr, nullptr, nullptr, 0, N, K, V, V_real, ly_rows,
-                    nullptr, lse_rows, nullptr, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream));
+                    nullptr, lse_rows, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
 int mce_bwd_lse_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,

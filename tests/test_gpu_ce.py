@@ -182,3 +182,53 @@ def test_sparse_zero_values_equal_plain():
     # equal up to fp32 rounding (the merge's running maximum may move by the candidate logits' rounding)
     torch.testing.assert_close(sp["loss_rows"], plain["loss_rows"], rtol=1e-6, atol=1e-6)
     torch.testing.assert_close(sp["lse"], plain["lse"], rtol=1e-6, atol=1e-6)
+
+
+def _dominant_case(N=600, K=128, V=1200, seed=61):
+    """Every row's first candidate (id 7) is its unbiased argmax by ~24 (h[:, 0] = 25 against w[7, 0] = 1, the
+    other logits ~N(0, 0.6^2)), and its sparse value is -30 .. -40, so the biased logit is far below the rest; every
+    other row also has a second, ordinary candidate. The tiles see the unbiased logits, in which the candidate
+    carries all but ~1e-8 of the softmax mass: moving its term by the bias must not cancel that mass against itself
+    (the merge falls back to an exact lse for such rows)."""
+    c = _case(N, K, V, kc=2, seed=seed, w_scale=0.05, v_scale=1.0)
+    c["h"][:, 0] = 0.0
+    c["w"][:, 0] = 0.0
+    c["w"][7, 0] = 1.0
+    c["h"][:, 0] = 25.0
+    c["y"][c["y"] == 7] = 8
+    c["cand"][:, 0] = 7
+    g = torch.Generator().manual_seed(seed + 1)
+    c["cval"][:, 0] = -30.0 - 10.0 * torch.rand(N, generator=g)
+    return c
+
+
+@pytest.mark.parametrize("mode", ["one_pass", "recompute", "fallback", "blocks"])
+def test_sparse_dominant_candidate_negative_bias(mode, monkeypatch):
+    from memarch_amd import _lib, fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", mode == "recompute")
+    if mode == "blocks":
+        monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256)
+    c = _dominant_case()
+    print(f"dominant candidate, {mode}", flush=True)
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    b = c["cval"].cuda().requires_grad_()
+    lib = _lib.load()
+    if mode == "fallback":
+        lib.mce_train_set_threshold(1e-30)
+    try:
+        loss = fused_ops.linear_ce_sparse(h, w, c["y"].cuda(), c["cand"].cuda(), b)
+    finally:
+        if mode == "fallback":
+            lib.mce_train_set_threshold(0.0)
+    rows = fused_ops.forward_rows(h.detach(), w.detach(), c["y"].cuda(), None, None, cand=c["cand"].cuda(),
+                                  cval=b.detach())
+    (loss * 0.5).backward()
+    fwd, bwd = _oracle(c, go=0.5)
+    x = orc.bf16_round(c["h"].numpy()) @ orc.bf16_round(c["w"].numpy()).T
+    assert (x[:, 7] - np.delete(x, 7, axis=1).max(1) > 20).all()      # the regime of the test
+    lse = rows["lse"].cpu().double().numpy()
+    assert np.isfinite(lse).all()
+    print(f"lse max abs err {np.abs(lse - fwd['lse']).max():.2e}", flush=True)
+    assert np.abs(lse - fwd["lse"]).max() <= 1e-3
+    _check(f"dominant candidate {mode}", loss, fwd, dict(dh=h.grad, dw=w.grad, dcval=b.grad), bwd)
