@@ -1286,7 +1286,7 @@ __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, co
 // Because e_n <= lse_n, E underflows only where the softmax is below e^-87 anyway. It could overflow only where a
 // logit exceeds e_n by more than ~88: a row whose sum of E over a half tile exceeds the bound s_max (or is not
 // finite) is flagged instead; its partials are then the usual (max, sum of exp(x - max)), so the merged lse is
-// exact, and k_repair rewrites its E' row exactly from a fresh dot-product pass with a_n = wgt_n.
+// exact, and k_exact_train rewrites its E' row exactly (an MFMA pass over the gathered rows) with a_n = wgt_n.
 
 // Largest accepted sum of E over one half tile (128 vocabulary rows): 2^64. With it every stored E' and every
 // sum over V of E' W stays far inside the fp32 / bf16 range. A test hook may lower it (mce_train_set_threshold).
@@ -1434,7 +1434,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
 
 // After the merge: a_n = wgt_n exp(e_n - lse_n), and the target element of E' (both buffers) for unflagged rows,
 // with a sparse bias also the entries of the row's candidates; flagged rows get a_n = wgt_n and are appended to
-// flag_list for k_repair. Rows N .. Np-1 get a_n = 0.
+// flag_list for the exact pass (k_gather_rows, k_exact_train, k_exact_fix). Rows N .. Np-1 get a_n = 0.
 __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ y, const float* __restrict__ xy,
                                                     const int64_t* __restrict__ cand, const float* __restrict__ cval,
                                                     const float* __restrict__ xc, int kc,
@@ -1478,62 +1478,112 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   }
 }
 
-// Exact E' rows of the flagged rows: work item i = (flagged row flag_list[i / tiles_v], vocabulary tile
-// i % tiles_v), a grid-stride loop over the items, so even one flagged row is spread over many workgroups. For
-// the item's 256 vocabulary rows v (thread t: v = v0 + t): x_v = b_v + h_n . w_v (fp32 sums of the bf16 products;
-// -inf for v >= V_real), E'[n, v] = exp(x_v - lse_n) - [v = y_n] into G and Gt. h_n is staged in LDS 16384 values
-// at a time. This is the fallback for rows whose logits exceed e_n by about 44 or more, which the bound from the
-// first vocabulary tile and the target makes rare; it reads all of W once per flagged row.
-__global__ __launch_bounds__(256) void k_repair(const uint16_t* __restrict__ H, int64_t ldh,
-                                                const uint16_t* __restrict__ W, int64_t ldw,
-                                                const float* __restrict__ bias, const int64_t* __restrict__ y,
-                                                const int64_t* __restrict__ cand, const float* __restrict__ cval,
-                                                int kc, const float* __restrict__ lse_rows,
-                                                const float* __restrict__ wgt_rows, int64_t K, int64_t V, int64_t Vp,
-                                                int64_t Vreal, int64_t Np, const int* __restrict__ flag_count,
-                                                const int* __restrict__ flag_list, uint16_t* __restrict__ G,
-                                                uint16_t* __restrict__ Gt) {
-  __shared__ __attribute__((aligned(16))) uint16_t hs[REPAIR_KC];
-  const int tiles_v = (int)(Vp / BM);
-  const int64_t items = (int64_t)(*flag_count) * tiles_v;
-  const int t = threadIdx.x;
-  const int nkc = (int)((K + REPAIR_KC - 1) / REPAIR_KC);
-  for (int64_t i = blockIdx.x; i < items; i += gridDim.x) {
-    const int64_t n = flag_list[i / tiles_v];
-    const int64_t v = (i % tiles_v) * BM + t;
-    const float l = lse_rows[n];
-    const int64_t yn = y[n];
-    // a row with wgt = 0 (under the clamp, or all its probability on the pointer) has a zero gradient: its E'
-    // row only has to be finite, so it is zeroed without the dot products
-    if (!(wgt_rows[n] != 0.f)) {
-      G[cm_index(n, v, Np)] = 0;
-      Gt[cm_index(v, n, Vp)] = 0;
-      continue;
-    }
-    float x = 0.f;
-    for (int kc = 0; kc < nkc; ++kc) {
-      const int64_t k0 = (int64_t)kc * REPAIR_KC;
-      const int kn = (int)((K - k0) < REPAIR_KC ? (K - k0) : REPAIR_KC);
-      __syncthreads();
-      for (int k = t * 8; k < kn; k += 256 * 8)
-        *reinterpret_cast<u16x8*>(hs + k) = *reinterpret_cast<const u16x8*>(H + n * ldh + k0 + k);
-      __syncthreads();
-      if (v < V) {
-        const uint16_t* wr = W + v * ldw + k0;
-        for (int k = 0; k < kn; k += 8) {
-          const u16x8 a = *reinterpret_cast<const u16x8*>(hs + k);
-          const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
+// The exact E' rows of the flagged rows (rows whose logits exceed e_n by about 44 or more, which the bound from
+// the first vocabulary tile and the target makes rare, or whose lse exceeds e_n by more than 60). Three kernels:
+// k_gather_rows copies the flagged rows of H into a dense operand Hf [F][K] (F = the flagged-row count); k_exact_train
+// runs the logits tile mainloop over (vocabulary tile, 256 gathered rows) items with each row shifted by its exact
+// lse, so E'[n, v] = exp(x_v - lse_n) (<= 1; a_n = wgt_n for these rows), and stores it in place: 16 bytes per lane
+// into G (the lane's own row), element by element into G^T (the rows are scattered); k_exact_fix then writes the
+// target's exp(x_y - lse) - 1 and, with a sparse bias, the candidates' exp(x_c + B_c - lse) over those entries.
+// The work is that of F rows of the forward tile pass (plus F * Vp scattered 2-byte stores), so the fallback costs
+// in proportion to the flagged rows; k_exact_train is a persistent loop whose item count it reads on the device.
+
+// Hf[i, :] = H[list[i], :] for i < *count (K % 8 == 0), 16 bytes per thread, grid-stride.
+__global__ __launch_bounds__(256) void k_gather_rows(const uint16_t* __restrict__ H, int64_t ldh,
+                                                     const int* __restrict__ list, const int* __restrict__ count,
+                                                     int64_t K, uint16_t* __restrict__ Hf) {
+  const int64_t per = K / 8, items = (int64_t)(*count) * per;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < items; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / per, c = (i % per) * 8;
+    *reinterpret_cast<u16x8*>(Hf + r * K + c) = *reinterpret_cast<const u16x8*>(H + (int64_t)list[r] * ldh + c);
+  }
+}
+
+template <bool KF>
+__global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
+void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, const float* __restrict__ bias,
+                   const int* __restrict__ count, const int* __restrict__ list, const float* __restrict__ lse_rows,
+                   int64_t Np, int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, uint16_t* __restrict__ G,
+                   uint16_t* __restrict__ Gt) {
+  __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
+  const int cnt = *count;
+  const int items = tiles_v * ((cnt + BN - 1) / BN);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+  const Operand Hop{Hf, K, cnt, K, 0};
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    const int tm = it % tiles_v, tn = it / tiles_v;
+    const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const float btile = tile_bias(bias, v0, V);
+    int64_t nrow[4];
+    float lb[4];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[e]), x);
+    for (int nj = 0; nj < 4; ++nj) {
+      const int64_t s = n0 + wn * 128 + nj * 32 + lr;   // slot in Hf
+      nrow[nj] = s < cnt ? list[s] : -1;
+      lb[nj] = nrow[nj] >= 0 ? lse_rows[nrow[nj]] * LOG2E : INFINITY;
+    }
+    f32x16 acc[4][4];
+    gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+                        reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj) {
+      const bool ok = nrow[nj] >= 0;
+      const int64_t n = ok ? nrow[nj] : 0;
+      // G: row n's block of vocabulary tile tm; the lane's 16 values of block mi sit at kperm positions
+      // wm*128 + mi*32 + 16lh + r, i.e. 16-byte chunks wm*16 + mi*4 + 2lh + r/8
+      uint16_t* grow = G + ((int64_t)tm * (Np / BM) + n / BM) * CM_TILE + ((n % BM) >> 3) * 32 * 64 + (n & 7) * 8 +
+                       (wm * 16 + 2 * lh) * 64;
+      // G^T: element (v, n) at block (n/256, v/256), piece (v%256/8, kperm(n%256)/8), offset (v%8)*8 + kperm%8;
+      // v%256 = wm*128 + mi*32 + 8(r/4) + 4lh + r%4, so piece row wm*16 + mi*4 + r/4 and v%8 = 4lh + r%4
+      const int kpn = kperm((int)(n & 255));
+      uint16_t* gtcol = Gt + ((n / BM) * (Vp / BM) + tm) * CM_TILE + (kpn >> 3) * 64 + (kpn & 7) +
+                        wm * 16 * 32 * 64 + lh * 4 * 8;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        uint32_t pk[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          pk[i] = pack_bf16x2(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][2 * i], LOG2E, -lb[nj])),
+                              __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][2 * i + 1], LOG2E, -lb[nj])));
+        if (ok) {
+#pragma unroll
+          for (int sc = 0; sc < 2; ++sc)
+            *reinterpret_cast<u32x4*>(grow + (mi * 4 + sc) * 64) =
+                u32x4{pk[4 * sc], pk[4 * sc + 1], pk[4 * sc + 2], pk[4 * sc + 3]};
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            gtcol[(mi * 4 + (r >> 2)) * 32 * 64 + (r & 3) * 8] = (uint16_t)((pk[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
         }
       }
     }
-    float g = 0.f;
-    if (v < Vreal) g = expf(x + (bias != nullptr ? bias[v] : 0.f) + (kc > 0 ? sparse_bias(cand, cval, kc, n, v) : 0.f) - l);
-    if (v == yn) g -= 1.f;
-    const uint16_t b = to_bf16(g);
-    G[cm_index(n, v, Np)] = b;
-    Gt[cm_index(v, n, Vp)] = b;
+  }
+}
+
+// The target and candidate entries of the rows k_exact_train rewrote (list[i], i < *count): E'[n, y_n] =
+// exp(x_y - lse_n) - 1 and, for each distinct valid candidate c != y_n, E'[n, c] = exp(x_c + B_c - lse_n), from the
+// row logits of k_row_logits (x_y with its sparse bias, x_c without), into G and G^T. One thread per entry.
+__global__ __launch_bounds__(256) void k_exact_fix(const int* __restrict__ count, const int* __restrict__ list,
+                                                   const int64_t* __restrict__ y, const float* __restrict__ xy,
+                                                   const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                   const float* __restrict__ xc, int kc,
+                                                   const float* __restrict__ lse_rows, int64_t Np, int64_t Vp,
+                                                   int64_t Vreal, uint16_t* __restrict__ G, uint16_t* __restrict__ Gt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= *count) return;
+  const int64_t n = list[i], yn = y[n];
+  const float l = lse_rows[n];
+  if (yn >= 0 && yn < Vreal) {
+    const uint16_t b = to_bf16(expf(xy[n] - l) - 1.f);
+    G[cm_index(n, yn, Np)] = b;
+    Gt[cm_index(yn, n, Vp)] = b;
+  }
+  for (int k = 0; k < kc; ++k) {
+    const int64_t c = cand[n * kc + k];
+    if (c == yn || !first_valid(cand, kc, n, k, Vreal)) continue;
+    const uint16_t b = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - l));
+    G[cm_index(n, c, Np)] = b;
+    Gt[cm_index(c, n, Vp)] = b;
   }
 }
 
@@ -2070,6 +2120,7 @@ int check_sparse(const int64_t* cand, const float* cval, int kc) {
 // The exact pass over the rows k_fwd_merge listed (count and list on the device): k_exact_tiles, k_exact_rows.
 // part_m / part_s (the merged partials, [>= tiles_v][N]) are reused as its scratch.
 constexpr int REPAIR_BLOCKS = 1024;
+constexpr int EXACT_BLOCKS = 256;  // workgroups of the persistent k_exact_train (one per CU)
 int launch_exact(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                  const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K, int64_t V, int64_t V_real,
                  int tv, const int* count, const int* list, float* part_m, float* part_s, const float* xy,
@@ -2407,9 +2458,20 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
                        lse_rows + row0, wgt_rows + row0, w.flag + row0, rows, rp, w.vp, V_real, w.arow + row0,
                        w.counts + b, w.flag_list, w.G, w.Gt);
     if ((rc = launch_status())) return rc;
-    hipLaunchKernelGGL(k_repair, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, W, ldw, bias, y + row0,
-                       at(cand, row0 * kc), at(cval, row0 * kc), kc, lse_rows + row0, wgt_rows + row0, K, V, w.vp,
-                       V_real, rp, w.counts + b, w.flag_list, w.G, w.Gt);
+    // the flagged rows' exact E' (the block's H^T buffer, rewritten later, holds their gathered rows)
+    hipLaunchKernelGGL(k_gather_rows, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, w.flag_list,
+                       w.counts + b, K, w.Ht);
+    if ((rc = launch_status())) return rc;
+    if (kf)
+      hipLaunchKernelGGL(k_exact_train<true>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias,
+                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, w.vp, V_real, tv, w.G, w.Gt);
+    else
+      hipLaunchKernelGGL(k_exact_train<false>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias,
+                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, w.vp, V_real, tv, w.G, w.Gt);
+    if ((rc = launch_status())) return rc;
+    hipLaunchKernelGGL(k_exact_fix, dim3((unsigned)(rp / 256)), dim3(256), 0, st, w.counts + b, w.flag_list, y + row0,
+                       w.xy + row0, at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, lse_rows + row0,
+                       rp, w.vp, V_real, w.G, w.Gt);
     if ((rc = launch_status())) return rc;
     if (b + 1 < w.nblk) {
       const bool first = b == 0;
