@@ -893,7 +893,30 @@ __global__ __launch_bounds__(256) void k_sum_i32(const int* __restrict__ p, int6
   if (t == 0) out[0] = red[0];
 }
 
-// Deterministic sum of `count` partials into out[0] (one block).
+// Deterministic sum of `count` values into out[0] in two levels: k_sum_chunks writes the sum of each SUM_CHUNK
+// values (block b: values [b*SUM_CHUNK, (b+1)*SUM_CHUNK), 16 per thread, independent loads) to part[b]; k_sum adds
+// the partials (one block). Fixed order throughout.
+constexpr int SUM_CHUNK = 4096;
+__global__ __launch_bounds__(256) void k_sum_chunks(const float* __restrict__ x, int64_t count,
+                                                    float* __restrict__ part) {
+  __shared__ float red[256];
+  const int t = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * SUM_CHUNK;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < SUM_CHUNK / 256; ++i) {
+    const int64_t k = base + i * 256 + t;
+    s += k < count ? x[k] : 0.f;
+  }
+  red[t] = s;
+  __syncthreads();
+  for (int k = 128; k > 0; k >>= 1) {
+    if (t < k) red[t] += red[t + k];
+    __syncthreads();
+  }
+  if (t == 0) part[blockIdx.x] = red[0];
+}
+
 __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int64_t count, float* __restrict__ out) {
   __shared__ float red[256];
   const int t = threadIdx.x;
@@ -1902,7 +1925,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 struct FwdWs {
-  float *part_m, *part_s, *xy, *xc;
+  float *part_m, *part_s, *xy, *xc, *sum_part;
   int *xcount, *xlist;
   size_t bytes;
 };
@@ -1918,6 +1941,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
   w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * MAX_KC);
   w.xcount = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
   w.xlist = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * N);
+  w.sum_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, SUM_CHUNK));
   w.bytes = off;
   return w;
 }
@@ -2117,6 +2141,16 @@ int check_sparse(const int64_t* cand, const float* cval, int kc) {
   return MCE_OK;
 }
 
+// out[0] = the sum of x[0 .. count-1] (k_sum_chunks, then k_sum over its partials).
+int launch_sum(const float* x, int64_t count, float* part, float* out, hipStream_t st) {
+  const int64_t chunks = cdiv(count, SUM_CHUNK);
+  hipLaunchKernelGGL(k_sum_chunks, dim3((unsigned)chunks), dim3(256), 0, st, x, count, part);
+  int rc = launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, part, chunks, out);
+  return launch_status();
+}
+
 // The exact pass over the rows k_fwd_merge listed (count and list on the device): k_exact_tiles, k_exact_rows.
 // part_m / part_s (the merged partials, [>= tiles_v][N]) are reused as its scratch.
 constexpr int REPAIR_BLOCKS = 1024;
@@ -2187,8 +2221,7 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
   if ((rc = fwd_launch(w, H, ldh, W, ldw, bias, y, gate, hit, cand, cval, kc, N, K, V, V_real, w.xy, loss_rows,
                        lse_rows, wgt_rows, dgr_rows, st)))
     return rc;
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, loss_rows, N, loss_sum);
-  return launch_status();
+  return launch_sum(loss_rows, N, w.sum_part, loss_sum, st);
 }
 
 // Logits gradient of every variant: G (and G^T) into the workspace, plus dBias, dGate (mixture) and dCval
@@ -2257,7 +2290,7 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
 struct TrainWs {
   int64_t np, vp, nb, nblk;
   uint16_t *G, *Gt, *Ht, *uperm, *Wt;
-  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *lse_est, *arow, *upart, *part, *dbias_part;
+  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *lse_est, *arow, *upart, *part, *dbias_part, *sum_part;
   int *flag, *flag_list, *counts, *xlist;
   size_t bytes;
 };
@@ -2313,6 +2346,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
       take(sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.vp / BM) * cdiv(K, BN) + TAIL_SLOTS)));
   w.part = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * BM * BN));
   w.dbias_part = reinterpret_cast<float*>(take(sizeof(float) * DBIAS_SPLITS * w.vp));
+  w.sum_part = reinterpret_cast<float*>(take(sizeof(float) * cdiv(np, SUM_CHUNK)));
   w.bytes = off;
   return w;
 }
@@ -2481,8 +2515,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
         return rc;
     }
   }
-  hipLaunchKernelGGL(k_sum, dim3(1), dim3(256), 0, st, loss_rows, N, loss_sum);
-  return launch_status();
+  return launch_sum(loss_rows, N, w.sum_part, loss_sum, st);
 }
 
 // Backward of the one-pass training path: the last block's contractions with go, added to the partial sums of the

@@ -30,6 +30,9 @@ MAX_KC = 8   # sparse candidates per row of linear_ce_sparse (the library's limi
 RECOMPUTE = os.environ.get("MEMARCH_AMD_RECOMPUTE", "0") == "1"   # True: the two-pass (recompute) backward
 BLOCK_ROWS = int(os.environ.get("MEMARCH_AMD_BLOCK_ROWS", "0"))   # rows per block of the one-pass path (0: library)
 GRAD_H, GRAD_W, GRAD_BIAS = 1, 2, 4   # MCE_GRAD_* of include/mce.h
+# Diagnostics: when set to a one-element int32 tensor on the device, every one-pass forward adds to it the number of
+# rows its exact fallback pass rewrote (mce_train_flagged, asynchronous).
+FLAGGED = None
 
 
 def _stream(dev):
@@ -140,6 +143,10 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
             _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
                       _ptr(hf), n, kp, v, v_real, BLOCK_ROWS, want, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr),
                       _ptr(loss_sum), pd, int(dh_bf16), kp, pw, kp, pb, _ptr(tws), ws_bytes, _stream(dev))
+        if FLAGGED is not None and n > 0:
+            cnt = torch.empty(1, dtype=torch.int32, device=dev)
+            _lib.call("mce_train_flagged", _ptr(tws), n, kp, v, BLOCK_ROWS, _ptr(cnt), _stream(dev))
+            FLAGGED.add_(cnt)
         rows = dict(loss_rows=loss_rows, lse=lse, wgt=wgt, dgr=dgr)
         state = dict(ws=tws, want=want, block_rows=BLOCK_ROWS, dh_bf16=dh_bf16, **parts)
         return (hd, wd, bf, y64, cand64, cval32), rows, loss_sum, (n, k, kp, v, v_real), state
