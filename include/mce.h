@@ -214,18 +214,21 @@ MCE_API int64_t mce_train_block_rows(int64_t N, int64_t K, int64_t V, int64_t bl
  * fp32 [1]); with more than one block also the partial sums of the gradients `want` asks for over the rows of all
  * blocks but the last, for go = 1: dH_part rows [0, R) (bf16 when dh_bf16, else fp32; row stride lddh), dW_part
  * fp32 [V, K] (row stride lddw), dBias_part fp32 [V], where R = (blocks - 1) * mce_train_block_rows(...). With one
- * block they are not touched and may be NULL. Replaces `_LinearCEMix.forward` (fused_ops.py:138-157): the chunk
+ * block they are not touched and may be NULL. W is the bf16 weight [V, ldw]: read, or, when the fp32 weight W32
+ * [V, ldw32] is given (16-byte aligned, ldw32 % 4 == 0), written by this call as bf16(W32) (round to nearest even,
+ * the cast of fused_ops.py:142) in the same pass that forms W^T. Replaces `_LinearCEMix.forward`
+ * (fused_ops.py:138-157): the chunk
  * loop of the logits GEMM (fused_ops.py:150), `_ce_mix_kernel` (fused_ops.py:104-134) and the gradient GEMMs
  * `gh[i] = logits @ wd`, `gw += (logits.T @ hc).float()` (fused_ops.py:153-154); gate = hit = NULL replaces
  * `_LinearCE.forward` (fused_ops.py:44-58) and `_ce_grad_kernel` (fused_ops.py:10-36). dBias replaces the bias
  * column of `gw` in the folded layout (full2.py:1842-1851).
  */
-MCE_API int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
-                          const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
-                          int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows,
-                          float* wgt_rows, float* dgr_rows, float* loss_sum, void* dH_part, int dh_bf16,
-                          int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes,
-                          void* stream);
+MCE_API int mce_fwd_train(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, const float* W32,
+                          int64_t ldw32, const float* bias, const int64_t* y, const float* gate, const float* hit,
+                          int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows, int want,
+                          float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
+                          void* dH_part, int dh_bf16, int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part,
+                          void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Forward of the training path with a sparse logit bias (plain cross-entropy): logits[n, cand[n, j]] += cval[n, j]
@@ -234,12 +237,12 @@ MCE_API int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int
  * mce_bwd_train_dcval. Replaces `_LinearCESparse.forward` (fused_ops.py:71-91): the logits GEMM, the scatter of b
  * into the bf16 logits (fused_ops.py:84), `_ce_grad_kernel` and the gradient GEMMs.
  */
-MCE_API int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
-                                 const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N,
-                                 int64_t K, int64_t V, int64_t V_real, int64_t block_rows, int want,
-                                 float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* dH_part,
-                                 int dh_bf16, int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part,
-                                 void* ws, size_t ws_bytes, void* stream);
+MCE_API int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, const float* W32,
+                                 int64_t ldw32, const float* bias, const int64_t* y, const int64_t* cand,
+                                 const float* cval, int kc, int64_t N, int64_t K, int64_t V, int64_t V_real,
+                                 int64_t block_rows, int want, float* loss_rows, float* lse_rows, float* wgt_rows,
+                                 float* loss_sum, void* dH_part, int dh_bf16, int64_t lddh, float* dW_part,
+                                 int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Backward of the training path (`go`: the fp32 upstream gradient of the loss sum on the device): dH = go * G W

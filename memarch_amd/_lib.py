@@ -38,10 +38,10 @@ SIGNATURES = {
                        _S, _P]),
     "mce_train_ws_bytes": (_S, [_I, _I, _I, _I]),
     "mce_train_block_rows": (_I, [_I, _I, _I, _I]),
-    "mce_fwd_train": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _INT, _P, _P, _P, _P, _P, _P, _INT,
-                             _I, _P, _I, _P, _P, _S, _P]),
-    "mce_fwd_train_sparse": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _I, _INT, _P, _P, _P, _P,
-                                    _P, _INT, _I, _P, _I, _P, _P, _S, _P]),
+    "mce_fwd_train": (_INT, [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _INT, _P, _P, _P, _P, _P,
+                             _P, _INT, _I, _P, _I, _P, _P, _S, _P]),
+    "mce_fwd_train_sparse": (_INT, [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _INT, _I, _I, _I, _I, _I, _INT, _P, _P,
+                                    _P, _P, _P, _INT, _I, _P, _I, _P, _P, _S, _P]),
     "mce_bwd_train": (_INT, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _INT, _I, _P, _I, _P, _P, _P, _S, _P]),
     "mce_bwd_train_dcval": (_INT, [_P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _S, _P]),
     "mce_train_flagged": (_INT, [_P, _I, _I, _I, _I, _P, _P]),

@@ -1711,6 +1711,50 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
   }
 }
 
+// The bf16 cast of an fp32 weight and its K-blocked transpose in one pass: w16[r, c] = bf16(src[r, c]) (round to
+// nearest even) for r < R, c < C (row stride ld16), and, when dst is not null, dst as k_transpose_blocked writes it
+// from w16 (zero for R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile.
+__global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict__ src, int64_t ld32, int64_t R,
+                                                        int64_t C, uint16_t* __restrict__ w16, int64_t ld16,
+                                                        uint16_t* __restrict__ dst) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][66];
+  const int t = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rl = (t >> 3) + 32 * h, cl = (t & 7) * 8;
+    const int64_t r = r0 + rl, c = c0 + cl;
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
+    if (r < R && c < C) {
+      const float4 a = *reinterpret_cast<const float4*>(src + r * ld32 + c);
+      const float4 b = *reinterpret_cast<const float4*>(src + r * ld32 + c + 4);
+      pk[0] = pack_bf16x2(a.x, a.y);
+      pk[1] = pack_bf16x2(a.z, a.w);
+      pk[2] = pack_bf16x2(b.x, b.y);
+      pk[3] = pack_bf16x2(b.z, b.w);
+      *reinterpret_cast<u32x4*>(w16 + r * ld16 + c) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+    uint32_t* row = reinterpret_cast<uint32_t*>(&tile[rl][cl]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) row[e] = pk[e];
+  }
+  if (dst == nullptr) return;
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int id = t + 256 * h;
+    const int cl = id >> 3, rq = id & 7;
+    const int64_t c = c0 + cl;
+    if (c < C) {
+      u16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = tile[kperm_inv(rq * 8 + e)][cl];
+      const int64_t r = r0 + rq * 8;
+      *reinterpret_cast<u16x8*>(dst + (r >> 8) * C * BLK + c * BLK + (r & (BLK - 1))) = v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------
 // Plain GEMM C[M, Nc] = s_i (A . B^T + Cin) with fp32 accumulation, stored as fp32 or bf16 (row stride ldc), over
 // nk_total K stages: s_i = go[0] * rscale[i] (1 for a null go or rscale), Cin an fp32 matrix with C's row stride
@@ -2410,9 +2454,10 @@ int train_block_grads(const TrainWs& w, int64_t b, const uint16_t* H, int64_t ld
 // the per-row outputs of fwd_impl; E' and a_n of each block; for every block but the last, its gradient
 // contractions with go = 1 into the partial sums dH_part (its rows), dW_part and dBias_part (the first block
 // writes them, the later ones accumulate). The last block's contractions run in bwd_train_impl. want: MCE_GRAD_*.
-int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
-                   const int64_t* y, const float* gate, const float* hit, const int64_t* cand, const float* cval,
-                   int kc, int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows, int want,
+int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, const float* W32, int64_t ldw32,
+                   const float* bias, const int64_t* y, const float* gate, const float* hit, const int64_t* cand,
+                   const float* cval, int kc, int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows,
+                   int want,
                    float* loss_rows, float* lse_rows, float* wgt_rows, float* dgr_rows, float* loss_sum,
                    void* dH_part, int dh_bf16, int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part,
                    void* ws, size_t ws_bytes, void* stream) {
@@ -2423,6 +2468,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
   if (rc) return rc;
   if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~7)) return MCE_EINVAL;
   if ((want & MCE_GRAD_BIAS) && bias == nullptr) return MCE_EINVAL;
+  if (W32 != nullptr && (ldw32 < K || ldw32 % 4 || (reinterpret_cast<uintptr_t>(W32) & 15))) return MCE_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
     hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, loss_sum, (int64_t)1, 0.f);
@@ -2438,6 +2484,17 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
   const int tv = (int)(w.vp / BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0};
   const bool kf = K % BK == 0;
+  // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V; with
+  // W32 the bf16 W itself comes from the same pass
+  if (W32 != nullptr) {
+    hipLaunchKernelGGL(k_cast_transpose, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W32,
+                       ldw32, V, K, W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr);
+    if ((rc = launch_status())) return rc;
+  } else if (want & MCE_GRAD_H) {
+    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
+                       ldw, V, K, w.Wt, nullptr, nullptr, nullptr);
+    if ((rc = launch_status())) return rc;
+  }
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand,
                      cval, kc, N, K, V_real, w.xy, w.xc);
   if ((rc = launch_status())) return rc;
@@ -2455,12 +2512,6 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ld
   hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, cval,
                      w.xc, kc, V_real, N, w.np, w.lse_est, w.flag, w.counts, (int)(2 * w.np / BLK));
   if ((rc = launch_status())) return rc;
-  if (want & MCE_GRAD_H) {
-    // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V
-    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
-                       ldw, V, K, w.Wt, nullptr, nullptr, nullptr);
-    if ((rc = launch_status())) return rc;
-  }
   for (int64_t b = 0; b < w.nblk; ++b) {
     const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
     const int tnb = (int)(rp / BN);
@@ -2779,22 +2830,25 @@ int64_t mce_train_block_rows(int64_t N, int64_t K, int64_t V, int64_t block_rows
   return train_block_rows(N, V, block_rows);
 }
 
-int mce_fwd_train(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
-                  const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K, int64_t V,
-                  int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows, float* wgt_rows,
-                  float* dgr_rows, float* loss_sum, void* dH_part, int dh_bf16, int64_t lddh, float* dW_part,
-                  int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes, void* stream) {
-  return fwd_train_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, block_rows, want,
+int mce_fwd_train(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, const float* W32, int64_t ldw32,
+                  const float* bias, const int64_t* y, const float* gate, const float* hit, int64_t N, int64_t K,
+                  int64_t V, int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows,
+                  float* wgt_rows, float* dgr_rows, float* loss_sum, void* dH_part, int dh_bf16, int64_t lddh,
+                  float* dW_part, int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes, void* stream) {
+  return fwd_train_impl(H, ldh, W, ldw, W32, ldw32, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real,
+                        block_rows, want,
                         loss_rows, lse_rows, wgt_rows, dgr_rows, loss_sum, dH_part, dh_bf16, lddh, dW_part, lddw,
                         dBias_part, ws, ws_bytes, stream);
 }
 
-int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
-                         const int64_t* y, const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K,
-                         int64_t V, int64_t V_real, int64_t block_rows, int want, float* loss_rows, float* lse_rows,
-                         float* wgt_rows, float* loss_sum, void* dH_part, int dh_bf16, int64_t lddh, float* dW_part,
-                         int64_t lddw, float* dBias_part, void* ws, size_t ws_bytes, void* stream) {
-  return fwd_train_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, cand, cval, kc, N, K, V, V_real, block_rows, want,
+int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, const float* W32, int64_t ldw32,
+                         const float* bias, const int64_t* y, const int64_t* cand, const float* cval, int kc,
+                         int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows, int want,
+                         float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* dH_part,
+                         int dh_bf16, int64_t lddh, float* dW_part, int64_t lddw, float* dBias_part, void* ws,
+                         size_t ws_bytes, void* stream) {
+  return fwd_train_impl(H, ldh, W, ldw, W32, ldw32, bias, y, nullptr, nullptr, cand, cval, kc, N, K, V, V_real,
+                        block_rows, want,
                         loss_rows, lse_rows, wgt_rows, nullptr, loss_sum, dH_part, dh_bf16, lddh, dW_part, lddw,
                         dBias_part, ws, ws_bytes, stream);
 }

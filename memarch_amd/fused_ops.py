@@ -104,7 +104,15 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
     _check_cuda(h, w, bias, y, gate, hit, cand, cval)
     kp = (k + 7) // 8 * 8
     dev = h.device
-    hd, wd = _bf16_operand(h, kp), _bf16_operand(w, kp)
+    hd = _bf16_operand(h, kp)
+    w32 = None
+    if train and w.dtype == torch.float32 and k == kp and w.stride(1) == 1 and w.stride(0) % 4 == 0 \
+            and w.data_ptr() % 16 == 0:
+        # the one-pass forward casts the fp32 weight itself, in the pass that also forms its transpose
+        w32 = w.detach()
+        wd = torch.empty(v, kp, dtype=_BF16, device=dev)
+    else:
+        wd = _bf16_operand(w, kp)
     y64 = _rows(y, torch.int64)
     gf = None if gate is None else _rows(gate, torch.float32)   # None: g = 0 (plain cross-entropy)
     hf = None if hit is None else _rows(hit, torch.float32)
@@ -134,13 +142,15 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
                 parts["dbias"] = torch.empty(v, **f32)
         pd, pw, pb = (_ptr(parts[x]) for x in ("dh", "dw", "dbias"))
         if kc:
-            _lib.call("mce_fwd_train_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
+            _lib.call("mce_fwd_train_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(w32),
+                      0 if w32 is None else w32.stride(0), _ptr(bf), _ptr(y64),
                       _ptr(cand64), _ptr(cval32), kc, n, kp, v, v_real, BLOCK_ROWS, want, _ptr(loss_rows), _ptr(lse),
                       _ptr(wgt), _ptr(loss_sum), pd, int(dh_bf16), kp, pw, kp, pb, _ptr(tws), ws_bytes,
                       _stream(dev))
             dgr.zero_()
         else:
-            _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
+            _lib.call("mce_fwd_train", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(w32),
+                      0 if w32 is None else w32.stride(0), _ptr(bf), _ptr(y64), _ptr(gf),
                       _ptr(hf), n, kp, v, v_real, BLOCK_ROWS, want, _ptr(loss_rows), _ptr(lse), _ptr(wgt), _ptr(dgr),
                       _ptr(loss_sum), pd, int(dh_bf16), kp, pw, kp, pb, _ptr(tws), ws_bytes, _stream(dev))
         if FLAGGED is not None and n > 0:

@@ -118,7 +118,7 @@ def capi_train(case, go=1.0, s_max=None, dev="cuda", block_rows=0):
     if s_max is not None:
         lib.mce_train_set_threshold(float(s_max))
     try:
-        _lib.call("mce_fwd_train", p(h), k, p(w), k, p(b), p(y), p(gate), p(hit), n, k, v, case["v_real"],
+        _lib.call("mce_fwd_train", p(h), k, p(w), k, None, 0, p(b), p(y), p(gate), p(hit), n, k, v, case["v_real"],
                   block_rows, want, p(loss_rows), p(lse), p(wgt), p(dgr), p(loss_sum), p(dh_part), 1, k, p(dw_part),
                   k, p(db_part), p(ws), nb, st)
     finally:

@@ -2,7 +2,8 @@
 e_n (the lower bound of the lse that k_fwd_train shifts by), so that E = exp(x - e_n) is +inf in fp32 for those
 entries. The design claims (mce.hip, k_fwd_train and store_g_block) that such a row is flagged, that its inf values
 (and the NaNs inf * 0 makes in the selector-MFMA transpose) stay inside its own row of G and G^T, and that the exact
-fallback pass (k_repair) rewrites that whole row; every kernel exits normally.
+fallback pass (k_exact_train, an MFMA pass over the gathered flagged rows) rewrites that whole row; every kernel
+exits normally.
 
 Because e_n >= x_y (the target logit is part of the bound), a row with such a gap has py < e^-88, below the 1e-30
 clamp of the mixture: with g = 0 (or hit = 0) its gradient is exactly zero, with hit = 1 and g > 0 it is tiny but
@@ -90,7 +91,7 @@ def _capi(case, go, block_rows):
     parts = [torch.empty(r, k, dtype=torch.bfloat16, device=dev), torch.empty(v, k, **f32),
              torch.empty(v, **f32)] if r else [None, None, None]
     st = torch.cuda.current_stream().cuda_stream
-    _lib.call("mce_fwd_train", p(h), k, p(w), k, p(b), p(y), p(gate), p(hit), n, k, v, v, block_rows, 7,
+    _lib.call("mce_fwd_train", p(h), k, p(w), k, None, 0, p(b), p(y), p(gate), p(hit), n, k, v, v, block_rows, 7,
               p(loss_rows), p(lse), p(wgt), p(dgr if gate is not None else None), p(loss_sum), p(parts[0]), 1, k,
               p(parts[1]), k, p(parts[2]), p(ws), nb, st)
     flagged = torch.zeros(1, dtype=torch.int32, device=dev)

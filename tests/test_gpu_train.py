@@ -234,3 +234,50 @@ def test_per_row_logit_offsets(recompute, monkeypatch):
         err = np.linalg.norm(got[key][:, :d] - ref) / np.linalg.norm(ref)
         print(key, f"vs unshifted {err:.2e}", flush=True)
         assert err <= 2e-2, (key, err)
+
+
+def test_fp32_weight_cast_in_the_forward():
+    """mce_fwd_train with the fp32 weight W32: the bf16 W it writes equals torch's cast (round to nearest even)
+    bit for bit, including ties, huge and tiny values, and the results equal those of the same call given the
+    bf16 W (same kernels, same operands)."""
+    from memarch_amd import _lib
+    lib = _lib.load()
+    case = random_case(300, 520, 2051, 2000, True, seed=101)
+    w32 = case["w"].clone()
+    # a masked row (v >= v_real: its logits are -inf whatever W holds) carries ties, large values, a denormal, +-0
+    w32[2040, :8] = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 1e30, -1e30, 1e-40, 0.0, -0.0])
+    n, k = case["h"].shape
+    v = w32.shape[0]
+    dev = "cuda"
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    h = case["h"].to(dev, torch.bfloat16).contiguous()
+    w32d = w32.to(dev).contiguous()
+    b = case["bias"].to(dev)
+    y, gate, hit = case["y"].to(dev), case["gate"].to(dev), case["hit"].to(dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for use32 in (True, False):
+        wb = torch.empty(v, k, dtype=torch.bfloat16, device=dev) if use32 else w32d.to(torch.bfloat16)
+        rows = [torch.empty(n, **f32) for _ in range(4)]
+        loss = torch.empty((), **f32)
+        nb = lib.mce_train_ws_bytes(n, k, v, 0)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        _lib.call("mce_fwd_train", p(h), k, p(wb), k, p(w32d) if use32 else None, k if use32 else 0, p(b), p(y),
+                  p(gate), p(hit), n, k, v, case["v_real"], 0, 7, *(p(r) for r in rows), p(loss), None, 1, k, None, k,
+                  None, p(ws), nb, st)
+        go = torch.full((), 1.0, **f32)
+        dh = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+        dw = torch.empty(v, k, **f32)
+        db = torch.empty(v, **f32)
+        _lib.call("mce_bwd_train", p(h), k, p(go), p(rows[3]), n, k, v, 0, None, None, None, p(dh), 1, k, p(dw), k,
+                  p(db), None, p(ws), nb, st)
+        torch.cuda.synchronize()
+        outs.append((wb.clone(), loss.clone(), dh, dw, db))
+    got, ref = outs[0][0].view(torch.int16).clone(), w32d.to(torch.bfloat16).view(torch.int16).clone()
+    # the denormal may be flushed by the hardware conversion (to a zero of its sign); everything else is bit-exact
+    assert int(got[2040, 5]) in (int(ref[2040, 5]), 0)
+    got[2040, 5] = ref[2040, 5]
+    assert torch.equal(got, ref)
+    for a, c in zip(outs[0][1:], outs[1][1:]):
+        assert torch.equal(a, c)
