@@ -48,8 +48,8 @@ STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_
                  "mce_bwd_dweight": "dweight", "mce_fwd_sparse": "fwd", "mce_bwd_logits_grad_sparse": "logits_grad",
                  "mce_lse_fwd": "fwd", "mce_bwd_lse_grad": "logits_grad"}
 # kernel classes of mce_prof_stop (include/mce.h) -> kernel name; each class runs one N x V x d contraction per step
-PROF_KERNELS = ("k_fwd_train<true>", "k_fwd_tiles<true>", "k_bwd_grad<true>", "k_gemm<true, true, true, 0>",
-                "k_gemm<false, true, true, {nr}>")
+PROF_KERNELS = ("k_fwd_train<true>", "k_fwd_tiles<true>", "k_bwd_grad<true>", "k_gemm<true, true, 1, 0>",
+                "k_gemm<false, true, 2, {nr}>")
 # the siblings of the north-star op (--op): the same contractions on the same configuration inputs
 SIBLING_OPS = ("linear_ce", "linear_ce_sparse", "chunk_ce")
 

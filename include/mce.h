@@ -108,15 +108,16 @@ MCE_API int mce_fwd_sparse(const uint16_t* H, int64_t ldh, const uint16_t* W, in
                    int64_t V_real, float* loss_rows, float* lse_rows, float* wgt_rows, float* loss_sum, void* ws,
                    size_t ws_bytes, void* stream);
 
-/* Workspace bytes needed by the backward entry points for this shape: the bf16 gradient of the logits twice, in
- * tile-blocked layouts (G with the vocabulary as its reduction index, for dH, and G^T with the rows, for dW; each
- * N x V rounded up to 256 x 256), the K-blocked transposed copies W^T and H^T, and the dBias partial sums.
+/* Workspace bytes needed by the backward entry points for this shape: the bf16 gradient of the logits G once, in a
+ * tile-blocked layout (N x V rounded up to 256 x 256; dH reads it with the vocabulary as its reduction index, dW
+ * reads it transposed with the rows as its reduction index), the K-blocked transposed copies W^T and H^T, and the
+ * dBias partial sums.
  * Replaces the bf16 logits chunk that fused_ops.py:150,134 overwrites with the gradient. */
 MCE_API size_t mce_bwd_ws_bytes(int64_t N, int64_t K, int64_t V);
 
 /*
- * Backward step 1: recompute the logits tile by tile and write G = go*wgt*(softmax - onehot) (bf16, both
- * layouts) into the workspace; reduce dBias (if dBias != NULL, requires bias != NULL) and write dGate (if
+ * Backward step 1: recompute the logits tile by tile and write G = go*wgt*(softmax - onehot) (bf16) into the
+ * workspace; reduce dBias (if dBias != NULL, requires bias != NULL) and write dGate (if
  * dGate != NULL).
  * `go` is a device pointer to the fp32 upstream gradient of the loss sum (a 0-dim tensor).
  * Replaces the gradient half of `_ce_mix_kernel` (fused_ops.py:127-134) and the `go` scaling of
@@ -151,7 +152,7 @@ MCE_API int mce_lse_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64
                 void* ws, size_t ws_bytes, void* stream);
 
 /*
- * Backward step 1 of `chunk_ce`: G = g_lse softmax + g_ly onehot (bf16, both layouts) into the workspace from the
+ * Backward step 1 of `chunk_ce`: G = g_lse softmax + g_ly onehot (bf16) into the workspace from the
  * forward's lse_rows and the upstream gradients g_lse, g_ly (fp32 [N], device); dBias (if dBias != NULL) is the
  * column sum of G. Replaces the per-chunk G of `_ChunkCE.backward` (full2.py:814-815) and `db` (full2.py:828-829);
  * steps 2 and 3 (mce_bwd_dhidden, mce_bwd_dweight) replace its dh and dW products (full2.py:816-827).
@@ -195,8 +196,8 @@ MCE_API int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
  * (only the earlier blocks' dH rows are, once).
  *
  * Blocks: `block_rows` rows each (rounded up to a multiple of 256 and evened out over the blocks), or, with
- * block_rows = 0, as many as keep the block's E' (two bf16 copies, 4 * rows * V bytes) within 2 GiB: 8192 rows at
- * V = 50304, 4096 at V = 131072. mce_train_ws_bytes bounds the workspace by one block, whatever N is. The same
+ * block_rows = 0, as many as keep the block's E' (bf16, 2 * rows * V bytes) within 2 GiB: up to 21248 rows at
+ * V = 50304 (two blocks of 16384 for 32768 rows), 8192 at V = 131072. mce_train_ws_bytes bounds the workspace by one block, whatever N is. The same
  * block_rows, `want` and buffers must be passed to the forward and the backward of one step, and the workspace
  * kept unchanged between them (it holds the last block's E' and the per-row state).
  */

@@ -11,19 +11,24 @@
 //
 // Every operand is a logical [M, K] matrix with K contiguous: element (m, k) at p[m*ld + k], or, in the
 // K-blocked layout of the transposed copies, at p[(k/256)*blk + m*256 + k%256] (256-wide K blocks, each a
-// contiguous [M][256] panel), or, for G and G^T, in tile-blocked 128-byte pieces (Operand::cm). The LDS image
-// of one stage is [256 m][64 k] with 128-byte rows and the 16-byte chunk index XOR-swizzled by the row (or in
-// piece order for a piece-layout operand), so fragment reads (ds_read_b128) are bank-conflict free. Elements
-// outside an operand's extent read as zero (out-of-range buffer offsets), so partial tiles need no special path.
+// contiguous [M][256] panel), or, for G, in tile-blocked 128-byte pieces (Operand::cm = 1), which the dW
+// contraction reads transposed (Operand::cm = 2). The LDS image of one stage is [256 m][64 k] with 128-byte rows and
+// the 16-byte chunk index XOR-swizzled by the row (or in piece order for a piece-layout operand), so fragment reads
+// (ds_read_b128, or two ds_read_b64_tr_b16 for the transposed pieces) are bank-conflict free. Elements outside an
+// operand's extent read as zero (out-of-range buffer offsets), so partial tiles need no special path.
 //
 //   forward     S^T = W H^T           -> per-half-tile row max / sum-exp; target logit by a dot product;
 //                                         merge -> lse, loss, wgt, dgr
-//   logits-grad S^T = W H^T recomputed -> G = go*wgt*(softmax - onehot) (bf16) stored from registers as G
-//                                         (for dH) and, transposed by MFMAs, as G^T (for dW); dBias partials
+//   logits-grad S^T = W H^T recomputed -> G = go*wgt*(softmax - onehot) (bf16) stored from registers; dBias
+//                                         partials from MFMA register transposes of the bf16 values
 //   dhidden     dH  = G   . Wt  with Wt = W^T (K-blocked copy made by k_transpose_blocked)
-//   dweight     dW  = G^T . Ht  with Ht = H^T (K-blocked copy)
-// (the reduction index of G, G^T, Wt and Ht is stored in the kperm order)
-// The N x V logits never reach memory; G is the only N x V intermediate.
+//   dweight     dW  = G^T . Ht  with Ht = H^T (K-blocked copy), G^T read from G through transposing LDS reads
+//   one-pass    per row block: the forward tiles store E' (the gradient over go*a_n) into G, then dhidden and
+//               dweight of the block (k_fwd_train ... train_block_grads)
+// (G's vocabulary positions and Wt's reduction index are stored in the kperm order; G's rows and Ht's reduction
+// index in natural order)
+// The N x V logits themselves never reach memory; G (bf16, of one row block on the one-pass path) is the only
+// N x V intermediate.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
@@ -72,11 +77,12 @@ static_assert(LDS_BYTES <= 160 * 1024, "operand ring exceeds the 160 KiB of LDS 
 
 struct Operand {
   const uint16_t* p;  // bf16 bits
-  int64_t ld;         // row stride in elements (256 in the K-blocked layout; unused when cm)
+  int64_t ld;         // row stride in elements (256 in the K-blocked layout; unused when cm = 1; the element
+                      // distance between consecutive 256-row M tiles when cm = 2)
   int64_t mext;       // valid extent along M
   int64_t kext;       // valid extent along K
   int64_t blk;        // 0, or the element distance between consecutive 256-wide K blocks
-  int cm;             // 1: tile-blocked chunk-major (below)
+  int cm;             // 1: tile-blocked piece layout (below); 2: the transpose of one, read as [M][K] (below)
 };
 // Tile-blocked piece layout (Operand::cm) of an [M][K] operand with M and K padded to multiples of 256: every
 // 256 x 256 tile is one contiguous 128 KiB block of 128-byte pieces [8 m][8 k], [32 row groups][32 k chunks], and
@@ -85,11 +91,17 @@ struct Operand {
 //   blk = 256 * Mpad.
 // The 8 rows x 64 k of one load instruction of a stage are then 1 KiB contiguous, and 32 consecutive m of one
 // 8-wide k chunk are four whole 128-byte pieces.
+// Transposed pieces (Operand::cm = 2): the A operand A[m][k] = S[k][m] of a piece-layout buffer S (rows k, columns m:
+// G read with the vocabulary as M and the rows as the reduction index). A stage (64 k x 256 m) is then 32 KiB of
+// whole pieces [8 k][8 m], contiguous in S, and the MFMA fragments (8 consecutive k of one m per lane) come from
+// transposing LDS reads (ds_read_b64_tr_b16).
 constexpr int64_t CM_TILE = 256 * 256;
-// The reduction index of G, Gt and of the transposed copies Wt, Ht is stored permuted inside each 32-wide group:
-// index 8q + 4h + e (q < 4, h < 2, e < 4) at position 16h + 4q + e. A lane of the logits-grad epilogue holds, for
-// one row, the indices with one h, which are then 16 consecutive positions (two 16-byte stores). The dH and dW
-// contractions sum over positions, so the permutation cancels as long as both operands use it.
+// The vocabulary index of G (the reduction index of the dH contraction) and of the transposed copy Wt is stored
+// permuted inside each 32-wide group: index 8q + 4h + e (q < 4, h < 2, e < 4) at position 16h + 4q + e. A lane of
+// the logits-grad epilogue holds, for one row, the indices with one h, which are then 16 consecutive positions (two
+// 16-byte stores). The dH contraction sums over positions, so the permutation cancels as both operands use it; the
+// dW contraction has the positions as its output rows and maps them back (out_row). G's rows, the dW reduction
+// index, stay in natural order, as does the H^T copy paired with them.
 __host__ __device__ constexpr int kperm(int k) {
   return (k & ~31) | (((k >> 2) & 1) << 4) | (((k >> 3) & 3) << 2) | (k & 3);
 }
@@ -166,11 +178,29 @@ struct Stream {
 // image: the 8 lanes of a row read one 128-byte segment.
 // Tile-blocked pieces (Operand::cm, m0 a multiple of 256): lane l reads row m = 8i + l%8, chunk
 // c = (l/8) ^ (i & 1), at (m/8)*4096 + c*128 + (m%8)*16, so an instruction reads 1 KiB contiguously (whole
-// 128-byte pieces, swapped in pairs for odd i) into the piece-order image (make_frag_addr<true>); a k step inside
+// 128-byte pieces, swapped in pairs for odd i) into the piece-order image (make_frag_addr<1>); a k step inside
 // a 256-wide K block is 16 bytes.
+// Transposed pieces (Operand::cm = 2, m0 a multiple of 256): the stage is the 32 KiB of pieces P = (k/8)*32 + m/8
+// (stage-local k) at P*128 in S's block; lane l of instruction i lands at LDS piece 8i + l/8, row l%8, and reads
+// the piece's row (l%8) ^ 4 sw(P) (sw(P) = (P ^ P/2) & 1), so the image holds every piece in place with its two
+// 4-row halves swapped when sw = 1 (the bank spread of make_frag_addr<2>); a k step is 512 bytes.
 __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
   Stream st;
   st.kext = op.kext;
+  if (op.cm == 2) {
+    st.blk = op.blk;
+    st.kmul = 512;
+    st.base = reinterpret_cast<uint64_t>(op.p + (m0 / BM) * op.ld);
+#pragma unroll
+    for (int j = 0; j < I::LPW; ++j) {
+      const int piece = (wave * I::LPW + j) * 8 + (lane >> 3);
+      const int sw = (piece ^ (piece >> 1)) & 1;
+      st.voff[j] = piece * 128 + ((lane & 7) ^ (4 * sw)) * 16;
+      st.kloc[j] = 0;
+      st.vfull[j] = st.voff[j];
+    }
+    return st;
+  }
   if (op.cm) {
     st.blk = op.blk;
     st.kmul = 16;
@@ -213,36 +243,71 @@ __device__ __forceinline__ StageSrc stage_src(const Stream& st, int stage, int s
 // buffer through the 16-bit immediate offset of ds_read_b128.
 constexpr int AOFF = 0, BOFF = 2 * I::OPB;
 
+// The same load as an inline-asm instruction (M0 = the wave's LDS address, then buffer_load_dwordx4 ... lds), which
+// the compiler does not see as a write to LDS. The kernels with transposed A pieces (AM = 2) issue all their LDS
+// loads this way: the compiler places s_waitcnt vmcnt(0) before every ds_read_b64_tr_b16 while it knows of a pending
+// LDS load, which would drain the load pipeline at every fragment read. The mainloop orders its LDS loads and
+// reads itself (s_waitcnt vmcnt + barrier before a stage's first read), and no compiler-generated code in those
+// kernels uses M0.
+__device__ __forceinline__ void dma16(const i32x4& rsrc, const char* lds, int dst, int voff) {
+  // the base's LDS address (loop-invariant: the cast of the kernel's LDS array) plus the wave-uniform offset
+  const uint32_t a = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(LDS_AS const char*)lds + (uint32_t)dst);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(a), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
 // Load j of this wave for one stage into the LDS byte offset `dst` (relative to the kernel's LDS base);
-// KF: the stage lies inside K (or past the range), so the precomputed offset needs no check.
-template <bool KF>
+// KF: the stage lies inside K (or past the range), so the precomputed offset needs no check. ASM: through dma16.
+template <bool KF, bool ASM = false>
 __device__ __forceinline__ void issue_one(const Stream& st, const StageSrc& src, int j, char* lds, int dst) {
   int vo;
   if constexpr (KF) vo = st.vfull[j];
   else vo = st.kloc[j] < src.klim ? st.voff[j] : OOB;
-  buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(lds + dst), 16, vo, 0, 0, 0);
+  if constexpr (ASM)
+    dma16(src.rsrc, lds, dst, vo);
+  else
+    buffer_load_lds(src.rsrc, (uint32_t LDS_AS*)(lds + dst), 16, vo, 0, 0, 0);
 }
 
 // This wave's loads of one operand of stage `stage` into the image at LDS byte offset `img`.
+template <bool ASM = false>
 __device__ __forceinline__ void issue_stage(const Stream& st, int stage, int send, char* lds, int img, int wave) {
   const StageSrc src = stage_src(st, stage, send);
 #pragma unroll
-  for (int j = 0; j < I::LPW; ++j) issue_one<false>(st, src, j, lds, img + (wave * I::LPW + j) * 1024);
+  for (int j = 0; j < I::LPW; ++j) issue_one<false, ASM>(st, src, j, lds, img + (wave * I::LPW + j) * 1024);
 }
 
 // Per-lane LDS byte offsets of the MFMA operand fragments (v_mfma_f32_32x32x16_bf16: lane l holds element
 // (row0 + l%32, kk*16 + 8*(l/32) + 0..7) of a 32-row block), computed once per tile. Fragment i of slice kk is
 // at a[kk][i&1] + (i>>1)*64 rows: rows 64 apart share the XOR swizzle, so the rest is a compile-time offset,
 // as is the ring buffer (b*OPB). The mainloop then reads with immediates only.
-// APC: the A image is in piece order (an Operand::cm operand): the 16-byte chunk c of row r at
+// AM = 1: the A image is in piece order (an Operand::cm = 1 operand): the 16-byte chunk c of row r at
 // (r/8)*1024 + (c ^ ((r/8) & 1))*128 + (r%8)*16. A ds_read_b128 serves 16 lanes (256 bytes) per cycle: those are
 // 16 consecutive rows at one chunk, i.e. two row groups, whose 128-byte runs the parity swizzle puts 1024 +- 128
 // bytes apart, in different bank halves, so the reads are conflict free; rows 64 apart are again 8 KiB apart.
+// AM (A image mode): 0 swizzled rows, 1 piece order (above), 2 transposed pieces (Operand::cm = 2).
+// AM = 2: a fragment is two ds_read_b64_tr_b16. Within each 16-lane group that instruction gives lane 4q + e element
+// e of the 8 bytes read by lanes q, 4 + q, 8 + q, 12 + q of the group (in that order); so if lane 4j + q reads the 4
+// consecutive m = mb + 4q .. +3 of row k = kb + j, lane i of the group receives m = mb + i, k = kb .. kb+3. Lane l
+// (group g = l/16, j = (l%16)/4, q = l%4) of fragment i, slice kk, half t reads row 4t + j of piece
+// (2kk + g/2)*32 + wm*16 + 4i + 2(g%2) + q/2 at byte 8(q%2) of the row: the fragment is rows m = wm*128 + 32i + l%32,
+// k = 16kk + 8(l/32) + 4t + j, exactly the MFMA layout. With the image's half swap (make_stream) the row sits at
+// 4(t ^ sw) + j, sw = (q/2) ^ (g%2): the two pieces a 16-lane group reads fall in different bank halves of a
+// 128-byte row, and the 4 pieces of lanes 0-31 cover all four 64-byte quarters of a 256-byte row, conflict free for
+// both LDS widths. ad.a[0][t] holds half t of fragment 0, slice 0; the rest are immediates (kk*8192 + i*512).
 struct FragAddr {
   uint32_t a[4][2];  // [kk][i & 1], A image of buffer 0
   uint32_t b[4][2];  // [kk][j & 1], B image of buffer 0
 };
-template <bool APC>
+__device__ __forceinline__ uint32_t tra_addr(int wm, int lane, int t) {
+  const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+  const int sw = (q >> 1) ^ (g & 1);
+  const int piece = (g >> 1) * 32 + wm * 16 + 2 * (g & 1) + (q >> 1);
+  return AOFF + piece * 128 + (4 * (t ^ sw) + j) * 16 + (q & 1) * 8;
+}
+template <int AM>
 __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
   FragAddr ad;
 #pragma unroll
@@ -252,7 +317,9 @@ __device__ __forceinline__ FragAddr make_frag_addr(int wm, int wn, int lane) {
       const int c = kk * 2 + (lane >> 5);
       const int ra = wm * 128 + p * 32 + (lane & 31);
       const int rb = wn * 128 + p * 32 + (lane & 31);
-      if constexpr (APC)
+      if constexpr (AM == 2)
+        ad.a[kk][p] = tra_addr(wm, lane, p);
+      else if constexpr (AM == 1)
         ad.a[kk][p] = AOFF + (ra >> 3) * 1024 + ((c ^ ((ra >> 3) & 1)) << 7) + (ra & 7) * 16;
       else
         ad.a[kk][p] = AOFF + ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
@@ -264,10 +331,25 @@ template <int OFF>
 __device__ __forceinline__ bf16x8 frag_at(const char* lds, uint32_t addr) {
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(lds + addr + OFF));
 }
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+template <int OFF>
+__device__ __forceinline__ bf16x4 tr_at(const char* lds, uint32_t addr) {
+  return __builtin_bit_cast(
+      bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 LDS_AS*)(const_cast<char*>(lds) + addr + OFF)));
+}
+// the fragment of the two transposing reads at a0 (k 0..3 of the lane's 8) and a1 (k 4..7)
+template <int OFF>
+__device__ __forceinline__ bf16x8 frag_tr(const char* lds, uint32_t a0, uint32_t a1) {
+  const bf16x4 lo = tr_at<OFF>(lds, a0), hi = tr_at<OFF>(lds, a1);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
 // A fragment I_ / B fragment J_ of slice KK in ring buffer BUF
-template <int BUF, int KK, int I_>
+template <int BUF, int KK, int I_, int AM = 0>
 __device__ __forceinline__ bf16x8 frag_a(const char* lds, const FragAddr& ad) {
-  return frag_at<BUF * I::OPB + (I_ >> 1) * 64 * I::ROWB>(lds, ad.a[KK][I_ & 1]);
+  if constexpr (AM == 2)
+    return frag_tr<BUF * I::OPB + KK * 8192 + I_ * 512>(lds, ad.a[0][0], ad.a[0][1]);
+  else
+    return frag_at<BUF * I::OPB + (I_ >> 1) * 64 * I::ROWB>(lds, ad.a[KK][I_ & 1]);
 }
 template <int BUF, int KK, int J_>
 __device__ __forceinline__ bf16x8 frag_b(const char* lds, const FragAddr& ad) {
@@ -275,22 +357,22 @@ __device__ __forceinline__ bf16x8 frag_b(const char* lds, const FragAddr& ad) {
 }
 // Read r (0..7) of a slice, in the order the next slice's MFMAs consume them: a0 b0 b1 b2 b3 a1 a2 a3 (the
 // MFMAs run (0,0) (0,1) (0,2) (0,3) (1,0) ...), so every read has most of a slice to complete.
-template <int BUF, int KK, int R>
+template <int BUF, int KK, int R, int AM = 0>
 __device__ __forceinline__ void frag_read(const char* lds, const FragAddr& ad, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
-  if constexpr (R == 0) a[0] = frag_a<BUF, KK, 0>(lds, ad);
+  if constexpr (R == 0) a[0] = frag_a<BUF, KK, 0, AM>(lds, ad);
   else if constexpr (R < 5) b[R - 1] = frag_b<BUF, KK, R - 1>(lds, ad);
-  else a[R - 4] = frag_a<BUF, KK, R - 4>(lds, ad);
+  else a[R - 4] = frag_a<BUF, KK, R - 4, AM>(lds, ad);
 }
-template <int BUF, int KK>
+template <int BUF, int KK, int AM = 0>
 __device__ __forceinline__ void read_frags(const char* lds, const FragAddr& ad, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
-  frag_read<BUF, KK, 0>(lds, ad, a, b);
-  frag_read<BUF, KK, 1>(lds, ad, a, b);
-  frag_read<BUF, KK, 2>(lds, ad, a, b);
-  frag_read<BUF, KK, 3>(lds, ad, a, b);
-  frag_read<BUF, KK, 4>(lds, ad, a, b);
-  frag_read<BUF, KK, 5>(lds, ad, a, b);
-  frag_read<BUF, KK, 6>(lds, ad, a, b);
-  frag_read<BUF, KK, 7>(lds, ad, a, b);
+  frag_read<BUF, KK, 0, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 1, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 2, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 3, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 4, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 5, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 6, AM>(lds, ad, a, b);
+  frag_read<BUF, KK, 7, AM>(lds, ad, a, b);
 }
 
 __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4], const bf16x8 (&b)[4]) {
@@ -300,12 +382,26 @@ __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4],
     for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
 
-// Interleave the current scheduling region: one LDS read between two MFMAs.
+// Interleave the current scheduling region: one LDS read between two MFMAs (AM = 2: the 12 reads of a slice with
+// transposing A reads, three per four MFMAs).
+template <int AM = 0>
 __device__ __forceinline__ void sched_slice() {
+  if constexpr (AM == 2) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(SG_MFMA, 2, 0);
+    }
   }
 }
 
@@ -314,12 +410,14 @@ __device__ __forceinline__ void sched_slice() {
 // (16 K positions) of each group: NR extra A fragment reads and one read of the slice's u values (the lane's 8 of
 // them), then 4 NR v_dot2c_f32_bf16; every wave and tile runs the same instructions, so the work adds a small,
 // even cost to every stage. u arrives through LDS: 64 bf16 values per stage (the slot of ring buffer b at
-// APOFF + 1024 b, written by one load instruction of wave 0).
+// APOFF + 1024 b, written by one load instruction of wave 0). With transposed pieces (AM = 2) each fragment is two
+// transposing reads, at faddr[j] and faddr2[j].
 constexpr int APOFF = LDS_BYTES;
 template <int NR>
 struct DotState {
   i32x4 rsrc;         // u, bf16
   uint32_t faddr[NR]; // LDS byte offsets of this lane's fragments (group rg_j, slice = wave), A image of buffer 0
+  uint32_t faddr2[NR];  // AM = 2: the second half of each fragment
   uint32_t uaddr;     // LDS byte offset of this lane's 8 u values (slice = wave) in the slot of buffer 0
   bf16x8 x[NR], u;    // the fragments and u values read for this stage
   float acc[NR];      // row rg_j*32 + lane%32, K positions of lane half lane/32 of slice `wave` of every stage
@@ -338,64 +436,73 @@ __device__ __forceinline__ float dot8(const bf16x8& a, const bf16x8& u, float c)
 // it to the end of the loop body).
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 // Wave 0's load of u[stage*64 .. +63] into the slot of ring buffer `slot` (lanes 8..63 write zeros).
+template <bool ASM = false>
 __device__ __forceinline__ void issue_ap(const i32x4& rsrc, int stage, int send, char* lds, int slot) {
   const int lane = threadIdx.x & 63;
   const int off = (stage < send && lane < 8) ? stage * 128 + lane * 16 : OOB;
-  buffer_load_lds(rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
+  if constexpr (ASM)
+    dma16(rsrc, lds, APOFF + slot * 1024, off);
+  else
+    buffer_load_lds(rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
 }
 // Slice 1 with the NR + 1 extra reads first; slice 2 with the 4 NR dot products, NR between each of its first MFMA
 // pairs.
-template <int NR>
+template <int NR, int AM = 0>
 __device__ __forceinline__ void sched_slice_rd2() {
-  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, NR + 1, 0);
-  sched_slice();
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, (AM == 2 ? 2 * NR : NR) + 1, 0);
+  sched_slice<AM>();
 }
-template <int NR, int I_>
+template <int NR, int I_, int AM = 0>
 __device__ __forceinline__ void sched_dot_pair() {
-  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
+  __builtin_amdgcn_sched_group_barrier(SG_DS_READ, (AM == 2 && I_ < 4) ? 2 : 1, 0);
   __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
   if constexpr (I_ < 4) __builtin_amdgcn_sched_group_barrier(SG_VALU, NR, 0);
   __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
 }
-template <int NR>
+template <int NR, int AM = 0>
 __device__ __forceinline__ void sched_slice_dot() {
-  sched_dot_pair<NR, 0>();
-  sched_dot_pair<NR, 1>();
-  sched_dot_pair<NR, 2>();
-  sched_dot_pair<NR, 3>();
-  sched_dot_pair<NR, 4>();
-  sched_dot_pair<NR, 5>();
-  sched_dot_pair<NR, 6>();
-  sched_dot_pair<NR, 7>();
+  sched_dot_pair<NR, 0, AM>();
+  sched_dot_pair<NR, 1, AM>();
+  sched_dot_pair<NR, 2, AM>();
+  sched_dot_pair<NR, 3, AM>();
+  sched_dot_pair<NR, 4, AM>();
+  sched_dot_pair<NR, 5, AM>();
+  sched_dot_pair<NR, 6, AM>();
+  sched_dot_pair<NR, 7, AM>();
 }
 
 // A slice without loads: reads of slice RK of buffer RBUF into (da, db), the 16 MFMAs of (ua, ub), interleaved by
 // the compiler one read per two MFMAs.
-template <int RBUF, int RK, int DB = 0>
+template <int RBUF, int RK, int DB = 0, int AM = 0>
 __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
                                             DotState<DB ? DB : 1>* dp = nullptr) {
   if constexpr (DB > 0 && RK == 2) {
     // slice 1 of the stage (reads slice 2): this wave's extra fragments and u values of the stage's buffer
 #pragma unroll
-    for (int j = 0; j < DB; ++j) dp->x[j] = frag_at<AOFF + RBUF * I::OPB>(lds, dp->faddr[j]);
+    for (int j = 0; j < DB; ++j) {
+      if constexpr (AM == 2)
+        dp->x[j] = frag_tr<RBUF * I::OPB>(lds, dp->faddr[j], dp->faddr2[j]);
+      else
+        dp->x[j] = frag_at<AOFF + RBUF * I::OPB>(lds, dp->faddr[j]);
+    }
     dp->u = frag_at<APOFF + RBUF * 1024>(lds, dp->uaddr);
-    read_frags<RBUF, RK>(lds, ad, da, db);
+    read_frags<RBUF, RK, AM>(lds, ad, da, db);
     mma16(acc, ua, ub);
-    sched_slice_rd2<DB>();
+    sched_slice_rd2<DB, AM>();
   } else if constexpr (DB > 0 && RK == 3) {
     // slice 2 of the stage (reads slice 3): the dot products of the fragments read in slice 1
-    read_frags<RBUF, RK>(lds, ad, da, db);
+    read_frags<RBUF, RK, AM>(lds, ad, da, db);
     mma16(acc, ua, ub);
 #pragma unroll
     for (int j = 0; j < DB; ++j) dp->acc[j] = dot8(dp->x[j], dp->u, dp->acc[j]);
-    sched_slice_dot<DB>();
+    sched_slice_dot<DB, AM>();
 #pragma unroll
     for (int j = 0; j < DB; ++j) pin(dp->acc[j]);
   } else {
-    read_frags<RBUF, RK>(lds, ad, da, db);
+    read_frags<RBUF, RK, AM>(lds, ad, da, db);
     mma16(acc, ua, ub);
-    sched_slice();
+    sched_slice<AM>();
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -403,7 +510,7 @@ __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&
 // A slice with loads, in a fixed order (a scheduling barrier after every MFMA): the 16 MFMAs of (ua, ub); the 8
 // fragment reads of slice RK of buffer RBUF into (da, db), one before every even MFMA; and this wave's 8 load
 // instructions of one operand of a stage into that operand's image of buffer LBUF, one after every odd MFMA.
-template <int RBUF, int RK, bool OPB_, int LBUF, bool KF>
+template <int RBUF, int RK, bool OPB_, int LBUF, bool KF, int AM = 0>
 __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
                                             const Stream& st, const StageSrc& g, int wave) {
@@ -411,20 +518,20 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
 #pragma unroll
   for (int idx = 0; idx < 16; ++idx) {
     if ((idx & 1) == 0) {
-      if (idx == 0) frag_read<RBUF, RK, 0>(lds, ad, da, db);
-      else if (idx == 2) frag_read<RBUF, RK, 1>(lds, ad, da, db);
-      else if (idx == 4) frag_read<RBUF, RK, 2>(lds, ad, da, db);
-      else if (idx == 6) frag_read<RBUF, RK, 3>(lds, ad, da, db);
-      else if (idx == 8) frag_read<RBUF, RK, 4>(lds, ad, da, db);
-      else if (idx == 10) frag_read<RBUF, RK, 5>(lds, ad, da, db);
-      else if (idx == 12) frag_read<RBUF, RK, 6>(lds, ad, da, db);
-      else frag_read<RBUF, RK, 7>(lds, ad, da, db);
+      if (idx == 0) frag_read<RBUF, RK, 0, AM>(lds, ad, da, db);
+      else if (idx == 2) frag_read<RBUF, RK, 1, AM>(lds, ad, da, db);
+      else if (idx == 4) frag_read<RBUF, RK, 2, AM>(lds, ad, da, db);
+      else if (idx == 6) frag_read<RBUF, RK, 3, AM>(lds, ad, da, db);
+      else if (idx == 8) frag_read<RBUF, RK, 4, AM>(lds, ad, da, db);
+      else if (idx == 10) frag_read<RBUF, RK, 5, AM>(lds, ad, da, db);
+      else if (idx == 12) frag_read<RBUF, RK, 6, AM>(lds, ad, da, db);
+      else frag_read<RBUF, RK, 7, AM>(lds, ad, da, db);
     }
     acc[idx >> 2][idx & 3] =
         __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua[idx >> 2], ub[idx & 3], acc[idx >> 2][idx & 3], 0, 0, 0);
     if (idx & 1) {
       const int j = idx >> 1;
-      issue_one<KF>(st, g, j, lds, IMG + (wave * I::LPW + j) * 1024);
+      issue_one<KF, AM == 2>(st, g, j, lds, IMG + (wave * I::LPW + j) * 1024);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -436,31 +543,37 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
 //   wait for this wave's loads of stage kt+1, barrier: every wave has read all of stage kt and stage kt+1 landed;
 //   slice 3: MFMAs on slice 3, reads of slice 0 of stage kt+1 (NB), loads of stage kt+2's A operand into CB.
 // A stage's loads are thus split in two halves, one load per two MFMAs, landing over three slices of MFMAs.
-template <int CB, bool KF, int DB = 0>
+template <int CB, bool KF, int DB = 0, int AM = 0>
 __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4][4], bf16x8 (&fa)[2][4],
                                            bf16x8 (&fb)[2][4], char* lds, const FragAddr& ad, const Stream& sa,
                                            const Stream& sb, int wave, DotState<DB ? DB : 1>* dp = nullptr) {
   constexpr int NB = CB ^ 1;
   {
     const StageSrc gb = stage_src(sb, stage + 1, send);
-    slice_loads<CB, 1, true, NB, KF>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave);
+    slice_loads<CB, 1, true, NB, KF, AM>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave);
   }
-  slice_plain<CB, 2, DB>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], dp);
-  slice_plain<CB, 3, DB>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], dp);
+  slice_plain<CB, 2, DB, AM>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], dp);
+  slice_plain<CB, 3, DB, AM>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], dp);
   wait_vmcnt<0>();
   __syncthreads();
   {
     const StageSrc ga = stage_src(sa, stage + 2, send);
-    slice_loads<NB, 0, false, CB, KF>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
+    slice_loads<NB, 0, false, CB, KF, AM>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
   }
   if constexpr (DB > 0) {
-    if (wave == 0) issue_ap(dp->rsrc, stage + 2, send, lds, CB);
+    if (wave == 0) issue_ap<AM == 2>(dp->rsrc, stage + 2, send, lds, CB);
   }
 }
 
 // Row offset (within the wave's 128 rows) held by accumulator register r of lane half lh in M-subtile mi.
 __device__ __forceinline__ constexpr int acc_row(int mi, int r, int lh) {
   return mi * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+}
+// The output row of that register for A image mode AM: with transposed pieces (AM = 2) A's M index is G's
+// vocabulary position, in kperm order inside each 32-wide group, so the row is the index stored there.
+template <int AM>
+__device__ __forceinline__ constexpr int out_row(int mi, int r, int lh) {
+  return AM == 2 ? kperm_inv(acc_row(mi, r, lh)) : acc_row(mi, r, lh);
 }
 
 // Bias + vocabulary mask of a tile's 256 vocabulary rows: tile_bias() reads bias[v0 + t] (one value per thread,
@@ -489,8 +602,8 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 
 // C[m0:m0+256, n0:n0+256] = sum_k A(m, k) B(n, k) over the K stages s0 .. s0+nk-1 (k in [s0*BK, (s0+nk)*BK),
 // clipped to each operand's extent), fp32 accumulation. KF: both operands' K extents are multiples of BK. Either
-// operand may be row-major or K-blocked; A may instead be in the tile-blocked piece layout (Operand::cm), which
-// needs APC (its LDS image is in piece order). BIAS: A's rows are vocabulary rows and every accumulator starts at its
+// operand may be row-major or K-blocked; A may instead be in the tile-blocked piece layout (Operand::cm = 1), which
+// needs AM = 1 (its LDS image is in piece order), or the transpose of one (Operand::cm = 2, needs AM = 2 and KF). BIAS: A's rows are vocabulary rows and every accumulator starts at its
 // row's bias, masked to -inf for rows >= Vreal (btile: this thread's bias value from tile_bias; bslot: 1 KiB of
 // LDS outside the operand ring), so the epilogue reads the biased, masked logits straight from the accumulators.
 // Output layout (32x32 MFMA): acc[mi][nj][r] is C[wm*128 + mi*32 + 8*(r/4) + 4*(lane/32) + r%4]
@@ -501,7 +614,7 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool BIAS = false, bool APC = false, int DB = 0>
+template <bool KF, bool BIAS = false, int AM = 0, int DB = 0>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
                                           int64_t Vreal = 0, DotState<DB ? DB : 1>* dp = nullptr, int rg0 = 0,
@@ -521,11 +634,11 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
 
   const Stream sa = make_stream(A, m0, wave, lane);
   const Stream sb = make_stream(B, n0, wave, lane);
-  const FragAddr ad = make_frag_addr<APC>(wm, wn, lane);
+  const FragAddr ad = make_frag_addr<AM>(wm, wn, lane);
   const int send = s0 + nk;
   // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
-  issue_stage(sa, s0, send, lds, AOFF, wave);
-  issue_stage(sb, s0, send, lds, BOFF, wave);
+  issue_stage<AM == 2>(sa, s0, send, lds, AOFF, wave);
+  issue_stage<AM == 2>(sb, s0, send, lds, BOFF, wave);
   if constexpr (DB > 0) {
     // this lane's extra fragments: rows rg_j*32 + lane%32 (rg_j = rg0 + j*rg_step), 16-byte chunk 2*wave + lane/32
     // of the stage (slice = wave)
@@ -534,19 +647,24 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
       int rg = rg0 + j * rg_step;
       if (rg > 7) rg = rg0;  // a group past the tile's 8 (tiles_n = 3, 5, 6, 7): computed, never read
       const int ra = rg * 32 + (lane & 31), c = 2 * wave + (lane >> 5);
-      if constexpr (APC)
+      if constexpr (AM == 2) {
+        // rows rg*32 .. +31 are pieces 4rg .. of each piece row; slice `wave` is 8192 bytes per slice in
+        dp->faddr[j] = tra_addr(0, lane, 0) + wave * 8192 + rg * 512;
+        dp->faddr2[j] = tra_addr(0, lane, 1) + wave * 8192 + rg * 512;
+      } else if constexpr (AM == 1) {
         dp->faddr[j] = (ra >> 3) * 1024 + ((c ^ ((ra >> 3) & 1)) << 7) + (ra & 7) * 16;
-      else
+      } else {
         dp->faddr[j] = ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
+      }
       dp->acc[j] = 0.f;
     }
     dp->uaddr = 32 * wave + 16 * (lane >> 5);
     // u of stage s0 before the A loads of stage s0+1, so the wait below covers it
-    if (wave == 0) issue_ap(dp->rsrc, s0, send, lds, 0);
+    if (wave == 0) issue_ap<AM == 2>(dp->rsrc, s0, send, lds, 0);
   }
-  issue_stage(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
+  issue_stage<AM == 2>(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
   if constexpr (DB > 0) {
-    if (wave == 0) issue_ap(dp->rsrc, s0 + 1, send, lds, 1);
+    if (wave == 0) issue_ap<AM == 2>(dp->rsrc, s0 + 1, send, lds, 1);
   }
   if constexpr (BIAS) stash_bias(bslot, btile, m0, Vreal);
   wait_vmcnt<I::LPW>();  // with DB, wave 0's u of stage s0 precedes its last 8 loads
@@ -564,13 +682,13 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   }
 
   bf16x8 fa[2][4], fb[2][4];
-  read_frags<0, 0>(lds, ad, fa[0], fb[0]);
+  read_frags<0, 0, AM>(lds, ad, fa[0], fb[0]);
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    gemm_stage<0, KF, DB>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
-    gemm_stage<1, KF, DB>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+    gemm_stage<0, KF, DB, AM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+    gemm_stage<1, KF, DB, AM>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   }
-  if (kt < nk) gemm_stage<0, KF, DB>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+  if (kt < nk) gemm_stage<0, KF, DB, AM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   wait_vmcnt<0>();
   __syncthreads();
 }
@@ -1076,25 +1194,20 @@ __global__ __launch_bounds__(256) void k_target_fix(const int64_t* __restrict__ 
 
 // Logits-grad tile: recompute S^T for the tile and form G = go*(wgt*exp(x - lse) + c*[v = y]) rounded to bf16,
 // with c = ycoef[n] when given (the (lse, x_y) gradient of chunk_ce: wgt = g_lse, c = g_ly, go = 1 when null)
-// and c = -wgt otherwise (cross-entropy and the mixture: go*wgt*(softmax - onehot)), written to two buffers in
-// the tile-blocked piece layout (Operand::cm), so each tile is one contiguous 128 KiB block of either:
-//   G   [M = n][K = v]  (for dH, reduction over v): block (tm*Np/256 + tn), element (n, v) in piece
-//       (n%256/8, v%256/8)
-//   Gt  [M = v][K = n]  (for dW, reduction over n): block (tn*Vp/256 + tm), element (v, n) in piece
-//       (v%256/8, n%256/8)
-// Both are written from registers; the epilogue uses no LDS and no barrier. For each 32 x 32 block (mi, nj) of a
+// and c = -wgt otherwise (cross-entropy and the mixture: go*wgt*(softmax - onehot)), written in the tile-blocked
+// piece layout (Operand::cm), so each tile is one contiguous 128 KiB block:
+//   G   [M = n][K = v]  (for dH, reduction over v; read transposed for dW, reduction over n): block
+//       (tm*Np/256 + tn), element (n, v) in piece (n%256/8, v%256/8)
+// It is written from registers; the epilogue uses no LDS and no barrier. For each 32 x 32 block (mi, nj) of a
 // wave's accumulators a lane holds one row n (lane%32) and the 16 vocabulary rows 8q + 4(lane/32) + e (q, e =
-// 0..3), i.e. four runs of 4 consecutive v:
-//   * each run is an 8-byte store into G, and the 64 lanes of one store instruction fill four whole 128-byte
-//     pieces (32 rows n x 16 bytes of one 8-wide v chunk);
-//   * the block's bf16 values then go through two v_mfma_f32_32x32x16_bf16 as the A operand (rows n) against
-//     0/1 B operands (transpose_selectors) that send each (lane half, register) slot to its column v; the result
-//     has lane j holding column v = j and the rows n = 8q + 4(lane/32) + e: the transpose, exact because every
-//     product is x*1 or x*0 summed in fp32 (a non-finite G value would spread along its row of the block; G is
-//     finite for finite inputs). Each run of 4 n is again an 8-byte store, four whole pieces per instruction,
-//     into Gt;
-//   * the transposed block also gives the dBias column sums of the bf16 G values (the reference's dBias is the
-//     column sum of its bf16 G) over the wave's 128 rows n: one partial row per (row tile, wave column),
+// 0..3), i.e. four runs of 4 consecutive v, at 16 consecutive kperm positions:
+//   * two 16-byte stores into G, and the 64 lanes of one store instruction fill four whole 128-byte pieces;
+//   * for dBias the block's bf16 values then go through two v_mfma_f32_32x32x16_bf16 as the A operand (rows n)
+//     against 0/1 B operands (transpose_selectors) that send each (lane half, register) slot to its column v; the
+//     result has lane j holding column v = j and the rows n = 8q + 4(lane/32) + e: the transpose, exact because
+//     every product is x*1 or x*0 summed in fp32 (a non-finite G value would spread along its row of the block; G
+//     is finite for finite inputs). It gives the dBias column sums of the bf16 G values (the reference's dBias is
+//     the column sum of its bf16 G) over the wave's 128 rows n: one partial row per (row tile, wave column),
 //     dbias_part[(2*tn + wn)*Vp + v].
 // The target element takes its fp32 value from k_target_fix and, with a sparse bias, the row's candidate
 // elements take their fix-up values (k_sparse_rows); both are register selects. Rows past N use lse = +inf and
@@ -1119,30 +1232,25 @@ __device__ __forceinline__ void store_b128_nt(uint16_t* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
-// One 32 x 32 block (mi, nj) of a wave's bf16 logits-grad values into both tile-blocked buffers. pk: lane (row
-// n = nb + lr) holds the 16 vocabulary rows vw + mi*32 + 8(r/4) + 4lh + r%4 (r = 0..15, two per word).
-//   G:  those sit at kperm positions mi*32 + 16lh + r: chunks wm*16 + mi*4 + 2lh + s (s = 0, 1) of the block,
-//       16 bytes each;
-//   Gt: the two selector MFMAs transpose the block, so lane lr holds column v = vw + mi*32 + lr and the rows
-//       n = nb + 8(r/4) + 4lh + r%4, at kperm positions nj*32 + 16lh + r: chunks wn*16 + nj*4 + 2lh + s.
-// Returns the transposed block (fp32 copies of the bf16 values) for column sums.
-__device__ __forceinline__ f32x16 store_g_block(uint16_t* gblk, uint16_t* tblk, const uint32_t (&pk)[8],
-                                                const bf16x8& b1, const bf16x8& b2, int wm, int wn, int mi, int nj,
-                                                int lr, int lh) {
-  const int nl = wn * 128 + nj * 32 + lr, vl = wm * 128 + mi * 32 + lr;
+// One 32 x 32 block (mi, nj) of a wave's bf16 logits-grad values into the tile-blocked G. pk: lane (row
+// n = nb + lr) holds the 16 vocabulary rows vw + mi*32 + 8(r/4) + 4lh + r%4 (r = 0..15, two per word), which sit at
+// kperm positions mi*32 + 16lh + r: chunks wm*16 + mi*4 + 2lh + s (s = 0, 1) of the block, 16 bytes each. (The dW
+// contraction reads G itself, transposed in LDS: no G^T copy is written.)
+__device__ __forceinline__ void store_g_block(uint16_t* gblk, const uint32_t (&pk)[8], int wm, int wn, int mi,
+                                              int nj, int lr, int lh) {
+  const int nl = wn * 128 + nj * 32 + lr;
 #pragma unroll
   for (int sc = 0; sc < 2; ++sc)
     store_b128_nt(gblk + ((nl >> 3) * 32 + wm * 16 + mi * 4 + 2 * lh + sc) * 64 + (nl & 7) * 8,
                   u32x4{pk[4 * sc], pk[4 * sc + 1], pk[4 * sc + 2], pk[4 * sc + 3]});
+}
+// The block's transpose by the two selector MFMAs, for column sums: lane lr then holds column v = vw + mi*32 + lr
+// and the rows n = nb + 8(r/4) + 4lh + r%4 (fp32 copies of the bf16 values).
+__device__ __forceinline__ f32x16 transpose_block(const uint32_t (&pk)[8], const bf16x8& b1, const bf16x8& b2) {
   const u32x4 a1{pk[0], pk[1], pk[2], pk[3]}, a2{pk[4], pk[5], pk[6], pk[7]};
   f32x16 tr = {};
   tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a1), b1, tr, 0, 0, 0);
   tr = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a2), b2, tr, 0, 0, 0);
-#pragma unroll
-  for (int sc = 0; sc < 2; ++sc)
-    store_b128_nt(tblk + ((vl >> 3) * 32 + wn * 16 + nj * 4 + 2 * lh + sc) * 64 + (vl & 7) * 8,
-                  u32x4{pack_bf16x2(tr[8 * sc], tr[8 * sc + 1]), pack_bf16x2(tr[8 * sc + 2], tr[8 * sc + 3]),
-                        pack_bf16x2(tr[8 * sc + 4], tr[8 * sc + 5]), pack_bf16x2(tr[8 * sc + 6], tr[8 * sc + 7])});
   return tr;
 }
 
@@ -1155,7 +1263,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
                 const float* __restrict__ wgt_rows, const int* __restrict__ fix_col,
                 const float* __restrict__ fix_val, int nfix, const float* __restrict__ go, int64_t N, int64_t Np,
                 int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n, uint16_t* __restrict__ G,
-                uint16_t* __restrict__ Gt, float* __restrict__ dbias_part) {
+                float* __restrict__ dbias_part) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
@@ -1192,9 +1300,9 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   }
   bf16x8 b1, b2;
   transpose_selectors(b1, b2, lane);
-  // this tile's 128 KiB blocks of G and Gt: element (row m, chunk c, e) at ((m/8)*32 + c)*64 + (m%8)*8 + e
+  // this tile's 128 KiB block of G: element (row m, chunk c, e) at ((m/8)*32 + c)*64 + (m%8)*8 + e
   uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
-  uint16_t* tblk = Gt + ((int64_t)tn * (Vp / BM) + tm) * CM_TILE;
+  const bool sums = dbias_part != nullptr;
   float db[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
@@ -1241,14 +1349,17 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
       uint32_t pk[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) pk[i] = pack_bf16x2(g[2 * i], g[2 * i + 1]);
-      const f32x16 tr = store_g_block(gblk, tblk, pk, b1, b2, wm, wn, mi, nj, lr, lh);
-      float s = 0.f;
+      store_g_block(gblk, pk, wm, wn, mi, nj, lr, lh);
+      if (sums) {
+        const f32x16 tr = transpose_block(pk, b1, b2);
+        float s = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s += tr[r];
-      db[mi] += s;
+        for (int r = 0; r < 16; ++r) s += tr[r];
+        db[mi] += s;
+      }
     }
   }
-  if (dbias_part != nullptr) {
+  if (sums) {
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) db[mi] += __shfl_xor(db[mi], 32);
     if (lh == 0) {
@@ -1303,7 +1414,7 @@ __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, co
 //   G[n, v] = go * wgt_n * (exp(x_v - lse_n) - [v = y_n]) = go * a_n * E'[n, v],
 //   E[n, v] = exp(x_v - e_n),  a_n = wgt_n * exp(e_n - lse_n),  E'[n, y_n] = (exp(x_y - lse_n) - 1) exp(lse_n - e_n)
 // with e_n a lower bound of lse_n that is known before the tiles run: the logsumexp of the first vocabulary tile
-// and of the target logit (k_lse_est). E' (= E except at the target) goes into the G / Gt buffers in the
+// and of the target logit (k_lse_est). E' (= E except at the target) goes into the G buffer in the
 // tile-blocked layout; the per-row factor a_n, which needs the final lse, is applied by the backward
 // (dH = go a . (E' W) in the GEMM epilogue, dW = E'^T (go a . H) through a row-scaled H^T copy, dBias = E'^T (go a)).
 // Because e_n <= lse_n, E underflows only where the softmax is below e^-87 anyway. It could overflow only where a
@@ -1373,15 +1484,15 @@ __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_
 }
 
 // Forward tile of the training path: the logits tile as in k_fwd_tiles, then E = exp(x - e_n) for its 256 x 256
-// elements, rounded to bf16 and stored into G and Gt exactly as k_bwd_grad stores G (store_g_block). The
+// elements, rounded to bf16 and stored into G exactly as k_bwd_grad stores it (store_g_block). The
 // half-tile partials are (e_n, sum of E) -- or, for a flagged row, (max, sum of exp(x - max)) -- in the part_m /
 // part_s format k_fwd_merge reads. Rows past N use e = +inf, so their E is exactly zero.
 template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const float* __restrict__ lse_est,
-                 int64_t N, int64_t Np, int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n, float s_max,
-                 uint16_t* __restrict__ G, uint16_t* __restrict__ Gt, float* __restrict__ part_m,
-                 float* __restrict__ part_s, int* __restrict__ flag) {
+                 int64_t N, int64_t Np, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, float s_max,
+                 uint16_t* __restrict__ G, float* __restrict__ part_m, float* __restrict__ part_s,
+                 int* __restrict__ flag) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
@@ -1400,10 +1511,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
   f32x16 acc[4][4];
   gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
                       reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
-  bf16x8 b1, b2;
-  transpose_selectors(b1, b2, lane);
   uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
-  uint16_t* tblk = Gt + ((int64_t)tn * (Vp / BM) + tm) * CM_TILE;
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
@@ -1419,7 +1527,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
       uint32_t pk[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) pk[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
-      (void)store_g_block(gblk, tblk, pk, b1, b2, wm, wn, mi, nj, lr, lh);
+      store_g_block(gblk, pk, wm, wn, mi, nj, lr, lh);
     }
     s += __shfl_xor(s, 32);
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
@@ -1464,10 +1572,9 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
                                                     const float* __restrict__ lse_est,
                                                     const float* __restrict__ lse_rows,
                                                     const float* __restrict__ wgt_rows, const int* __restrict__ flag,
-                                                    int64_t N, int64_t Np, int64_t Vp, int64_t Vreal,
+                                                    int64_t N, int64_t Np, int64_t Vreal,
                                                     float* __restrict__ arow, int* __restrict__ flag_count,
-                                                    int* __restrict__ flag_list, uint16_t* __restrict__ G,
-                                                    uint16_t* __restrict__ Gt) {
+                                                    int* __restrict__ flag_list, uint16_t* __restrict__ G) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= Np) return;
   if (n >= N) {
@@ -1486,18 +1593,14 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   arow[n] = w * expf(e - l);
   const int64_t yn = y[n];
   if (yn >= 0 && yn < Vreal) {
-    const uint16_t b = to_bf16((expf(xy[n] - l) - 1.f) * expf(l - e));
-    G[cm_index(n, yn, Np)] = b;
-    Gt[cm_index(yn, n, Vp)] = b;
+    G[cm_index(n, yn, Np)] = to_bf16((expf(xy[n] - l) - 1.f) * expf(l - e));
   }
   // sparse bias: each distinct valid candidate other than the target gets its true logit x_c + B_c (the target's
   // x_y already includes its bias)
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
     if (c == yn || !first_valid(cand, kc, n, k, Vreal)) continue;
-    const uint16_t b = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - e));
-    G[cm_index(n, c, Np)] = b;
-    Gt[cm_index(c, n, Vp)] = b;
+    G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - e));
   }
 }
 
@@ -1505,11 +1608,11 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
 // the first vocabulary tile and the target makes rare, or whose lse exceeds e_n by more than 60). Three kernels:
 // k_gather_rows copies the flagged rows of H into a dense operand Hf [F][K] (F = the flagged-row count); k_exact_train
 // runs the logits tile mainloop over (vocabulary tile, 256 gathered rows) items with each row shifted by its exact
-// lse, so E'[n, v] = exp(x_v - lse_n) (<= 1; a_n = wgt_n for these rows), and stores it in place: 16 bytes per lane
-// into G (the lane's own row), element by element into G^T (the rows are scattered); k_exact_fix then writes the
-// target's exp(x_y - lse) - 1 and, with a sparse bias, the candidates' exp(x_c + B_c - lse) over those entries.
-// The work is that of F rows of the forward tile pass (plus F * Vp scattered 2-byte stores), so the fallback costs
-// in proportion to the flagged rows; k_exact_train is a persistent loop whose item count it reads on the device.
+// lse, so E'[n, v] = exp(x_v - lse_n) (<= 1; a_n = wgt_n for these rows), and stores it in place in G, 16 bytes per
+// lane (the lane's own row); k_exact_fix then writes the target's exp(x_y - lse) - 1 and, with a sparse bias, the
+// candidates' exp(x_c + B_c - lse) over those entries. The work is that of F rows of the forward tile pass, so the
+// fallback costs in proportion to the flagged rows; k_exact_train is a persistent loop whose item count it reads on
+// the device.
 
 // Hf[i, :] = H[list[i], :] for i < *count (K % 8 == 0), 16 bytes per thread, grid-stride.
 __global__ __launch_bounds__(256) void k_gather_rows(const uint16_t* __restrict__ H, int64_t ldh,
@@ -1526,8 +1629,7 @@ template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, const float* __restrict__ bias,
                    const int* __restrict__ count, const int* __restrict__ list, const float* __restrict__ lse_rows,
-                   int64_t Np, int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, uint16_t* __restrict__ G,
-                   uint16_t* __restrict__ Gt) {
+                   int64_t Np, int64_t V, int64_t Vreal, int tiles_v, uint16_t* __restrict__ G) {
   __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
   const int cnt = *count;
   const int items = tiles_v * ((cnt + BN - 1) / BN);
@@ -1557,11 +1659,6 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
       // wm*128 + mi*32 + 16lh + r, i.e. 16-byte chunks wm*16 + mi*4 + 2lh + r/8
       uint16_t* grow = G + ((int64_t)tm * (Np / BM) + n / BM) * CM_TILE + ((n % BM) >> 3) * 32 * 64 + (n & 7) * 8 +
                        (wm * 16 + 2 * lh) * 64;
-      // G^T: element (v, n) at block (n/256, v/256), piece (v%256/8, kperm(n%256)/8), offset (v%8)*8 + kperm%8;
-      // v%256 = wm*128 + mi*32 + 8(r/4) + 4lh + r%4, so piece row wm*16 + mi*4 + r/4 and v%8 = 4lh + r%4
-      const int kpn = kperm((int)(n & 255));
-      uint16_t* gtcol = Gt + ((n / BM) * (Vp / BM) + tm) * CM_TILE + (kpn >> 3) * 64 + (kpn & 7) +
-                        wm * 16 * 32 * 64 + lh * 4 * 8;
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         uint32_t pk[8];
@@ -1574,9 +1671,6 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
           for (int sc = 0; sc < 2; ++sc)
             *reinterpret_cast<u32x4*>(grow + (mi * 4 + sc) * 64) =
                 u32x4{pk[4 * sc], pk[4 * sc + 1], pk[4 * sc + 2], pk[4 * sc + 3]};
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            gtcol[(mi * 4 + (r >> 2)) * 32 * 64 + (r & 3) * 8] = (uint16_t)((pk[r >> 1] >> (16 * (r & 1))) & 0xFFFFu);
         }
       }
     }
@@ -1585,73 +1679,60 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
 
 // The target and candidate entries of the rows k_exact_train rewrote (list[i], i < *count): E'[n, y_n] =
 // exp(x_y - lse_n) - 1 and, for each distinct valid candidate c != y_n, E'[n, c] = exp(x_c + B_c - lse_n), from the
-// row logits of k_row_logits (x_y with its sparse bias, x_c without), into G and G^T. One thread per entry.
+// row logits of k_row_logits (x_y with its sparse bias, x_c without), into G. One thread per entry.
 __global__ __launch_bounds__(256) void k_exact_fix(const int* __restrict__ count, const int* __restrict__ list,
                                                    const int64_t* __restrict__ y, const float* __restrict__ xy,
                                                    const int64_t* __restrict__ cand, const float* __restrict__ cval,
                                                    const float* __restrict__ xc, int kc,
-                                                   const float* __restrict__ lse_rows, int64_t Np, int64_t Vp,
-                                                   int64_t Vreal, uint16_t* __restrict__ G, uint16_t* __restrict__ Gt) {
+                                                   const float* __restrict__ lse_rows, int64_t Np,
+                                                   int64_t Vreal, uint16_t* __restrict__ G) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= *count) return;
   const int64_t n = list[i], yn = y[n];
   const float l = lse_rows[n];
-  if (yn >= 0 && yn < Vreal) {
-    const uint16_t b = to_bf16(expf(xy[n] - l) - 1.f);
-    G[cm_index(n, yn, Np)] = b;
-    Gt[cm_index(yn, n, Vp)] = b;
-  }
+  if (yn >= 0 && yn < Vreal) G[cm_index(n, yn, Np)] = to_bf16(expf(xy[n] - l) - 1.f);
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
     if (c == yn || !first_valid(cand, kc, n, k, Vreal)) continue;
-    const uint16_t b = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - l));
-    G[cm_index(n, c, Np)] = b;
-    Gt[cm_index(c, n, Vp)] = b;
+    G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - l));
   }
 }
 
 // dBias partials of the training path: part[s][v] = go * sum over the row tiles of split s of
-// sum_n a_n E'[n, v], read from Gt (block (n/256, v/256), one 128 KiB block per row tile). Block (v tile, split s);
-// thread t owns the vocabulary rows 8i + t%8 (i = 0..31) of the tile and the 8-wide chunk t/8 of reduction
-// positions (kperm order), so each 16-byte load is one piece row; the 32 chunk sums of a row are added in a fixed
-// order through LDS.
-__global__ __launch_bounds__(256) void k_dbias_gemv(const uint16_t* __restrict__ Gt, const float* __restrict__ arow,
+// sum_n a_n E'[n, v], read from G (block (v/256, n/256), one 128 KiB block per row tile). Block (v tile, split s);
+// thread t owns row t%8 of every 8-row piece group and the vocabulary chunk t/8 (positions 8(t/8) .. +7, kperm
+// order), so the 256 threads read each 4 KiB piece row of a block contiguously; the 8 row sums of a chunk are
+// added by a fixed butterfly, and thread t then writes position 8(t/8) + t%8, i.e. vocabulary row
+// kperm_inv(8(t/8) + t%8) of the tile.
+__global__ __launch_bounds__(256) void k_dbias_gemv(const uint16_t* __restrict__ G, const float* __restrict__ arow,
                                                     const float* __restrict__ go, int64_t Np, int64_t Vp,
                                                     int per_split, float* __restrict__ part) {
-  __shared__ float red[32][257];
-  const int t = threadIdx.x, c = t >> 3;
+  const int t = threadIdx.x, r = t & 7;
   const int64_t tv = blockIdx.x;
   const int s = (int)blockIdx.y;
   const int nt = (int)(Np / BM);
   const int j0 = s * per_split, j1 = min(nt, j0 + per_split);
-  float acc[32];
+  float acc[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-  // positions 8c .. 8c+7 hold the rows kperm_inv(8c + e): two runs of 4 consecutive n
-  const int r0 = kperm_inv(8 * c), r1 = kperm_inv(8 * c + 4);
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   for (int j = j0; j < j1; ++j) {
-    const float4 a0 = *reinterpret_cast<const float4*>(arow + (int64_t)j * BM + r0);
-    const float4 a1 = *reinterpret_cast<const float4*>(arow + (int64_t)j * BM + r1);
-    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const uint16_t* blk = Gt + ((int64_t)j * (Vp / BM) + tv) * CM_TILE;
-#pragma unroll 8
-    for (int i = 0; i < 32; ++i) {
-      const u16x8 g = *reinterpret_cast<const u16x8*>(blk + ((int64_t)i * 256 + t) * 8);
-      float d = 0.f;
+    const uint16_t* blk = G + (tv * (Np / BM) + j) * CM_TILE;
+#pragma unroll 4
+    for (int ng = 0; ng < 32; ++ng) {
+      const float a = arow[(int64_t)j * BM + ng * 8 + r];
+      const u16x8 g = *reinterpret_cast<const u16x8*>(blk + ((int64_t)ng * 256 + t) * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = __builtin_fmaf(bf16_to_f32(g[e]), av[e], d);
-      acc[i] += d;
+      for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(bf16_to_f32(g[e]), a, acc[e]);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 32; ++i) red[i][t] = acc[i];
-  __syncthreads();
-  // vocabulary row 8i + r of the tile (thread t: i = t/8, r = t%8) = sum over the 32 chunks c of red[i][8c + r]
-  const int i = t >> 3, r = t & 7;
-  float sum = 0.f;
+  for (int m = 1; m < 8; m <<= 1)
 #pragma unroll
-  for (int cc = 0; cc < 32; ++cc) sum += red[i][cc * 8 + r];
-  part[(int64_t)s * Vp + tv * BM + t] = (go != nullptr ? go[0] : 1.f) * sum;
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], m);
+  float mine = acc[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mine = r == e ? acc[e] : mine;
+  part[(int64_t)s * Vp + tv * BM + kperm_inv((t >> 3) * 8 + r)] = (go != nullptr ? go[0] : 1.f) * mine;
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1659,19 +1740,20 @@ __global__ __launch_bounds__(256) void k_dbias_gemv(const uint16_t* __restrict__
 // 0 for R <= r < (grid rows); c < C (C % 8 == 0). With rscale, source row r is first multiplied by
 // go[0] * rscale[r] (fp32) and rounded to bf16; uperm (needs rscale) then also receives those factors as bf16 in
 // the same kperm order, uperm[p] for every p < grid rows (0 past R). One workgroup per 64 x 64 tile, staged through LDS. The
-// reduction index r is stored in the permuted order kperm that G and Gt use (their 16-byte stores), so the
-// products of the dH and dW contractions pair up.
+// reduction index r is stored in the permuted order kperm that G uses for its vocabulary positions (its 16-byte
+// stores), so the products of the dH contraction (W^T) pair up; natural != 0 stores r (and uperm) in natural order
+// instead, the order of G's rows that the dW contraction reduces over (H^T).
 __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __restrict__ src, int64_t ld, int64_t R,
                                                            int64_t C, uint16_t* __restrict__ dst,
                                                            const float* __restrict__ rscale = nullptr,
                                                            const float* __restrict__ go = nullptr,
-                                                           uint16_t* __restrict__ uperm = nullptr) {
+                                                           uint16_t* __restrict__ uperm = nullptr, int natural = 0) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64][66];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   if (uperm != nullptr && blockIdx.y == 0 && t < 64) {
-    // the row scales themselves, bf16, in the same kperm order: uperm[r0 + p] = go * rscale[r0 + kperm_inv(p)]
-    const int64_t r = r0 + kperm_inv(t);
+    // the row scales themselves, bf16, in the same order: uperm[r0 + p] = go * rscale[r0 + kperm_inv(p)]
+    const int64_t r = r0 + (natural ? t : kperm_inv(t));
     uperm[r0 + t] = r < R ? to_bf16((go != nullptr ? go[0] : 1.f) * rscale[r]) : (uint16_t)0;
   }
 #pragma unroll
@@ -1704,7 +1786,7 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
       // output positions r0 + 8rq .. +7 (kperm order) hold the rows kperm_inv(8rq + e)
       u16x8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = tile[kperm_inv(rq * 8 + e)][cl];
+      for (int e = 0; e < 8; ++e) v[e] = tile[natural ? rq * 8 + e : kperm_inv(rq * 8 + e)][cl];
       const int64_t r = r0 + rq * 8;
       *reinterpret_cast<u16x8*>(dst + (r >> 8) * C * BLK + c * BLK + (r & (BLK - 1))) = v;
     }
@@ -1765,7 +1847,7 @@ __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict_
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16, bool KF, bool APC, int DB>
+template <bool OUT_BF16, bool KF, int AM, int DB>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* C, int64_t ldc, float* __restrict__ part,
@@ -1798,7 +1880,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
     DotState<DB> dp;
     dp.rsrc = make_rsrc(reinterpret_cast<uint64_t>(u));
     const bool active = tn < 8;  // tiles_n > 8: the tiles past the 8th column have no group
-    gemm_tile<KF, false, APC, DB>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, active ? tn : 0, tiles_n);
+    gemm_tile<KF, false, AM, DB>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, active ? tn : 0, tiles_n);
     // lanes l and l+32 hold the two K halves of row rg_j*32 + l%32; the four waves hold the four slices
     float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
@@ -1811,10 +1893,10 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
       const int j = t >> 5, r = t & 31;
       const int64_t row = (slot >= 0 ? (int64_t)tiles_m * tiles_n + slot : lin) * DB + j;
       const float* rj = red + j * 128;
-      upart[row * 32 + r] = (rj[r] + rj[32 + r]) + (rj[64 + r] + rj[96 + r]);
+      upart[row * 32 + (AM == 2 ? kperm_inv(r) : r)] = (rj[r] + rj[32 + r]) + (rj[64 + r] + rj[96 + r]);
     }
   } else {
-    gemm_tile<KF, false, APC>(A, B, s0, nk, m0, n0, lds, acc);
+    gemm_tile<KF, false, AM>(A, B, s0, nk, m0, n0, lds, acc);
   }
   if (slot >= 0) {
     float* pt = part + (int64_t)slot * BM * BN;
@@ -1824,7 +1906,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          pt[(wm * 128 + acc_row(mi, r, lh)) * BN + wn * 128 + nj * 32 + lr] = acc[mi][nj][r];
+          pt[(wm * 128 + out_row<AM>(mi, r, lh)) * BN + wn * 128 + nj * 32 + lr] = acc[mi][nj][r];
     return;
   }
   const float gs = go != nullptr ? go[0] : 1.f;
@@ -1848,7 +1930,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
         for (int q = 0; q < 2; ++q)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int64_t i = m0 + wm * 128 + acc_row(2 * mh + q, r, lh);
+            const int64_t i = m0 + wm * 128 + out_row<AM>(2 * mh + q, r, lh);
 #pragma unroll
             for (int nj = 0; nj < 4; ++nj) {
               const int64_t j = n0 + wn * 128 + nj * 32 + lr;
@@ -1869,9 +1951,9 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int mi = 2 * mh + q;
-        const int64_t i = m0 + wm * 128 + acc_row(mi, r, lh);
+        const int64_t i = m0 + wm * 128 + out_row<AM>(mi, r, lh);
         if (i >= M) continue;
-        const float sc = rscale != nullptr ? rs[wm * 128 + acc_row(mi, r, lh)] : gs;
+        const float sc = rscale != nullptr ? rs[wm * 128 + out_row<AM>(mi, r, lh)] : gs;
 #pragma unroll
         for (int nj = 0; nj < 4; ++nj) {
           const int64_t j = n0 + wn * 128 + nj * 32 + lr;
@@ -1991,15 +2073,14 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
 }
 
 // Backward workspace (Np = N and Vp = V rounded up to 256):
-//   G   [Vp/256][Np/256][32][32][8][8] bf16, Gt [Np/256][Vp/256][32][32][8][8] bf16 (tile-blocked pieces;
-//       written by k_bwd_grad)
+//   G   [Vp/256][Np/256][32][32][8][8] bf16 (tile-blocked pieces; written by k_bwd_grad)
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
 //   dbias_part [2*Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split
 //   tails), ty int32 / tval fp32 [Np] (k_target_fix)
 //   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), fix_col int32 / fix_val fp32 [Np][MAX_KC]
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
-  uint16_t *G, *Gt, *Wt, *Ht;
+  uint16_t *G, *Wt, *Ht;
   float *dbias_part, *xy, *part, *xc, *fix_val, *tval;
   int *fix_col, *ty;
   int64_t np, vp;
@@ -2011,7 +2092,6 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.vp = cdiv(V, BLK) * BLK;
   size_t off = 0;
   w.G = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * w.np);
-  w.Gt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * w.np);
   w.Wt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * K);
   w.Ht = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.np * K);
   w.dbias_part = reinterpret_cast<float*>(base + off);
@@ -2123,43 +2203,48 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (B.cm) return MCE_EINVAL;  // only the A operand may be in the piece layout
   if (p_out) *p_out = P;
   if (full_out) *full_out = full;
-  // dot products with u: only for an A operand in the piece layout (G^T), fp32 output; with more than one row
-  // group per tile only for whole K stages
+  // transposed pieces (G read with the vocabulary as M, for dW): whole K stages only. Dot products with u: only
+  // with such an A operand and fp32 output
   const int nr = fold_nr(tiles_n);
-  if (u != nullptr && (OUT_BF16 || !A.cm || upart == nullptr || (nr > 1 && !kf))) return MCE_EINVAL;
+  if (A.cm == 2 && !kf) return MCE_EINVAL;
+  if (u != nullptr && (OUT_BF16 || A.cm != 2 || upart == nullptr)) return MCE_EINVAL;
   ProfScope prof(pcls, st);
   if (u != nullptr) {
     if constexpr (!OUT_BF16) {
-#define MCE_GEMM_DB(KF_, NR_)                                                                                \
-  hipLaunchKernelGGL((k_gemm<false, KF_, true, NR_>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, \
+#define MCE_GEMM_DB(NR_)                                                                                   \
+  hipLaunchKernelGGL((k_gemm<false, true, 2, NR_>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, \
                      tiles_n, group, full, P, C, ldc, part, rscale, go, cin, u, upart)
-      if (!kf)
-        MCE_GEMM_DB(false, 1);
-      else if (nr == 1)
-        MCE_GEMM_DB(true, 1);
+      if (nr == 1)
+        MCE_GEMM_DB(1);
       else if (nr == 2)
-        MCE_GEMM_DB(true, 2);
+        MCE_GEMM_DB(2);
       else if (nr == 3)
-        MCE_GEMM_DB(true, 3);
+        MCE_GEMM_DB(3);
       else if (nr == 4)
-        MCE_GEMM_DB(true, 4);
+        MCE_GEMM_DB(4);
       else
-        MCE_GEMM_DB(true, 8);
+        MCE_GEMM_DB(8);
 #undef MCE_GEMM_DB
     }
+  } else if (A.cm == 2) {
+    if constexpr (!OUT_BF16)
+      hipLaunchKernelGGL((k_gemm<false, true, 2, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, tiles_n,
+                         group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
+    else
+      return MCE_EINVAL;
   } else if (A.cm) {
     if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, true, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, 1, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
     else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, true, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, 1, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
   } else {
     if (kf)
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, false, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, true, 0, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
     else
-      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, false, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
+      hipLaunchKernelGGL((k_gemm<OUT_BF16, false, 0, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
                          tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
   }
   prof.end();
@@ -2268,7 +2353,7 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
   return launch_sum(loss_rows, N, w.sum_part, loss_sum, st);
 }
 
-// Logits gradient of every variant: G (and G^T) into the workspace, plus dBias, dGate (mixture) and dCval
+// Logits gradient of every variant: G into the workspace, plus dBias, dGate (mixture) and dCval
 // (sparse bias) when requested.
 int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
               const int64_t* cand, const float* cval, int kc, const float* lse_rows, const float* wgt_rows,
@@ -2305,11 +2390,11 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
     ProfScope prof(PROF_BWD_GRAD, st);
     if (K % BK == 0)
       hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G,
                          dBias ? w.dbias_part : nullptr);
     else
       hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G, w.Gt,
+                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G,
                          dBias ? w.dbias_part : nullptr);
   }
   if ((rc = launch_status())) return rc;
@@ -2326,28 +2411,28 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
 }
 
 // Training-path workspace. The rows are processed in blocks of `nb` rows (a multiple of 256; the last block may be
-// shorter): per block E' in G / Gt (tile-blocked, the block's rows padded to a multiple of 256), the row-scaled
-// H^T copy and go*a in bf16 (kperm order), the half-tile partials and the flagged-row list, all reused block after
+// shorter): per block E' in G (tile-blocked, the block's rows padded to a multiple of 256), the row-scaled
+// H^T copy and go*a in bf16 (natural row order), the half-tile partials and the flagged-row list, all reused block after
 // block (the last block's stay for the backward); once per call W^T (for dH), the first vocabulary tile's partials,
 // the target / candidate logits, e_n, a_n, the flags and the per-block flagged-row counts over all rows, the loss
 // partials, the dW blocks' dBias partials, the K-split tail tiles and the dBias GEMV partials.
 struct TrainWs {
   int64_t np, vp, nb, nblk;
-  uint16_t *G, *Gt, *Ht, *uperm, *Wt;
+  uint16_t *G, *Ht, *uperm, *Wt;
   float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *lse_est, *arow, *upart, *part, *dbias_part, *sum_part;
   int *flag, *flag_list, *counts, *xlist;
   size_t bytes;
 };
 constexpr int DBIAS_SPLITS = 8;
-// Memory for the G / G^T pair of one row block when the caller leaves the block size to the library: 2 GiB, i.e.
-// 8192 rows at V = 50304 and 4096 rows at V = 131072.
+// Memory for G of one row block when the caller leaves the block size to the library: 2 GiB, i.e. at most 21248
+// rows at V = 50304 (16384-row blocks for 32768 rows) and 8192 rows at V = 131072.
 constexpr int64_t TRAIN_BLOCK_BUDGET = int64_t(2) << 30;
 
-// Rows per block: the requested count (0: the largest that keeps G / G^T within TRAIN_BLOCK_BUDGET) rounded up to
-// a multiple of 256, then evened out over the blocks it takes.
+// Rows per block: the requested count (0: the largest that keeps G within TRAIN_BLOCK_BUDGET) rounded up to a
+// multiple of 256, then evened out over the blocks it takes.
 int64_t train_block_rows(int64_t N, int64_t V, int64_t req) {
   const int64_t np = cdiv(N, BLK) * BLK, vp = cdiv(V, BLK) * BLK;
-  int64_t cap = req > 0 ? cdiv(req, BLK) * BLK : TRAIN_BLOCK_BUDGET / (4 * vp) / BLK * BLK;
+  int64_t cap = req > 0 ? cdiv(req, BLK) * BLK : TRAIN_BLOCK_BUDGET / (2 * vp) / BLK * BLK;
   if (cap < BLK) cap = BLK;
   if (cap >= np) return np > 0 ? np : BLK;
   return cdiv(cdiv(np, cdiv(np, cap)), BLK) * BLK;
@@ -2367,7 +2452,6 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
     return p;
   };
   w.G = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * nb));
-  w.Gt = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * nb));
   w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb * K));
   w.uperm = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb));
   w.part_m = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
@@ -2425,9 +2509,11 @@ int train_block_grads(const TrainWs& w, int64_t b, const uint16_t* H, int64_t ld
     // H^T of the block scaled by a (and, for dBias, a itself in bf16); dW = E'^T (a . H), and the dW tiles also form
     // the dBias partials sum_n E'[n, v] a_n, each over its share of the K stages (k_dbias_tiles adds them)
     hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(rp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st,
-                       H + row0 * ldh, ldh, rows, K, w.Ht, w.arow + row0, nullptr, dBias ? w.uperm : nullptr);
+                       H + row0 * ldh, ldh, rows, K, w.Ht, w.arow + row0, nullptr, dBias ? w.uperm : nullptr, 1);
     if ((rc = launch_status())) return rc;
-    const Operand Aop{w.Gt, 0, V, rp, w.vp * BLK, 1};
+    // G read transposed: M = the vocabulary (v tiles rp*256 elements apart), K = the block's rows (row tiles
+    // 65536 elements apart)
+    const Operand Aop{w.G, rp * BLK, V, rp, CM_TILE, 2};
     const Operand Bop{w.Ht, BLK, K, rp, K * BLK, 0};
     int P = 1, full = 0;
     if ((rc = launch_gemm<false>(Aop, Bop, (int)(rp / BK), V, K, 4, dW, lddw, w.part, st, nullptr, go, dW_in,
@@ -2438,11 +2524,11 @@ int train_block_grads(const TrainWs& w, int64_t b, const uint16_t* H, int64_t ld
                        (int)cdiv(K, BN), fold_nr(cdiv(K, BN)), 4, full, P, V, go, dBias_in, dBias);
     return launch_status();
   }
-  // dBias without dW: a pass over the block's G^T
+  // dBias without dW: a pass over the block's G
   const int nt = (int)(rp / BM);
   const int per = (int)cdiv(nt, DBIAS_SPLITS);
   const int splits = (int)cdiv(nt, per);
-  hipLaunchKernelGGL(k_dbias_gemv, dim3((unsigned)(w.vp / BM), (unsigned)splits), dim3(256), 0, st, w.Gt,
+  hipLaunchKernelGGL(k_dbias_gemv, dim3((unsigned)(w.vp / BM), (unsigned)splits), dim3(256), 0, st, w.G,
                      w.arow + row0, nullptr, rp, w.vp, per, w.dbias_part);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, splits, w.vp, V,
@@ -2520,12 +2606,11 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
       ProfScope prof(PROF_FWD_TRAIN, st);
       if (kf)
         hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est + row0,
-                           rows, rp, V, w.vp, V_real, tv, tnb, g_train_s_max, w.G, w.Gt, w.part_m, w.part_s,
-                           w.flag + row0);
+                           rows, rp, V, V_real, tv, tnb, g_train_s_max, w.G, w.part_m, w.part_s, w.flag + row0);
       else
         hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias,
-                           w.lse_est + row0, rows, rp, V, w.vp, V_real, tv, tnb, g_train_s_max, w.G, w.Gt, w.part_m,
-                           w.part_s, w.flag + row0);
+                           w.lse_est + row0, rows, rp, V, V_real, tv, tnb, g_train_s_max, w.G, w.part_m, w.part_s,
+                           w.flag + row0);
     }
     if ((rc = launch_status())) return rc;
     int* xcount = w.counts + w.np / BLK + b;
@@ -2540,8 +2625,8 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
       return rc;
     hipLaunchKernelGGL(k_train_rows, dim3((unsigned)(rp / 256)), dim3(256), 0, st, y + row0, w.xy + row0,
                        at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, w.lse_est + row0,
-                       lse_rows + row0, wgt_rows + row0, w.flag + row0, rows, rp, w.vp, V_real, w.arow + row0,
-                       w.counts + b, w.flag_list, w.G, w.Gt);
+                       lse_rows + row0, wgt_rows + row0, w.flag + row0, rows, rp, V_real, w.arow + row0,
+                       w.counts + b, w.flag_list, w.G);
     if ((rc = launch_status())) return rc;
     // the flagged rows' exact E' (the block's H^T buffer, rewritten later, holds their gathered rows)
     hipLaunchKernelGGL(k_gather_rows, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, w.flag_list,
@@ -2549,14 +2634,14 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     if ((rc = launch_status())) return rc;
     if (kf)
       hipLaunchKernelGGL(k_exact_train<true>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias,
-                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, w.vp, V_real, tv, w.G, w.Gt);
+                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     else
       hipLaunchKernelGGL(k_exact_train<false>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias,
-                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, w.vp, V_real, tv, w.G, w.Gt);
+                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     if ((rc = launch_status())) return rc;
     hipLaunchKernelGGL(k_exact_fix, dim3((unsigned)(rp / 256)), dim3(256), 0, st, w.counts + b, w.flag_list, y + row0,
                        w.xy + row0, at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, lse_rows + row0,
-                       rp, w.vp, V_real, w.G, w.Gt);
+                       rp, V_real, w.G);
     if ((rc = launch_status())) return rc;
     if (b + 1 < w.nblk) {
       const bool first = b == 0;
@@ -2797,11 +2882,11 @@ int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   // Ht = H^T, K-blocked: element (k, n) at Ht[(n/256)*K*256 + k*256 + n%256], zero for N <= n < Np
   hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, H,
-                     ldh, N, K, w.Ht);
+                     ldh, N, K, w.Ht, nullptr, nullptr, nullptr, 1);
   if ((rc = launch_status())) return rc;
-  // dW[v, k] = sum_n Gt(v, n) Ht(k, n), reduction over the padded n < Np: the kperm order moves indices across
-  // 32-wide groups' halves, and Gt's and Ht's columns N..Np-1 are zero
-  const Operand Aop{w.Gt, 0, V, w.np, w.vp * BLK, 1};
+  // dW[v, k] = sum_n G(n, v) Ht(k, n), G read transposed, reduction over the padded n < Np (G's rows and Ht's
+  // columns N..Np-1 are zero)
+  const Operand Aop{w.G, w.np * BLK, V, w.np, CM_TILE, 2};
   const Operand Bop{w.Ht, BLK, K, w.np, K * BLK, 0};
   return launch_gemm<false>(Aop, Bop, (int)(w.np / BK), V, K, 4, dW, lddw, w.part, st, nullptr, nullptr, nullptr,
                             nullptr, nullptr, nullptr, nullptr, PROF_GEMM_DW);

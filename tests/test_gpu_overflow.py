@@ -1,8 +1,8 @@
 """The overflow branch of the one-pass training path on the GPU: rows whose largest logit lies 100 or more above
 e_n (the lower bound of the lse that k_fwd_train shifts by), so that E = exp(x - e_n) is +inf in fp32 for those
 entries. The design claims (mce.hip, k_fwd_train and store_g_block) that such a row is flagged, that its inf values
-(and the NaNs inf * 0 makes in the selector-MFMA transpose) stay inside its own row of G and G^T, and that the exact
-fallback pass (k_exact_train, an MFMA pass over the gathered flagged rows) rewrites that whole row; every kernel
+stay inside its own row of G, and that the exact fallback pass (k_exact_train, an MFMA pass over the gathered
+flagged rows) rewrites that whole row before the contractions read G (dH directly, dW transposed); every kernel
 exits normally.
 
 Because e_n >= x_y (the target logit is part of the bound), a row with such a gap has py < e^-88, below the 1e-30
