@@ -80,6 +80,10 @@ def _args():
                          "recomputes the logits")
     ap.add_argument("--other-path-steps", type=int, default=3,
                     help="timed steps of the other path, reported beside the line (0: skip)")
+    ap.add_argument("--layout", choices=("biased", "folded"), default="biased",
+                    help="biased: linear_ce_mix_biased(h [N, d], W [V, d], fp32 bias) (default); folded: the "
+                         "caller's own call, linear_ce_mix(hn [B, T, d+16], W' [V, d+16], y [B, T], g [B, T], hit) "
+                         "on the _head_w layout with the bias in column d (full2.py:1842-1851,1860)")
     ap.add_argument("--peaked", type=float, default=0.0,
                     help="fraction of rows given a logit 50-100 above their e_n (the one-pass path's exact fallback); "
                          "reports the rows it rewrote per step")
@@ -469,10 +473,26 @@ def main():
 
     cand, cval = sparse_bias(inp.y.cpu(), inp.c1.cpu(), cfg.v_real)
     cand, cval = cand.to(dev), cval.to(dev).requires_grad_()
+    folded = args.op == "fused_ce" and args.layout == "folded"
+    if folded:
+        # _head_w (full2.py:1842-1851): hn' = [hn, 1, 0 x 15] in bf16, W' = [W, bias, 0 x 15]; the padded ids get
+        # the bias -1e4 in that column (their softmax weight underflows to exactly 0)
+        bf = inp.bias.clone()
+        bf[cfg.v_real:] = -1e4
+        hf = torch.cat([inp.h, torch.ones(n, 1, device=dev), torch.zeros(n, 15, device=dev)], 1).bfloat16()
+        hf = hf.reshape(cfg.texts, cfg.seq, d + 16).detach().requires_grad_()
+        wf = torch.cat([inp.w, bf.bfloat16().float()[:, None], torch.zeros(v, 15, device=dev)], 1)
+        wf = wf.detach().requires_grad_()
+        yf = inp.y.reshape(cfg.texts, cfg.seq)
+        gf = inp.gate.reshape(cfg.texts, cfg.seq).detach().requires_grad_()
+        hitf = inp.hit.reshape(cfg.texts, cfg.seq)
 
     def step():
         h.grad = w.grad = b.grad = gate.grad = cval.grad = None
-        if args.op == "linear_ce":
+        if folded:
+            hf.grad = wf.grad = gf.grad = None
+            loss = fused_ops.linear_ce_mix(hf, wf, yf, gf, hitf)
+        elif args.op == "linear_ce":
             loss = fused_ops.linear_ce(h, w, inp.y)
         elif args.op == "linear_ce_sparse":
             loss = fused_ops.linear_ce_sparse(h, w, inp.y, cand, cval)
@@ -549,9 +569,12 @@ def main():
     stages = {k: sum(x) / args.steps for k, x in live.items()}
     # the contraction kernels, timed by the library's HIP events around each launch on the launch stream: every
     # class present runs one N x V x d contraction per step, over one or several launches (row blocks)
-    nr = fold_nr(d) if (args.op == "fused_ce" and args.path == "one-pass") else 0   # dBias inside the dW tiles
-    kernels = {PROF_KERNELS[c].format(nr=nr): (kern_ms[c], kern_n[c] // args.steps)
-               for c in range(len(PROF_KERNELS)) if kern_n[c] > 0}
+    nr = fold_nr(d) if (args.op == "fused_ce" and args.path == "one-pass" and not folded) else 0  # dBias in dW
+    names = [k.format(nr=nr) for k in PROF_KERNELS]
+    if folded:   # K = d + 16: the logits tiles take the checked-load variant
+        names = [k.replace("<true>", "<false>") if k.startswith(("k_fwd_train", "k_fwd_tiles", "k_bwd_grad")) else k
+                 for k in names]
+    kernels = {names[c]: (kern_ms[c], kern_n[c] // args.steps) for c in range(len(PROF_KERNELS)) if kern_n[c] > 0}
     tok_s = n / dt
     flops = 6.0 * n * v * d
     if args.stage_reps > 0:
@@ -562,7 +585,7 @@ def main():
     kflops = 2.0 * n * v * d / launches                     # per launch: one row block's contraction
     avg_ms = kernels[dom][0] / (args.steps * launches)    # average launch duration
     ach = kflops / (avg_ms * 1e-3)
-    traffic = traffic_bytes(dom, cfg.index) if args.op == "fused_ce" else None
+    traffic = traffic_bytes(dom, cfg.index) if (args.op == "fused_ce" and not folded) else None
     res = {
         "metric": METRIC if args.op == "fused_ce" else f"tokens/s {args.op} fwd+bwd, d={d} V={v}; % bf16 MFMA peak",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -585,6 +608,9 @@ def main():
         # allocated before them (the op's workspace, saved state and gradients), as bench_fused.py:21-30 reports
         "peak_mem_gb": round(mem_peak / 1e9, 4), "step_mem_gb": round((mem_peak - mem_base) / 1e9, 4),
     }
+    if folded:
+        res["config"]["layout"] = ("folded: linear_ce_mix(hn [B, T, d+16], W' [V, d+16], y, g, hit) on the _head_w "
+                                   "layout; K = d + 16, credited 6 N V d")
     if args.peaked > 0:
         res["config"]["peaked_rows"] = args.peaked
         res["fallback_rows_per_step"] = int(flagged.item()) // args.steps if args.path == "one-pass" else None

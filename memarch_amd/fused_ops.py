@@ -49,17 +49,29 @@ def _check_cuda(*ts):
             raise ValueError("memarch_amd.fused_ops runs on the GPU only; got a tensor on " + str(t.device))
 
 
+def _row_stride(kp):
+    """Row stride (elements) of the bf16 operands the logits tiles read: a multiple of 64, so that each 128-byte
+    load segment of a row is one cache line (a stride of K = d + 16 = 2064, the folded-bias layout, splits most
+    segments over two lines and made the logits kernels 20% slower)."""
+    return (kp + 63) // 64 * 64
+
+
 def _bf16_operand(t, kp):
-    """bf16 copy/view of a 2-D operand whose row stride and width are multiples of 8 and whose base is 16-byte
-    aligned, zero-padded to `kp` columns when the width is not a multiple of 8."""
+    """bf16 view of a 2-D operand [R, kp] (zero-padded to kp columns when the width is not a multiple of 8) whose
+    row stride is a multiple of 64 and whose base is 16-byte aligned: the operand itself when it already is one,
+    else a copy with the row stride _row_stride(kp)."""
     t = t.detach()
-    if t.dtype != _BF16:
-        t = t.to(_BF16)
     k = t.shape[1]
-    if k == kp and t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0:
+    if t.dtype == _BF16 and k == kp and t.stride(1) == 1 and t.stride(0) % 64 == 0 and t.data_ptr() % 16 == 0:
         return t
-    out = torch.zeros(t.shape[0], kp, dtype=_BF16, device=t.device)
+    if k == kp and kp % 64 == 0:
+        c = t.to(_BF16).contiguous()   # a contiguous copy already has the row stride
+        if c.data_ptr() % 16 == 0:
+            return c
+    out = torch.empty(t.shape[0], _row_stride(kp), dtype=_BF16, device=t.device)[:, :kp]
     out[:, :k] = t
+    if kp > k:
+        out[:, k:].zero_()
     return out
 
 
@@ -110,7 +122,7 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
             and w.data_ptr() % 16 == 0:
         # the one-pass forward casts the fp32 weight itself, in the pass that also forms its transpose
         w32 = w.detach()
-        wd = torch.empty(v, kp, dtype=_BF16, device=dev)
+        wd = torch.empty(v, _row_stride(kp), dtype=_BF16, device=dev)[:, :kp]
     else:
         wd = _bf16_operand(w, kp)
     y64 = _rows(y, torch.int64)
