@@ -84,6 +84,8 @@ def _args():
                     help="biased: linear_ce_mix_biased(h [N, d], W [V, d], fp32 bias) (default); folded: the "
                          "caller's own call, linear_ce_mix(hn [B, T, d+16], W' [V, d+16], y [B, T], g [B, T], hit) "
                          "on the _head_w layout with the bias in column d (full2.py:1842-1851,1860)")
+    ap.add_argument("--gpu-reference-steps", type=int, default=3,
+                    help="timed steps of the reference's method restated with torch ops on the same GPU (0: skip)")
     ap.add_argument("--peaked", type=float, default=0.0,
                     help="fraction of rows given a logit 50-100 above their e_n (the one-pass path's exact fallback); "
                          "reports the rows it rewrote per step")
@@ -179,6 +181,73 @@ def cpu_baseline(cfg, rows, chunk=4096, op="fused_ce"):
                 sample=f"first {rows} of {cfg.n} rows of config {cfg.index} (d={cfg.d}, V={cfg.v}), fp32 torch eager "
                        f"fwd+bwd in {chunk}-row chunks, {dt:.1f} s on {torch.get_num_threads()} threads "
                        f"(os.cpu_count()={os.cpu_count()}); rows are independent, so tokens/s holds for all N")
+
+
+def gpu_reference_method(inp, v_real, steps, chunk=4096):
+    """The reference's method (fused_ops.py:138-162) on the same GPU and inputs, restated with torch ops: the fp32
+    weight cast to bf16 once per step, then per 4096-row chunk the bf16 logits GEMM (hipBLASLt), the row pass of
+    `_ce_mix_kernel` (fused_ops.py:104-134: lse, py, P, loss, dg, and G = wgt (softmax - onehot) in bf16 over the
+    logits chunk; here torch ops in fp32 with the bias added and padded ids masked, as the fused op's biased form
+    does), gh = G @ W and gw += (G^T @ h).float(), dBias += G.sum(0); the backward's scaling by go. Returns the step
+    time and, as a floor for that method on this GPU, the time of its GEMMs alone (the same chunked matmuls with no
+    row pass), both over `steps` steps after one warm-up step."""
+    h, w, b, y, gate, hit = inp.h, inp.w, inp.bias, inp.y, inp.gate, inp.hit
+    n, d = h.shape
+    v = w.shape[0]
+    bias = b.clone()
+    bias[v_real:] = float("-inf")
+    go = 1.0 / n
+
+    def step():
+        hd, wd = h.to(torch.bfloat16), w.to(torch.bfloat16)
+        gh = torch.empty_like(hd)
+        gw = torch.zeros(v, d, device=h.device, dtype=torch.float32)
+        db = torch.zeros(v, device=h.device, dtype=torch.float32)
+        loss = torch.empty(n, device=h.device, dtype=torch.float32)
+        dg = torch.empty(n, device=h.device, dtype=torch.float32)
+        for i in range(0, n, chunk):
+            hc = hd[i:i + chunk]
+            logits = hc @ wd.T
+            x = logits.float() + bias
+            lse = torch.logsumexp(x, 1)
+            yc = y[i:i + chunk]
+            py = (x.gather(1, yc[:, None])[:, 0] - lse).exp()
+            gc, hic = gate[i:i + chunk], hit[i:i + chunk]
+            P = ((1 - gc) * py + gc * hic).clamp(min=1e-30)
+            loss[i:i + chunk] = -P.log()
+            dg[i:i + chunk] = (py - hic) / P
+            wgt = (1 - gc) * py / P
+            x.sub_(lse[:, None]).exp_()
+            x.scatter_add_(1, yc[:, None], -torch.ones_like(lse)[:, None])
+            x.mul_(wgt[:, None])
+            G = x.to(torch.bfloat16)
+            db += G.float().sum(0)
+            gh[i:i + chunk] = G @ wd
+            gw += (G.T @ hc).float()
+        loss.sum()
+        return (gh * go), (gw * go), (db * go), (dg * go)
+
+    def gemms():
+        hd, wd = h.to(torch.bfloat16), w.to(torch.bfloat16)
+        gw = torch.zeros(v, d, device=h.device, dtype=torch.float32)
+        for i in range(0, n, chunk):
+            hc = hd[i:i + chunk]
+            logits = hc @ wd.T
+            _ = logits @ wd
+            gw += (logits.T @ hc).float()
+
+    out = {}
+    for name, fn in (("ms_per_step", step), ("gemms_only_ms_per_step", gemms)):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        out[name] = round((time.perf_counter() - t0) / steps * 1e3, 3)
+    out["method"] = ("fused_ops.py:138-162 in torch ops: 4096-row chunks, bf16 GEMMs (hipBLASLt), fp32 row pass "
+                     "with materialised logits; gemms_only: the same chunked GEMMs without the row pass")
+    return out
 
 
 def peak_rows(inp, frac, vid=1000, seed=5):
@@ -624,6 +693,11 @@ def main():
         fused_ops.RECOMPUTE = args.path == "recompute"
     if args.stage_reps > 0:
         res["isolated_stages_ms"] = {k: round(x, 3) for k, x in isolated.items()}
+    if args.gpu_reference_steps > 0 and args.op == "fused_ce":
+        print("[bench] the reference's method in torch ops on the GPU", file=sys.stderr, flush=True)
+        h.grad = w.grad = b.grad = gate.grad = None
+        torch.cuda.empty_cache()
+        res["gpu_reference_method"] = gpu_reference_method(inp, cfg.v_real, args.gpu_reference_steps)
     if args.cpu_rows > 0:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_rows, n), op=args.op)
