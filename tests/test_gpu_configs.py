@@ -170,15 +170,18 @@ def test_full_size_config(index):
     compare(cfg, got, ref, f"config {index}")
 
 
-def test_config1_caller_shape_folded_layout():
-    """Config 1 trained through the call exactly as full2.py:1860 makes it, on the _head_w layout: hn' = [hn, 1,
-    0 x 15] as (B, T, d+16), w' = [W, bias in bf16, 0 x 15]; the padded ids get the bias -1e4 in that column (exp
+@pytest.mark.parametrize("index", [1, 2])
+def test_caller_shape_folded_layout(index):
+    """Configs 1 and 2 trained through the call exactly as full2.py:1860 makes it, on the _head_w layout: hn' = [hn,
+    1, 0 x 15] as (B, T, d+16), w' = [W, bias in bf16, 0 x 15]; the padded ids get the bias -1e4 in that column (exp
     underflows to exactly 0), as -inf would make the bias column of dH NaN (0 * -inf). The bias gradient is dW's
-    column d. Checked on every element against the closed form on the same folded operands."""
+    column d. K = d + 16 is not a multiple of 64, so h is copied to a 128-byte-multiple row stride and the logits
+    tiles take the checked-load mainloop with a partial last stage. Checked on every element against the closed form
+    on the same folded operands."""
     from memarch_amd import fused_ops
     from memarch_amd.workloads import CONFIGS, make_inputs
-    cfg = CONFIGS[1]
-    print("config 1, caller shape (B, T, d+16)", flush=True)
+    cfg = CONFIGS[index]
+    print(f"config {index}, caller shape (B, T, d+16)", flush=True)
     inp = make_inputs(cfg)
     B, T, d, V = cfg.texts, cfg.seq, cfg.d, cfg.v
     bias = inp.bias.clone()
@@ -203,4 +206,4 @@ def test_config1_caller_shape_folded_layout():
     got = dict(loss=float(loss.detach()), loss_rows=rows["loss_rows"], lse=rows["lse"],
                dh=h.grad.reshape(-1, d + 16).float(), dw=w.grad, dbias=w.grad[:, d], dgate=gate.grad.reshape(-1))
     ref["dbias"] = ref["dw"][:, d]
-    compare(cfg, got, ref, "config 1 caller shape")
+    compare(cfg, got, ref, f"config {index} caller shape")
