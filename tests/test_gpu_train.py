@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from cases import assert_parity, capi_train, gpu_run, oracle_of, random_case
+from cases import GRAD_RTOL, LOSS_RTOL, assert_parity, capi_train, gpu_run, oracle_of, random_case
+from oracle import mce_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -281,3 +282,40 @@ def test_fp32_weight_cast_in_the_forward():
     assert torch.equal(got, ref)
     for a, c in zip(outs[0][1:], outs[1][1:]):
         assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
+@pytest.mark.parametrize("grads", [("h", "bias"), ("bias",), ("w",), ("h",), ("gate",)],
+                         ids=lambda g: "+".join(g))
+def test_partial_gradient_sets(grads, block_rows, monkeypatch):
+    """Only some inputs require a gradient, as autograd's needs_input_grad reports it: the training forward forms
+    only the contractions asked for (dH + dBias without dW takes dBias from a separate pass over the logits
+    gradient; with dW it comes out of the dW pass; dgate alone asks for none), and the other leaves get no
+    gradient."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", block_rows)
+    case = random_case(700, 384, 3000, 2990, True, seed=53)
+    n = case["h"].shape[0]
+    go = 1.0 / n
+    fwd, bwd = oracle_of(case, go=go)
+    leaves = dict(h=case["h"].cuda().bfloat16(), w=case["w"].cuda(), bias=case["bias"].cuda(),
+                  gate=case["gate"].cuda())
+    for name in grads:
+        leaves[name].requires_grad_()
+    loss = fused_ops.linear_ce_mix_biased(leaves["h"], leaves["w"], leaves["bias"], case["y"].cuda(), leaves["gate"],
+                                          case["hit"].cuda(), v_real=case["v_real"])
+    (loss * go).backward()
+    torch.cuda.synchronize()
+    lerr = abs(float(loss.detach()) - float(fwd["loss_sum"])) / abs(float(fwd["loss_sum"]))
+    errs = dict(loss=lerr)
+    ref = dict(h="dh", w="dw", bias="dbias", gate="dgate")
+    for name, t in leaves.items():
+        if name in grads:
+            assert t.grad is not None, (name, grads)
+            errs[name] = orc.rel_fro(t.grad.float().cpu().numpy(), bwd[ref[name]])
+        else:
+            assert t.grad is None, (name, grads)
+    print(f"partial {grads} block_rows={block_rows}", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert errs["loss"] <= LOSS_RTOL, errs
+    for name in grads:
+        assert errs[name] <= GRAD_RTOL, (name, errs)
