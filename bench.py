@@ -17,6 +17,10 @@ accumulation), with every input resident in HBM before the timed region. Prints 
 `--calibrate-copy` instead times a plain 1 GiB device-to-device copy (the reference kernel for scaling the
 FETCH_SIZE / WRITE_SIZE counters) and prints its size.
 
+`--calibrate-mfma` instead measures the bf16 MFMA rate that the contraction kernels' register tile sustains on this
+board with no global memory traffic (memarch_amd/csrc/probe.hip): from registers only, and with the mainloop's LDS
+fragment reads; the upper bound the contraction kernels' rates are read against.
+
 `--op swiglu` instead measures the SwiGLU gate kernels (memarch fused_ops.py:175-228) on the FFN of the same
 d = 2048 model (rows = N = 32768, H = 4d = 8192, bf16, lm.py:45-50): one line with the forward + backward HBM
 throughput against the 8 TB/s roofline (algorithmic bytes: forward reads gu and writes out, 3 rows x H
@@ -71,6 +75,8 @@ def _args():
     ap.add_argument("--stage-reps", type=int, default=0,
                     help="extra isolated timed repetitions of each C-ABI stage after the timed steps (0: none)")
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
+    ap.add_argument("--calibrate-mfma", action="store_true",
+                    help="time the MFMA-rate probe (register tile without global memory traffic) and exit")
     ap.add_argument("--op", choices=("fused_ce",) + SIBLING_OPS + ("induct", "swiglu"), default="fused_ce",
                     help="fused_ce: the north-star operator (default); linear_ce, linear_ce_sparse, chunk_ce: its "
                          "siblings (fused_ops.py:39-101, full2.py:753-836) on the same inputs; induct: the "
@@ -445,6 +451,48 @@ def calibrate_copy():
                       "launches": 5}), flush=True)
 
 
+def calibrate_mfma():
+    """The bf16 MFMA rate of the contraction kernels' register tile (a 4 x 4 block of 32x32x16 accumulators per wave,
+    random operands) with no global memory traffic, one workgroup of 4 waves per CU: mode 0 with the fragments in
+    registers, mode 1 reading them from LDS as the GEMM mainloop does. A warm-up launch, then 3 timed launches of
+    about 30 ms each per mode, timed with torch events on the stream the probe is launched on."""
+    path = os.path.join(ROOT, "memarch_amd", "libmce_probe.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is missing; build it with `python -m memarch_amd.build`")
+    lib = ctypes.CDLL(path)
+    lib.mce_probe_mfma.restype = ctypes.c_int
+    lib.mce_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    dev = torch.device("cuda", 0)
+    blocks = torch.cuda.get_device_properties(dev).multi_processor_count
+    steps = 100000
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    modes = []
+    for mode, name in ((0, "registers"), (1, "lds fragment reads")):
+        def launch(n):
+            rc = lib.mce_probe_mfma(mode, blocks, n, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st.cuda_stream))
+            if rc:
+                raise RuntimeError(f"mce_probe_mfma returned {rc}")
+        launch(steps // 10)
+        torch.cuda.synchronize()
+        secs = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            launch(steps)
+            e1.record(st)
+            e1.synchronize()
+            secs.append(e0.elapsed_time(e1) * 1e-3)
+        flop = blocks * 4 * steps * 16 * 32768
+        sec = sorted(secs)[1]
+        modes.append({"mode": mode, "operands": name, "ms": round(sec * 1e3, 3),
+                      "tflops": round(flop / sec / 1e12, 1), "frac": round(flop / sec / PEAK_BF16, 4)})
+    assert torch.isfinite(out).all().item()
+    print(json.dumps({"calibration": "bf16 MFMA rate without global memory traffic", "workgroups": blocks,
+                      "steps_per_wave": steps, "flop_per_launch": blocks * 4 * steps * 16 * 32768,
+                      "peak": PEAK_BF16, "modes": modes}), flush=True)
+
+
 def bench_swiglu(args):
     """Forward and backward of the SwiGLU gate at rows = 32768, H = 8192, bf16; each kernel timed with torch events
     on the current stream (the stream the C-ABI calls launch on)."""
@@ -512,6 +560,9 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.calibrate_mfma:
+        calibrate_mfma()
         return
     if args.op == "swiglu":
         bench_swiglu(args)

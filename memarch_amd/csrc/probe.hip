@@ -1,0 +1,146 @@
+// Measurement aid, not part of the operator's C ABI: the bf16 MFMA rate this board sustains with the contraction
+// kernels' register tile and no global memory traffic, as the upper bound their measured rates are read against.
+//
+// Both kernels run the mainloop shape of the contraction kernels in mce.hip on one wave per SIMD (256 threads per
+// workgroup, one workgroup per CU when blocks = 256): a 4 x 4 block of v_mfma_f32_32x32x16_bf16 accumulators per
+// wave (all 256 AGPRs), fed by 4 A and 4 B fragments of random bf16 values (random sign and mantissa, exponents
+// 2^-7 .. 2^-6), so that consecutive MFMAs see different operands, as in a GEMM.
+//   mode 0 (k_probe_regs): the 8 fragments stay in registers; MFMA work only.
+//   mode 1 (k_probe_lds):  every 16 MFMAs read their 8 fragments from LDS with ds_read_b128, the next step's
+//                          fragments issued between this step's MFMAs (the mainloop's LDS read pattern and rate,
+//                          without the global-to-LDS staging and barriers).
+// Each thread writes the sum of its accumulators to out[thread], so the MFMAs are not dead code.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t MANT_SIGN = 0x80FF80FFu, EXP_BASE = 0x3C003C00u;
+
+__device__ __forceinline__ uint32_t xorshift(uint32_t x) {
+  x ^= x << 13;
+  x ^= x >> 17;
+  x ^= x << 5;
+  return x;
+}
+
+__device__ __forceinline__ f32x16 mfma(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+__device__ __forceinline__ void step(f32x16 (&acc)[4][4], const u32x4 (&a)[4], const u32x4 (&b)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
+}
+
+__device__ __forceinline__ void finish(const f32x16 (&acc)[4][4], float* out) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s += acc[i][j][e];
+  out[(int64_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+__global__ __launch_bounds__(256) void k_probe_regs(int steps, float* __restrict__ out) {
+  uint32_t h = ((uint32_t)blockIdx.x * 256u + threadIdx.x) * 2654435761u + 1u;
+  u32x4 a[4], b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h = xorshift(h);
+      a[i][e] = (h & MANT_SIGN) | EXP_BASE;
+      h = xorshift(h);
+      b[i][e] = (h & MANT_SIGN) | EXP_BASE;
+    }
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  for (int s = 0; s < steps; ++s) step(acc, a, b);
+  finish(acc, out);
+}
+
+// 64 KiB of random bf16 pairs in LDS, as 64 fragment lines of 1 KiB (64 lanes x 16 bytes: conflict-free
+// ds_read_b128); step s reads lines (s % 8) * 8 + f (+ 2 per wave), f < 8, all within the buffer
+__global__ __launch_bounds__(256) void k_probe_lds(int steps, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint32_t lds[16384];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  uint32_t h = ((uint32_t)blockIdx.x * 256u + t) * 2654435761u + 1u;
+  for (int i = t; i < 16384; i += 256) {
+    h = xorshift(h);
+    lds[i] = (h & MANT_SIGN) | EXP_BASE;
+  }
+  __syncthreads();
+  const u32x4* line = reinterpret_cast<const u32x4*>(lds);
+  auto at = [&](int s, int f) { return ((((s & 7) * 8 + f + wave * 2) & 63) * 64) + lane; };
+  u32x4 a0[4], b0[4], a1[4], b1[4];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    a0[f] = line[at(0, f)];
+    b0[f] = line[at(0, 4 + f)];
+  }
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  // two steps per iteration with explicit fragment buffers: step s uses one set while the other is read for s + 1;
+  // the scheduling groups place one LDS read after every two MFMAs
+  for (int s = 0; s < steps; s += 2) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      a1[f] = line[at(s + 1, f)];
+      b1[f] = line[at(s + 1, 4 + f)];
+    }
+    step(acc, a0, b0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      a0[f] = line[at(s + 2, f)];
+      b0[f] = line[at(s + 2, 4 + f)];
+    }
+    step(acc, a1, b1);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  }
+  finish(acc, out);
+}
+
+}  // namespace
+
+// mode 0 or 1 (above); blocks workgroups of 256 threads, each wave `steps` x 16 MFMAs (steps even, > 0); out holds
+// blocks * 256 floats. Returns 0, 1 for bad arguments, 2 for a launch error. Work per launch:
+// blocks * 4 waves * steps * 16 MFMAs * 32768 FLOP.
+extern "C" __attribute__((visibility("default"))) int mce_probe_mfma(int mode, int blocks, int steps, float* out,
+                                                                     hipStream_t st) {
+  if (mode < 0 || mode > 1 || blocks < 1 || blocks > 65536 || steps < 2 || steps % 2 || out == nullptr) return 1;
+  if (mode == 0)
+    hipLaunchKernelGGL(k_probe_regs, dim3((unsigned)blocks), dim3(256), 0, st, steps, out);
+  else
+    hipLaunchKernelGGL(k_probe_lds, dim3((unsigned)blocks), dim3(256), 0, st, steps, out);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
