@@ -120,3 +120,60 @@ def test_large_bias_with_partial_row_tile():
     bwd = orc.backward(hh, ww, case["y"].numpy(), None, None, case["bias"].numpy(), None, 1.0, fwd, np.float64)
     bwd = dict(bwd, dgate=np.zeros(300))
     assert_parity(got, fwd, bwd, "large bias")
+
+
+@pytest.mark.parametrize("outputs", ["all_bf16_dh", "all_fp32_dh", "dbias_dgate_only", "dw_only"])
+@pytest.mark.parametrize("shape", [(300, 72, 1000, None, True), (777, 520, 2051, 2000, True),
+                                   (64, 2064, 1024, None, False)], ids=lambda s: "N{}_K{}_V{}".format(*s[:3]))
+def test_capi_two_pass_composite(shape, outputs):
+    """mce_fwd then mce_bwd (the three backward steps in one call) through the C ABI, with go = 1/N, on bf16
+    copies of the operands; outputs not asked for are passed as NULL and must stay untouched."""
+    from memarch_amd import _lib
+    n, k, v, vr, bias = shape
+    print(f"two-pass composite {shape} {outputs}", flush=True)
+    case = random_case(n, k, v, vr, bias, seed=61)
+    go = 1.0 / n
+    fwd, bwd = oracle_of(case, go=go)
+    lib = _lib.load()
+    dev = "cuda"
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    h = case["h"].to(dev, torch.bfloat16).contiguous()
+    w = case["w"].to(dev, torch.bfloat16).contiguous()
+    b = None if case["bias"] is None else case["bias"].to(dev).contiguous()
+    y, gate, hit = (case[x].to(dev).contiguous() for x in ("y", "gate", "hit"))
+    f32 = dict(dtype=torch.float32, device=dev)
+    loss_rows, lse, wgt, dgr = (torch.empty(n, **f32) for _ in range(4))
+    loss_sum = torch.empty((), **f32)
+    st = torch.cuda.current_stream().cuda_stream
+    nf = lib.mce_fwd_ws_bytes(n, k, v)
+    wsf = torch.empty(nf, dtype=torch.uint8, device=dev)
+    _lib.call("mce_fwd", p(h), k, p(w), k, p(b), p(y), p(gate), p(hit), n, k, v, case["v_real"], p(loss_rows), p(lse),
+              p(wgt), p(dgr), p(loss_sum), p(wsf), nf, st)
+    sentinel = 12345.0
+    dh_bf16 = outputs == "all_bf16_dh"
+    dh = dw = dbias = dgate = None
+    if outputs.startswith("all"):
+        dh = torch.full((n, k), sentinel, dtype=torch.bfloat16 if dh_bf16 else torch.float32, device=dev)
+    if outputs.startswith("all") or outputs == "dw_only":
+        dw = torch.full((v, k), sentinel, **f32)
+    if outputs != "dw_only":
+        dbias = torch.full((v,), sentinel, **f32) if b is not None else None
+        dgate = torch.full((n,), sentinel, **f32)
+    go_t = torch.full((), go, **f32)
+    nbw = lib.mce_bwd_ws_bytes(n, k, v)
+    wsb = torch.empty(nbw, dtype=torch.uint8, device=dev)
+    _lib.call("mce_bwd", p(h), k, p(w), k, p(b), p(y), p(lse), p(wgt), p(dgr), p(go_t), n, k, v, case["v_real"],
+              p(dh), int(dh_bf16), k, p(dw), k, p(dbias), p(dgate), p(wsb), nbw, st)
+    torch.cuda.synchronize()
+    lerr = abs(float(loss_sum) - float(fwd["loss_sum"])) / abs(float(fwd["loss_sum"]))
+    errs = dict(loss=lerr)
+    for name, t, ref in (("dh", dh, "dh"), ("dw", dw, "dw"), ("dbias", dbias, "dbias"), ("dgate", dgate, "dgate")):
+        if t is not None:
+            got = t.float().cpu().numpy()
+            assert np.isfinite(got).all() and not (got == sentinel).any(), (name, "unwritten or non-finite")
+            errs[name] = orc.rel_fro(got, bwd[ref])
+    print(f"two-pass composite {shape} {outputs}", {x: f"{e:.2e}" for x, e in errs.items()}, flush=True)
+    assert errs["loss"] <= LOSS_RTOL, errs
+    for name, e in errs.items():
+        if name != "loss":
+            assert e <= GRAD_RTOL, (name, errs)
