@@ -2107,16 +2107,26 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   return w;
 }
 
-int check_common(const void* H, int64_t ldh, const void* W, int64_t ldw, int64_t N, int64_t K, int64_t V,
-                 int64_t V_real) {
-  if (N < 0 || K <= 0 || V <= 0 || V_real <= 0 || V_real > V) return MCE_EINVAL;
-  if ((H == nullptr && N > 0) || W == nullptr) return MCE_EINVAL;
-  if (ldh < K || ldw < K) return MCE_EINVAL;
-  if (K % 8 || ldh % 8 || ldw % 8) return MCE_EALIGN;
-  if (!aligned16(H) || !aligned16(W)) return MCE_EALIGN;
+// H [N, K] with row stride ldh against a vocabulary of V rows: H may be null when N == 0
+int check_hidden(const void* H, int64_t ldh, int64_t N, int64_t K, int64_t V) {
+  if (N < 0 || K <= 0 || V <= 0) return MCE_EINVAL;
+  if ((H == nullptr && N > 0) || ldh < K) return MCE_EINVAL;
+  if (K % 8 || ldh % 8 || !aligned16(H)) return MCE_EALIGN;
   // tile counts fit in int; per-lane buffer offsets (256 rows of a row-major operand) stay below 2^30
   if (cdiv(N, BN) * cdiv(V, BM) > INT32_MAX || cdiv(K, BN) * cdiv(V, BM) > INT32_MAX) return MCE_EINVAL;
-  if ((int64_t)BM * (ldh > ldw ? ldh : ldw) * 2 > (int64_t(1) << 30)) return MCE_EINVAL;
+  if ((int64_t)BM * ldh * 2 > (int64_t(1) << 30)) return MCE_EINVAL;
+  return MCE_OK;
+}
+
+// H as above and W [V, K] with row stride ldw (never null), V_real in [1, V]
+int check_common(const void* H, int64_t ldh, const void* W, int64_t ldw, int64_t N, int64_t K, int64_t V,
+                 int64_t V_real) {
+  if (V_real <= 0 || V_real > V) return MCE_EINVAL;
+  int rc = check_hidden(H, ldh, N, K, V);
+  if (rc) return rc;
+  if (W == nullptr || ldw < K) return MCE_EINVAL;
+  if (ldw % 8 || !aligned16(W)) return MCE_EALIGN;
+  if ((int64_t)BM * ldw * 2 > (int64_t(1) << 30)) return MCE_EINVAL;
   return MCE_OK;
 }
 
@@ -2264,9 +2274,10 @@ int launch_status() {
   return MCE_OK;
 }
 
-int check_sparse(const int64_t* cand, const float* cval, int kc) {
+// cand / cval [N, kc] may be null only when they hold no element (kc == 0 or N == 0)
+int check_sparse(const int64_t* cand, const float* cval, int kc, int64_t N) {
   if (kc < 0 || kc > MAX_KC) return MCE_EINVAL;
-  if (kc > 0 && (cand == nullptr || cval == nullptr)) return MCE_EINVAL;
+  if (kc > 0 && N > 0 && (cand == nullptr || cval == nullptr)) return MCE_EINVAL;
   return MCE_OK;
 }
 
@@ -2336,7 +2347,7 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
              float* dgr_rows, float* loss_sum, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (!rc) rc = check_bias(bias);
-  if (!rc) rc = check_sparse(cand, cval, kc);
+  if (!rc) rc = check_sparse(cand, cval, kc, N);
   if (rc) return rc;
   if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr)) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -2361,10 +2372,10 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
               int64_t V_real, float* dBias, float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (!rc) rc = check_bias(bias);
-  if (!rc) rc = check_sparse(cand, cval, kc);
+  if (!rc) rc = check_sparse(cand, cval, kc, N);
   if (rc) return rc;
   if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
-  if (go == nullptr && ycoef == nullptr) return MCE_EINVAL;
+  if (N > 0 && go == nullptr && ycoef == nullptr) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (N == 0) {
     if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
@@ -2549,7 +2560,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
                    void* ws, size_t ws_bytes, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (!rc) rc = check_bias(bias);
-  if (!rc) rc = check_sparse(cand, cval, kc);
+  if (!rc) rc = check_sparse(cand, cval, kc, N);
   if (!rc && kc > 0 && gate != nullptr) rc = MCE_EINVAL;  // the sparse bias is for plain cross-entropy
   if (rc) return rc;
   if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~7)) return MCE_EINVAL;
@@ -2662,7 +2673,7 @@ int bwd_train_impl(const uint16_t* H, int64_t ldh, const float* go, const float*
                    int64_t V, int64_t block_rows, const void* dH_part, const float* dW_part,
                    const float* dBias_part, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
                    float* dBias, float* dGate, void* ws, size_t ws_bytes, hipStream_t st) {
-  int rc = check_common(H, ldh, H, ldh, N, K, V, V);
+  int rc = check_hidden(H, ldh, N, K, V);
   if (rc) return rc;
   if (block_rows < 0 || (dH && lddh < K) || (dW && lddw < K)) return MCE_EINVAL;
   if ((dH || dW || dBias || dGate) && go == nullptr) return MCE_EINVAL;
@@ -2869,7 +2880,7 @@ int mce_bwd_dhidden(const uint16_t* W, int64_t ldw, int64_t N, int64_t K, int64_
 
 int mce_bwd_dweight(const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_t V, float* dW, int64_t lddw,
                     void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_common(H, ldh, H, ldh, N, K, V, V);
+  int rc = check_hidden(H, ldh, N, K, V);
   if (rc) return rc;
   if (!dW || lddw < K) return MCE_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -2949,7 +2960,7 @@ int mce_bwd_train(const uint16_t* H, int64_t ldh, const float* go, const float* 
 int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
                         const float* wgt_rows, const float* go, int64_t N, int64_t K, int64_t V, int64_t V_real,
                         int64_t block_rows, float* dCval, void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_sparse(cand, cval, kc);
+  int rc = check_sparse(cand, cval, kc, N);
   if (rc) return rc;
   if (N < 0 || K <= 0 || V <= 0 || V_real < 0 || V_real > V || block_rows < 0) return MCE_EINVAL;
   if (N == 0 || kc == 0) return MCE_OK;

@@ -177,3 +177,42 @@ def test_capi_two_pass_composite(shape, outputs):
     for name, e in errs.items():
         if name != "loss":
             assert e <= GRAD_RTOL, (name, errs)
+
+
+@pytest.mark.parametrize("path", ["one_pass", "blocks256", "recompute"])
+def test_empty_batch(path, monkeypatch):
+    """No rows (N = 0, as a [0, K] and as a [B, 0, K] batch): the reference's chunk loop (fused_ops.py:148) runs no
+    iteration, so the loss sum is 0, dW and dBias are zero and the per-row gradients are empty; every surface
+    (linear_ce_mix, linear_ce_mix_biased, linear_ce, linear_ce_sparse, chunk_ce) on each path."""
+    from memarch_amd import fused_ops
+    from memarch_amd.chunk_ce import chunk_ce
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", path == "recompute")
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256 if path == "blocks256" else 0)
+    print(f"empty batch {path}", flush=True)
+    dev = "cuda"
+    K, V = 72, 1000
+    w = (torch.randn(V, K) * 0.05).to(dev).requires_grad_()
+    b = torch.randn(V).to(dev).requires_grad_()
+    for hshape in ((0, K), (2, 0, K)):
+        rows = hshape[:-1]
+        h = torch.randn(hshape).bfloat16().to(dev).requires_grad_()
+        y = torch.zeros(rows, dtype=torch.int64, device=dev)
+        gate = torch.rand(rows).to(dev).requires_grad_()
+        hit = torch.zeros(rows, device=dev)
+        cand = torch.zeros(rows + (2,), dtype=torch.int64, device=dev)
+        cval = torch.zeros(rows + (2,), device=dev).requires_grad_()
+        losses = [fused_ops.linear_ce_mix(h, w, y, gate, hit),
+                  fused_ops.linear_ce_mix_biased(h.reshape(-1, K), w, b, y.reshape(-1), gate.reshape(-1),
+                                                 hit.reshape(-1), v_real=990),
+                  fused_ops.linear_ce(h, w, y),
+                  fused_ops.linear_ce_sparse(h, w, y, cand, cval)]
+        lse, ly = chunk_ce(h.reshape(-1, K), w, b, y.reshape(-1))
+        assert lse.shape == (0,) and ly.shape == (0,)
+        total = sum(losses) + (lse - ly).sum()
+        total.backward()
+        torch.cuda.synchronize()
+        for x in losses:
+            assert float(x.detach()) == 0.0
+        assert h.grad.shape == h.shape and gate.grad.shape == gate.shape and cval.grad.shape == cval.shape
+        assert torch.count_nonzero(w.grad).item() == 0 and torch.count_nonzero(b.grad).item() == 0
+        w.grad = b.grad = None
