@@ -319,3 +319,15 @@ def test_partial_gradient_sets(grads, block_rows, monkeypatch):
     assert errs["loss"] <= LOSS_RTOL, errs
     for name in grads:
         assert errs[name] <= GRAD_RTOL, (name, errs)
+
+
+def test_many_blocks(monkeypatch):
+    """20 row blocks of 256 rows (N = 5000, ragged last block): dW and dBias accumulate their partial sums through 19
+    epilogue additions before the backward's; dH comes from 19 stored partial blocks plus the last."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256)
+    case = random_case(5000, 256, 1500, 1490, True, seed=57)
+    go = 1.0 / 5000
+    got = gpu_run(case, go=go)
+    fwd, bwd = oracle_of(case, go=go)
+    assert_parity(got, fwd, bwd, "20 blocks")
