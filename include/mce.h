@@ -29,6 +29,8 @@
  *     fused_ops.py:39-63,170-172). With the mixture, a target outside [0, V_real) has probability 0 (py = 0).
  *   - cand is int64 [N, kc], cval fp32 [N, kc], 0 <= kc <= 8.
  *   - bias may be NULL (no bias; e.g. the `_head_w` layout of full2.py:1842-1851 that folds the bias into W).
+ *   - N = 0 (an empty batch) is valid: the [N]-sized and [N, *]-sized pointers may then be NULL; the calls write
+ *     loss_sum = 0 and zero dW / dBias where asked, as the reference's chunk loop over no rows leaves them.
  *   - Every call is asynchronous on `stream` (hipStream_t passed as void*); nothing synchronises the host.
  *   - Buffers are caller-owned. The library allocates no device memory: scratch lives in the caller's
  *     workspace `ws` of at least the size returned by the matching *_ws_bytes function (256-byte aligned).
