@@ -69,3 +69,49 @@ def test_single_vocabulary_entry(path, monkeypatch):
         assert np.isfinite(got[x]).all() and float(np.abs(got[x]).max()) <= 1e-6, x
     from oracle import mce_oracle as orc
     assert orc.rel_fro(got["dgate"], bwd["dgate"]) <= 2e-2
+
+
+def _sibling_cases(count, seed):
+    r = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        n = int(r.integers(1, 1537))
+        k = int(8 * r.integers(1, 265))
+        v = int(r.integers(2, 3073))
+        out.append((n, k, v, int(r.integers(1, 9)), float(r.choice([0.5, 2.0, 4.0])), bool(r.random() < 0.5),
+                    str(r.choice(["one_pass", "blocks256", "recompute"])), 2000 + i))
+    return out
+
+
+@pytest.mark.parametrize("case", _sibling_cases(12, 2027), ids=lambda c: "N{}_K{}_V{}_kc{}_s{}_{}".format(*c[:5], c[6]))
+def test_sparse_sweep(case, monkeypatch):
+    """linear_ce_sparse on seeded random shapes: kc random up to 8, candidates with repeats, the target and ignored
+    ids (tests/test_gpu_ce.py's generator), on both paths and in row blocks."""
+    import test_gpu_ce as ce
+    from memarch_amd import fused_ops
+    n, k, v, kc, scale, _, path, seed = case
+    print(f"sparse sweep {case}", flush=True)
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", path == "recompute")
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256 if path == "blocks256" else 0)
+    c = ce._case(n, k, v, kc=kc, seed=seed, v_scale=scale)
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    cval = c["cval"].cuda().requires_grad_()
+    loss = fused_ops.linear_ce_sparse(h, w, c["y"].cuda(), c["cand"].cuda(), cval)
+    go = 1.0 / n
+    (loss * go).backward()
+    torch.cuda.synchronize()
+    fwd, bwd = ce._oracle(c, go=go)
+    ce._check(f"sparse sweep {case}", float(loss.detach()), fwd, dict(dh=h.grad, dw=w.grad, dcval=cval.grad), bwd)
+
+
+@pytest.mark.parametrize("case", _sibling_cases(10, 2028), ids=lambda c: "N{}_K{}_V{}_b{}".format(c[0], c[1], c[2], c[5]))
+def test_chunk_ce_sweep(case):
+    """chunk_ce on seeded random shapes with random upstream gradients (g_lse, g_ly)."""
+    import test_gpu_chunk_ce as cc
+    n, k, v, _, _, bias, _, seed = case
+    print(f"chunk_ce sweep {case}", flush=True)
+    c = cc._case(n, k, v, seed=seed, bias=bias)
+    lse, ly, h, w, b = cc._run(c)
+    fwd, g = cc._oracle(c)
+    cc._check(f"chunk_ce sweep {case}", lse, ly, h, w, b, fwd, g)
