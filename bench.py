@@ -19,7 +19,9 @@ FETCH_SIZE / WRITE_SIZE counters) and prints its size.
 
 `--calibrate-mfma` instead measures the bf16 MFMA rate that the contraction kernels' register tile sustains on this
 board with no global memory traffic (memarch_amd/csrc/probe.hip): from registers only, and with the mainloop's LDS
-fragment reads; the upper bound the contraction kernels' rates are read against.
+fragment reads; the upper bound the contraction kernels' rates are read against. `--calibrate-stream` times a
+streaming copy of 2 GiB (the same probe library, plain and non-temporal accesses): the HBM bandwidth a kernel
+reaches on this board, which the HBM-bound kernels (SwiGLU, the weight cast) are read against.
 
 `--op swiglu` instead measures the SwiGLU gate kernels (memarch fused_ops.py:175-228) on the FFN of the same
 d = 2048 model (rows = N = 32768, H = 4d = 8192, bf16, lm.py:45-50): one line with the forward + backward HBM
@@ -77,6 +79,8 @@ def _args():
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
     ap.add_argument("--calibrate-mfma", action="store_true",
                     help="time the MFMA-rate probe (register tile without global memory traffic) and exit")
+    ap.add_argument("--calibrate-stream", action="store_true",
+                    help="time a 2 GiB streaming copy (plain and non-temporal) and exit")
     ap.add_argument("--op", choices=("fused_ce",) + SIBLING_OPS + ("induct", "swiglu"), default="fused_ce",
                     help="fused_ce: the north-star operator (default); linear_ce, linear_ce_sparse, chunk_ce: its "
                          "siblings (fused_ops.py:39-101, full2.py:753-836) on the same inputs; induct: the "
@@ -451,17 +455,60 @@ def calibrate_copy():
                       "launches": 5}), flush=True)
 
 
-def calibrate_mfma():
-    """The bf16 MFMA rate of the contraction kernels' register tile (a 4 x 4 block of 32x32x16 accumulators per wave,
-    random operands) with no global memory traffic, one workgroup of 4 waves per CU: mode 0 with the fragments in
-    registers, mode 1 reading them from LDS as the GEMM mainloop does. A warm-up launch, then 3 timed launches of
-    about 30 ms each per mode, timed with torch events on the stream the probe is launched on."""
+def _probe_lib():
     path = os.path.join(ROOT, "memarch_amd", "libmce_probe.so")
     if not os.path.exists(path):
         raise SystemExit(f"{path} is missing; build it with `python -m memarch_amd.build`")
     lib = ctypes.CDLL(path)
     lib.mce_probe_mfma.restype = ctypes.c_int
     lib.mce_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mce_probe_copy.restype = ctypes.c_int
+    lib.mce_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_void_p]
+    return lib
+
+
+def calibrate_stream():
+    """A 2 GiB device-to-device copy by the probe kernel (grid-stride, 4 16-byte vectors per thread in flight),
+    plain and non-temporal, over a few grid sizes: a warm-up launch, then 5 timed launches each (median), timed
+    with torch events on the stream the probe is launched on."""
+    lib = _probe_lib()
+    dev = torch.device("cuda", 0)
+    nbytes = 1 << 31
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    st = torch.cuda.current_stream(dev)
+    rows = []
+    for nt in (0, 1):
+        for blocks in (4096, 8192, 32768):
+            def launch():
+                rc = lib.mce_probe_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes // 16,
+                                        blocks, nt, ctypes.c_void_p(st.cuda_stream))
+                if rc:
+                    raise RuntimeError(f"mce_probe_copy returned {rc}")
+            launch()
+            secs = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(st)
+                launch()
+                e1.record(st)
+                e1.synchronize()
+                secs.append(e0.elapsed_time(e1) * 1e-3)
+            sec = sorted(secs)[2]
+            rows.append({"nontemporal": bool(nt), "workgroups": blocks, "ms": round(sec * 1e3, 3),
+                         "GBps": round(2 * nbytes / sec / 1e9, 1), "frac": round(2 * nbytes / sec / PEAK_HBM, 4)})
+    assert torch.equal(src[:1 << 20], dst[:1 << 20])
+    print(json.dumps({"calibration": "streaming copy (read + write bytes)", "bytes_read": nbytes,
+                      "bytes_written": nbytes, "peak": PEAK_HBM, "runs": rows}), flush=True)
+
+
+def calibrate_mfma():
+    """The bf16 MFMA rate of the contraction kernels' register tile (a 4 x 4 block of 32x32x16 accumulators per wave,
+    random operands) with no global memory traffic, one workgroup of 4 waves per CU: mode 0 with the fragments in
+    registers, mode 1 reading them from LDS as the GEMM mainloop does. A warm-up launch, then 3 timed launches of
+    about 30 ms each per mode, timed with torch events on the stream the probe is launched on."""
+    lib = _probe_lib()
     dev = torch.device("cuda", 0)
     blocks = torch.cuda.get_device_properties(dev).multi_processor_count
     steps = 100000
@@ -563,6 +610,9 @@ def main():
         return
     if args.calibrate_mfma:
         calibrate_mfma()
+        return
+    if args.calibrate_stream:
+        calibrate_stream()
         return
     if args.op == "swiglu":
         bench_swiglu(args)

@@ -1,7 +1,8 @@
-// Measurement aid, not part of the operator's C ABI: the bf16 MFMA rate this board sustains with the contraction
-// kernels' register tile and no global memory traffic, as the upper bound their measured rates are read against.
+// Measurement aids, not part of the operator's C ABI: the bf16 MFMA rate this board sustains with the contraction
+// kernels' register tile and no global memory traffic, and the HBM bandwidth a streaming copy reaches, as the upper
+// bounds the kernels' measured rates are read against.
 //
-// Both kernels run the mainloop shape of the contraction kernels in mce.hip on one wave per SIMD (256 threads per
+// The two MFMA kernels run the mainloop shape of the contraction kernels in mce.hip on one wave per SIMD (256 threads per
 // workgroup, one workgroup per CU when blocks = 256): a 4 x 4 block of v_mfma_f32_32x32x16_bf16 accumulators per
 // wave (all 256 AGPRs), fed by 4 A and 4 B fragments of random bf16 values (random sign and mantissa, exponents
 // 2^-7 .. 2^-6), so that consecutive MFMAs see different operands, as in a GEMM.
@@ -10,6 +11,8 @@
 //                          fragments issued between this step's MFMAs (the mainloop's LDS read pattern and rate,
 //                          without the global-to-LDS staging and barriers).
 // Each thread writes the sum of its accumulators to out[thread], so the MFMAs are not dead code.
+// The copy (k_probe_copy) moves n 16-byte vectors with a grid-stride loop, 4 vectors per thread in flight, plain or
+// non-temporal loads and stores.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -130,7 +133,48 @@ __global__ __launch_bounds__(256) void k_probe_lds(int steps, float* __restrict_
   finish(acc, out);
 }
 
+template <bool NT>
+__global__ __launch_bounds__(256) void k_probe_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                   int64_t n) {
+  constexpr int U = 4;
+  const int64_t stride = (int64_t)gridDim.x * 256 * U;
+  for (int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x; base < n; base += stride) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + (int64_t)u * 256;
+      if (i < n) v[u] = NT ? __builtin_nontemporal_load(src + i) : src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + (int64_t)u * 256;
+      if (i < n) {
+        if (NT)
+          __builtin_nontemporal_store(v[u], dst + i);
+        else
+          dst[i] = v[u];
+      }
+    }
+  }
+}
+
 }  // namespace
+
+// dst[0 .. 16 n) = src[0 .. 16 n) (bytes; both 16-byte aligned, not overlapping) with `blocks` workgroups of 256
+// threads; nt != 0: non-temporal accesses. Returns 0, 1 for bad arguments, 2 for a launch error.
+extern "C" __attribute__((visibility("default"))) int mce_probe_copy(const void* src, void* dst, int64_t n, int blocks,
+                                                                     int nt, hipStream_t st) {
+  if (src == nullptr || dst == nullptr || n < 1 || blocks < 1 || blocks > (1 << 20) ||
+      (reinterpret_cast<uintptr_t>(src) & 15) || (reinterpret_cast<uintptr_t>(dst) & 15))
+    return 1;
+  const u32x4* s = reinterpret_cast<const u32x4*>(src);
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  if (nt)
+    hipLaunchKernelGGL(k_probe_copy<true>, dim3((unsigned)blocks), dim3(256), 0, st, s, d, n);
+  else
+    hipLaunchKernelGGL(k_probe_copy<false>, dim3((unsigned)blocks), dim3(256), 0, st, s, d, n);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
 
 // mode 0 or 1 (above); blocks workgroups of 256 threads, each wave `steps` x 16 MFMAs (steps even, > 0); out holds
 // blocks * 256 floats. Returns 0, 1 for bad arguments, 2 for a launch error. Work per launch:

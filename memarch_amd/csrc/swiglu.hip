@@ -5,7 +5,8 @@
 // about bytes in flight, not arithmetic: every thread moves 8 consecutive columns per access (16-byte vector
 // loads and stores for 2-byte types, two of them for fp32), each thread handles UNR such chunks spaced one block
 // apart so that their loads are issued together, and the flat (row, chunk) index is split with one 32-bit division
-// per chunk. A row width that is not a multiple of 8, or a base that is not 16-byte aligned, takes the
+// per chunk. The vector accesses are non-temporal: every byte is touched once, and a streaming copy measured 10%
+// faster that way on MI355X (5.9-6.0 TB/s against 5.4-5.5 with plain accesses). A row width that is not a multiple of 8, or a base that is not 16-byte aligned, takes the
 // one-element-per-lane path of the same kernels.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -15,7 +16,7 @@
 namespace {
 
 constexpr int THREADS = 256;
-constexpr int UNR = 2;                 // chunks per thread
+constexpr int UNR = 4;                 // chunks per thread
 constexpr float LOG2E = 1.4426950408889634f;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -28,7 +29,8 @@ template <int W>
 struct Access<float, W> {
   __device__ static __forceinline__ void load(const float* p, float (&v)[W]) {
     if constexpr (W == 8) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+      const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)),
+                  b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[e] = a[e];
@@ -46,8 +48,8 @@ struct Access<float, W> {
         a[e] = v[e];
         b[e] = v[4 + e];
       }
-      *reinterpret_cast<f32x4*>(p) = a;
-      *reinterpret_cast<f32x4*>(p + 4) = b;
+      __builtin_nontemporal_store(a, reinterpret_cast<f32x4*>(p));
+      __builtin_nontemporal_store(b, reinterpret_cast<f32x4*>(p + 4));
     } else {
       *p = v[0];
     }
@@ -60,7 +62,7 @@ struct Access {
   __device__ static __forceinline__ uint16_t from_f32(float x) { return __builtin_bit_cast(uint16_t, (T)x); }
   __device__ static __forceinline__ void load(const T* p, float (&v)[W]) {
     if constexpr (W == 8) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+      const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[2 * e] = to_f32((uint16_t)(a[e] & 0xFFFFu));
@@ -75,7 +77,7 @@ struct Access {
       u32x4 a;
 #pragma unroll
       for (int e = 0; e < 4; ++e) a[e] = (uint32_t)from_f32(v[2 * e]) | ((uint32_t)from_f32(v[2 * e + 1]) << 16);
-      *reinterpret_cast<u32x4*>(p) = a;
+      __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>(p));
     } else {
       *reinterpret_cast<uint16_t*>(p) = from_f32(v[0]);
     }
