@@ -1563,7 +1563,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
   }
 }
 
-// After the merge: a_n = wgt_n exp(e_n - lse_n), and the target element of E' (both buffers) for unflagged rows,
+// After the merge: a_n = wgt_n exp(e_n - lse_n), and the target element of E' in G for unflagged rows,
 // with a sparse bias also the entries of the row's candidates; flagged rows get a_n = wgt_n and are appended to
 // flag_list for the exact pass (k_gather_rows, k_exact_train, k_exact_fix). Rows N .. Np-1 get a_n = 0.
 __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ y, const float* __restrict__ xy,
