@@ -32,6 +32,8 @@
  *   - N = 0 (an empty batch) is valid: the [N]-sized and [N, *]-sized pointers may then be NULL; the calls write
  *     loss_sum = 0 and zero dW / dBias where asked, as the reference's chunk loop over no rows leaves them.
  *   - Every call is asynchronous on `stream` (hipStream_t passed as void*); nothing synchronises the host.
+ *   - Host threads may call concurrently: the calls share no mutable host state (mce_last_hip_error is per thread)
+ *     and no device memory beyond the caller's buffers, except mce_fwd_noalloc's per-GPU scratch (below).
  *   - Buffers are caller-owned. The library allocates no device memory: scratch lives in the caller's
  *     workspace `ws` of at least the size returned by the matching *_ws_bytes function (256-byte aligned).
  *   - Return value: 0 on success, otherwise an MCE_E* code; mce_error_string() describes it.
@@ -65,7 +67,7 @@ MCE_API int mce_version(void);
 /* Human-readable text for a return code. No counterpart in the reference. */
 MCE_API const char* mce_error_string(int code);
 
-/* The hipError_t of the last failed launch in this process (0 if none). No counterpart in the reference. */
+/* The hipError_t of the calling thread's last failed launch (0 if none). No counterpart in the reference. */
 MCE_API int mce_last_hip_error(void);
 
 /* Workspace bytes needed by mce_fwd for this shape. Replaces the temporaries of fused_ops.py:143-146,150. */

@@ -44,7 +44,7 @@ MCE_SWIGLU_API int mce_swiglu_fwd(const void* gu, int64_t rows, int64_t H, int d
 MCE_SWIGLU_API int mce_swiglu_bwd(const void* gu, const void* go, int go_dtype, int64_t rows, int64_t H, int dtype,
                                   void* dgu, void* stream);
 
-/* The hipError_t of the last failed launch in these entry points (0 if none). No counterpart in the reference,
+/* The hipError_t of the calling thread's last failed launch in these entry points (0 if none). No counterpart in the reference,
  * whose launch errors surface as Python exceptions from Triton. */
 MCE_SWIGLU_API int mce_swiglu_last_hip_error(void);
 

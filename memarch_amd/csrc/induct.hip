@@ -143,7 +143,7 @@ __global__ __launch_bounds__(IND_THREADS_MAX) void k_induct(const int64_t* __res
   }
 }
 
-int g_induct_hip_error = 0;
+thread_local int g_induct_hip_error = 0;  // the calling thread's last failed launch
 
 }  // namespace
 

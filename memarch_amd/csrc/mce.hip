@@ -2041,7 +2041,8 @@ __global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ u
 
 // ---------------------------------------------------------------------------------------------------------
 // Host side: argument checks, workspace layout, launches.
-int g_last_hip_error = 0;
+// The hipError_t of the calling thread's last failed launch (mce_last_hip_error).
+thread_local int g_last_hip_error = 0;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Row groups per tile for the dot products of k_gemm<.., DB> over a grid `tiles_n` tiles wide: the 8 row groups of a
@@ -2490,7 +2491,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   return w;
 }
 
-float g_train_s_max = TRAIN_S_MAX;
+std::atomic<float> g_train_s_max{TRAIN_S_MAX};  // test hook: mce_train_set_threshold
 
 template <typename T>
 inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
@@ -2609,6 +2610,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, cval,
                      w.xc, kc, V_real, N, w.np, w.lse_est, w.flag, w.counts, (int)(2 * w.np / BLK));
   if ((rc = launch_status())) return rc;
+  const float s_max = g_train_s_max.load(std::memory_order_relaxed);
   for (int64_t b = 0; b < w.nblk; ++b) {
     const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
     const int tnb = (int)(rp / BN);
@@ -2617,10 +2619,10 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
       ProfScope prof(PROF_FWD_TRAIN, st);
       if (kf)
         hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est + row0,
-                           rows, rp, V, V_real, tv, tnb, g_train_s_max, w.G, w.part_m, w.part_s, w.flag + row0);
+                           rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s, w.flag + row0);
       else
         hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias,
-                           w.lse_est + row0, rows, rp, V, V_real, tv, tnb, g_train_s_max, w.G, w.part_m, w.part_s,
+                           w.lse_est + row0, rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s,
                            w.flag + row0);
     }
     if ((rc = launch_status())) return rc;
@@ -3016,6 +3018,8 @@ int mce_prof_stop(double* ms, int64_t* launches, int nclass) {
   return rc;
 }
 
-void mce_train_set_threshold(float s_max) { g_train_s_max = s_max > 0.f ? s_max : TRAIN_S_MAX; }
+void mce_train_set_threshold(float s_max) {
+  g_train_s_max.store(s_max > 0.f ? s_max : TRAIN_S_MAX, std::memory_order_relaxed);
+}
 
 }  // extern "C"

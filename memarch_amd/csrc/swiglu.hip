@@ -160,7 +160,7 @@ __global__ __launch_bounds__(THREADS) void k_swiglu_bwd(const T* __restrict__ gu
   }
 }
 
-int g_swiglu_hip_error = 0;
+thread_local int g_swiglu_hip_error = 0;  // the calling thread's last failed launch
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
