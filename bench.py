@@ -13,6 +13,8 @@ accumulation), with every input resident in HBM before the timed region. Prints 
                 logits recompute of the backward earns no credit)
   cpu_baseline  the oracle's torch restatement of the reference eager formula (oracle.mce_oracle.eager_ce_part,
                 fp32 fwd+bwd, materialised logits) on a row sample of the same inputs, on the host cores
+  graph_ms_per_step  the same step captured once in a HIP graph and replayed (the host's launch work and the gaps
+                between kernels taken out); `value` stays the eager step's, the way the drop-in is called
 
 `--calibrate-copy` instead times a plain 1 GiB device-to-device copy (the reference kernel for scaling the
 FETCH_SIZE / WRITE_SIZE counters) and prints its size.
@@ -94,6 +96,8 @@ def _args():
                     help="biased: linear_ce_mix_biased(h [N, d], W [V, d], fp32 bias) (default); folded: the "
                          "caller's own call, linear_ce_mix(hn [B, T, d+16], W' [V, d+16], y [B, T], g [B, T], hit) "
                          "on the _head_w layout with the bias in column d (full2.py:1842-1851,1860)")
+    ap.add_argument("--graph-steps", type=int, default=10,
+                    help="timed replays of the same step captured in a HIP graph, reported beside the line (0: skip)")
     ap.add_argument("--gpu-reference-steps", type=int, default=3,
                     help="timed steps of the reference's method restated with torch ops on the same GPU (0: skip)")
     ap.add_argument("--peaked", type=float, default=0.0,
@@ -441,6 +445,37 @@ def bench_config0(args):
         print("[bench] cpu baseline (config 0 at full size)", file=sys.stderr, flush=True)
         res["cpu_baseline"], res["cpu_loss"] = cpu_forward_config0(cfg)
     print(json.dumps(res), flush=True)
+
+
+def graph_time(step, steps):
+    """The step captured once in a HIP graph (torch.cuda.graph, after two warm-up steps on a side stream) and
+    replayed `steps` times between two synchronisations: ms per replay, the same work as an eager step with the
+    host's launch work and the gaps between kernels taken out. None (and a note on stderr) if capture fails."""
+    try:
+        cur = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        cur.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t) / steps * 1e3
+        del graph
+        torch.cuda.empty_cache()
+        return round(ms, 3)
+    except Exception as e:  # reported, never fatal: the line's own measurement is the eager one
+        print(f"[bench] graph capture failed: {e}", file=sys.stderr, flush=True)
+        return None
 
 
 def calibrate_copy():
@@ -795,6 +830,9 @@ def main():
         fused_ops.RECOMPUTE = args.path == "recompute"
     if args.stage_reps > 0:
         res["isolated_stages_ms"] = {k: round(x, 3) for k, x in isolated.items()}
+    if args.graph_steps > 0 and args.peaked == 0:
+        print("[bench] the same step replayed from a HIP graph", file=sys.stderr, flush=True)
+        res["graph_ms_per_step"] = graph_time(step, args.graph_steps)
     if args.gpu_reference_steps > 0 and args.op == "fused_ce":
         print("[bench] the reference's method in torch ops on the GPU", file=sys.stderr, flush=True)
         h.grad = w.grad = b.grad = gate.grad = None
