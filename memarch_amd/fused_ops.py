@@ -378,3 +378,13 @@ def linear_ce_mix_biased(h, w, bias, y, gate, hit, v_real=None, chunk=4096):
     del chunk
     return _LinearCEMixBiased.apply(h.reshape(-1, h.shape[-1]), w, bias, y.reshape(-1), _flat(gate), _flat(hit),
                                     v_real)
+
+
+def __getattr__(name):
+    """`swiglu` / `_SwiGLU` (memarch_amd.swiglu) through this module too, as the reference's fused_ops.py:201-228
+    defines them beside the cross-entropy ops; resolved on first use because memarch_amd.swiglu imports this
+    module."""
+    if name in ("swiglu", "_SwiGLU"):
+        from . import swiglu as _swiglu
+        return getattr(_swiglu, name)
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

@@ -110,3 +110,16 @@ def test_swiglu_c_abi_argument_checks_need_no_gpu():
     assert lib.mce_swiglu_bwd(p, p, 7, 4, 8, 1, p, None) == 1    # unknown upstream type
     assert lib.mce_swiglu_bwd(p, None, 1, 4, 8, 1, p, None) == 1
     assert lib.mce_swiglu_bwd(None, None, 1, 4, 0, 1, None, None) == 0
+
+
+def test_reference_module_surface():
+    """Every name the reference's fused_ops.py defines for callers (fused_ops.py:39,66,99,137,166,170,201,226) is
+    importable from memarch_amd.fused_ops, so a caller can switch the module import and nothing else."""
+    import importlib
+    mod = importlib.import_module("memarch_amd.fused_ops")
+    for name in ("_LinearCE", "_LinearCESparse", "linear_ce_sparse", "_LinearCEMix", "linear_ce_mix", "linear_ce",
+                 "_SwiGLU", "swiglu"):
+        assert callable(getattr(mod, name)), name
+    from memarch_amd.fused_ops import swiglu, _SwiGLU  # noqa: F401
+    from memarch_amd import swiglu as sw
+    assert mod.swiglu is sw.swiglu and mod._SwiGLU is sw._SwiGLU
