@@ -115,3 +115,21 @@ def test_chunk_ce_sweep(case):
     lse, ly, h, w, b = cc._run(c)
     fwd, g = cc._oracle(c)
     cc._check(f"chunk_ce sweep {case}", lse, ly, h, w, b, fwd, g)
+
+
+@pytest.mark.parametrize("case", [(300, 4096, 3000, 2990, "one_pass"), (520, 4096, 1300, None, "blocks256"),
+                                  (300, 8192, 2100, 2050, "one_pass"), (260, 8192, 700, None, "recompute")],
+                         ids=lambda c: "N{}_K{}_V{}_vr{}_{}".format(*c))
+def test_large_hidden(case, monkeypatch):
+    """Hidden sizes of larger models (d = 4096, 8192): 16 and 32 dW tile columns (only the first 8 of which form
+    dBias partials), 64 and 128 K stages per logits tile."""
+    from memarch_amd import fused_ops
+    n, k, v, vr, path = case
+    print(f"large hidden {case}", flush=True)
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", path == "recompute")
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256 if path == "blocks256" else 0)
+    c = random_case(n, k, v, vr, True, seed=k + n, w_scale=0.02)
+    go = 1.0 / n
+    got = gpu_run(c, go=go)
+    fwd, bwd = oracle_of(c, go=go)
+    assert_parity(got, fwd, bwd, f"large hidden {case}")
