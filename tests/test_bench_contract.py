@@ -1,4 +1,4 @@
-"""bench.py's bookkeeping, on the CPU: the dominant kernel of every stage at config 2 has a traffic line in the
+"""bench.py's bookkeeping, on the CPU: its command-line contract (one GPU only, the headline run by default); the dominant kernel of every stage at config 2 has a traffic line in the
 committed rocprofv3 summary (so the bench line's roofline.traffic is measured, not null), and the dW kernel's name
 follows the library's row-group count (the last template argument of k_gemm, fold_nr in mce.hip)."""
 import os
@@ -28,3 +28,25 @@ def test_traffic_lines_cover_config2_kernels():
         for nr in {bench.fold_nr(2048), 0} if "{nr}" in kern else {0}:
             name = kern.format(nr=nr)
             assert bench.traffic_bytes(name, 2) is not None, name
+
+
+def test_more_than_one_gpu_is_refused():
+    """`bench.py --gpus N` with N > 1 exits with status 2 and says why, before it touches a GPU."""
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 2, (r.returncode, r.stderr[-500:])
+    assert "one GPU" in r.stderr and r.stdout.strip() == ""
+
+
+def test_defaults_are_the_headline_run():
+    """With no flags the bench runs the headline workload on one GPU: config 2, 10 timed steps after 3 warm-up
+    steps, the one-pass path of the fused op with the biased layout."""
+    old = sys.argv
+    try:
+        sys.argv = ["bench.py"]
+        a = bench._args()
+    finally:
+        sys.argv = old
+    assert (a.gpus, a.steps, a.warmup, a.config, a.op, a.path, a.layout) == (1, 10, 3, 2, "fused_ce", "one-pass",
+                                                                            "biased")
