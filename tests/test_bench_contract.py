@@ -1,6 +1,7 @@
-"""bench.py's bookkeeping, on the CPU: its command-line contract (one GPU only, the headline run by default); the dominant kernel of every stage at config 2 has a traffic line in the
-committed rocprofv3 summary (so the bench line's roofline.traffic is measured, not null), and the dW kernel's name
-follows the library's row-group count (the last template argument of k_gemm, fold_nr in mce.hip)."""
+"""bench.py's bookkeeping, on the CPU: its command-line contract (one GPU only, the headline run by default); the
+dominant kernel of every stage at config 2 has a traffic line in the committed rocprofv3 summary (so the bench
+line's roofline.traffic is measured, not null); and the dW kernel's name follows the library's row-group count (the
+last template argument of k_gemm, fold_nr in mce.hip)."""
 import os
 import sys
 
