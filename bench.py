@@ -541,16 +541,18 @@ def calibrate_stream():
 def calibrate_mfma():
     """The bf16 MFMA rate of the contraction kernels' register tile (a 4 x 4 block of 32x32x16 accumulators per wave,
     random operands) with no global memory traffic, one workgroup of 4 waves per CU: mode 0 with the fragments in
-    registers, mode 1 reading them from LDS as the GEMM mainloop does. A warm-up launch, then 3 timed launches of
+    registers, mode 1 reading them from LDS as the GEMM mainloop does; mode 2 the tile of a two-waves-per-SIMD design
+    (4 x 2 blocks per wave, 8 waves per workgroup) reading from LDS. A warm-up launch, then 3 timed launches of
     about 30 ms each per mode, timed with torch events on the stream the probe is launched on."""
     lib = _probe_lib()
     dev = torch.device("cuda", 0)
     blocks = torch.cuda.get_device_properties(dev).multi_processor_count
     steps = 100000
-    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    out = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
     st = torch.cuda.current_stream(dev)
     modes = []
-    for mode, name in ((0, "registers"), (1, "lds fragment reads")):
+    for mode, name in ((0, "registers"), (1, "lds fragment reads"),
+                       (2, "lds fragment reads, 4x2 blocks per wave, two waves per SIMD")):
         def launch(n):
             rc = lib.mce_probe_mfma(mode, blocks, n, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st.cuda_stream))
             if rc:

@@ -10,6 +10,9 @@
 //   mode 1 (k_probe_lds):  every 16 MFMAs read their 8 fragments from LDS with ds_read_b128, the next step's
 //                          fragments issued between this step's MFMAs (the mainloop's LDS read pattern and rate,
 //                          without the global-to-LDS staging and barriers).
+//   mode 2 (k_probe_lds2w): the tile of a two-waves-per-SIMD design: 4 x 2 accumulator blocks per wave (128
+//                          AGPRs), 6 fragments read from LDS per 8 MFMAs, 8 waves per workgroup (512 threads), the
+//                          same MFMA work per launch as modes 0 and 1.
 // Each thread writes the sum of its accumulators to out[thread], so the MFMAs are not dead code.
 // The copy (k_probe_copy) moves n 16-byte vectors with a grid-stride loop, 4 vectors per thread in flight, plain or
 // non-temporal loads and stores.
@@ -133,6 +136,71 @@ __global__ __launch_bounds__(256) void k_probe_lds(int steps, float* __restrict_
   finish(acc, out);
 }
 
+
+// mode 2: 4 x 2 accumulator blocks per wave, 8 waves per workgroup, the fragments as in k_probe_lds
+__global__ __launch_bounds__(512) void k_probe_lds2w(int steps, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint32_t lds[16384];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  uint32_t h = ((uint32_t)blockIdx.x * 512u + t) * 2654435761u + 1u;
+  for (int i = t; i < 16384; i += 512) {
+    h = xorshift(h);
+    lds[i] = (h & MANT_SIGN) | EXP_BASE;
+  }
+  __syncthreads();
+  const u32x4* line = reinterpret_cast<const u32x4*>(lds);
+  auto at = [&](int s, int f) { return ((((s & 7) * 8 + f + wave * 2) & 63) * 64) + lane; };
+  u32x4 a0[4], b0[2], a1[4], b1[2];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) a0[f] = line[at(0, f)];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) b0[f] = line[at(0, 4 + f)];
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  for (int s = 0; s < steps; s += 2) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) a1[f] = line[at(s + 1, f)];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) b1[f] = line[at(s + 1, 4 + f)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma(a0[i], b0[j], acc[i][j]);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) a0[f] = line[at(s + 2, f)];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) b0[f] = line[at(s + 2, 4 + f)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma(a1[i], b1[j], acc[i][j]);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum += acc[i][j][e];
+  out[(int64_t)blockIdx.x * 512 + t] = sum;
+}
+
 template <bool NT>
 __global__ __launch_bounds__(256) void k_probe_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
                                                    int64_t n) {
@@ -176,15 +244,17 @@ extern "C" __attribute__((visibility("default"))) int mce_probe_copy(const void*
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// mode 0 or 1 (above); blocks workgroups of 256 threads, each wave `steps` x 16 MFMAs (steps even, > 0); out holds
-// blocks * 256 floats. Returns 0, 1 for bad arguments, 2 for a launch error. Work per launch:
-// blocks * 4 waves * steps * 16 MFMAs * 32768 FLOP.
+// mode 0, 1 or 2 (above); blocks workgroups of 256 threads (mode 2: 512), each wave `steps` x 16 MFMAs (mode 2:
+// x 8; steps even, > 0); out holds blocks * 256 floats (mode 2: blocks * 512). Returns 0, 1 for bad arguments, 2 for
+// a launch error. Work per launch, every mode: blocks * 4 * steps * 16 * 32768 FLOP.
 extern "C" __attribute__((visibility("default"))) int mce_probe_mfma(int mode, int blocks, int steps, float* out,
                                                                      hipStream_t st) {
-  if (mode < 0 || mode > 1 || blocks < 1 || blocks > 65536 || steps < 2 || steps % 2 || out == nullptr) return 1;
+  if (mode < 0 || mode > 2 || blocks < 1 || blocks > 65536 || steps < 2 || steps % 2 || out == nullptr) return 1;
   if (mode == 0)
     hipLaunchKernelGGL(k_probe_regs, dim3((unsigned)blocks), dim3(256), 0, st, steps, out);
-  else
+  else if (mode == 1)
     hipLaunchKernelGGL(k_probe_lds, dim3((unsigned)blocks), dim3(256), 0, st, steps, out);
+  else
+    hipLaunchKernelGGL(k_probe_lds2w, dim3((unsigned)blocks), dim3(512), 0, st, steps, out);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }

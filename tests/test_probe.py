@@ -1,6 +1,6 @@
 """The measurement probes behind `bench.py --calibrate-mfma` and `--calibrate-stream` (memarch_amd/csrc/probe.hip,
 libmce_probe.so): they load, reject bad arguments on the host (before any HIP call, so no GPU is needed), and on the
-GPU the MFMA probe's two modes produce the accumulator sums their operands determine (the same finite values on two
+GPU the MFMA probe's three modes produce the accumulator sums their operands determine (the same finite values on two
 launches) and the copy copies, plain and non-temporal, with a ragged length."""
 import ctypes
 import os
@@ -27,7 +27,7 @@ def probe():
 
 def test_rejects_bad_arguments(probe):
     out = ctypes.c_void_p(16)  # never dereferenced: every call below fails its host check first
-    for mode, blocks, steps, ptr in ((2, 4, 2, out), (-1, 4, 2, out), (0, 0, 2, out), (0, 65537, 2, out),
+    for mode, blocks, steps, ptr in ((3, 4, 2, out), (-1, 4, 2, out), (0, 0, 2, out), (0, 65537, 2, out),
                                      (0, 4, 0, out), (1, 4, 3, out), (0, 4, 2, None)):
         assert probe.mce_probe_mfma(mode, blocks, steps, ptr, None) == 1, (mode, blocks, steps)
     a, b = ctypes.c_void_p(16), ctypes.c_void_p(32)
@@ -37,18 +37,19 @@ def test_rejects_bad_arguments(probe):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 def test_probe_runs(probe, mode):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     print(f"probe mode {mode}", flush=True)
-    out = torch.full((8 * 256,), float("nan"), device="cuda")
+    out = torch.full((8 * 512,), float("nan"), device="cuda")
     st = torch.cuda.current_stream().cuda_stream
+    n = 8 * (512 if mode == 2 else 256)  # one value per thread
     got = []
     for _ in range(2):
         assert probe.mce_probe_mfma(mode, 8, 64, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st)) == 0
         torch.cuda.synchronize()
-        got.append(out.clone().cpu())
+        got.append(out[:n].clone().cpu())
         out.fill_(float("nan"))
     assert torch.isfinite(got[0]).all()
     assert torch.equal(got[0], got[1])
