@@ -216,3 +216,30 @@ def test_empty_batch(path, monkeypatch):
         assert h.grad.shape == h.shape and gate.grad.shape == gate.shape and cval.grad.shape == cval.shape
         assert torch.count_nonzero(w.grad).item() == 0 and torch.count_nonzero(b.grad).item() == 0
         w.grad = b.grad = None
+
+
+@pytest.mark.parametrize("path", ["one_pass", "recompute"])
+def test_mixed_input_dtypes(path, monkeypatch):
+    """h in fp16, W in bf16, gate and hit in bf16: every gradient comes back in its input's dtype, as the
+    reference's backward returns them (fused_ops.py:155,161), and matches the oracle on the same rounded values."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", path == "recompute")
+    print(f"mixed dtypes {path}", flush=True)
+    c = random_case(500, 264, 1200, None, False, seed=71)
+    c["h"] = c["h"].half().float()          # the values the op sees (it rounds fp16 h to bf16 like fp32 h)
+    c["w"] = c["w"].bfloat16().float()
+    c["gate"] = c["gate"].bfloat16().float()
+    h = c["h"].cuda().half().requires_grad_()
+    w = c["w"].cuda().bfloat16().requires_grad_()
+    g = c["gate"].cuda().bfloat16().requires_grad_()
+    hit = c["hit"].cuda().bfloat16()
+    loss = fused_ops.linear_ce_mix(h, w, c["y"].cuda(), g, hit)
+    go = 1.0 / 500
+    (loss * go).backward()
+    torch.cuda.synchronize()
+    assert (h.grad.dtype, w.grad.dtype, g.grad.dtype, loss.dtype) == (torch.float16, torch.bfloat16, torch.bfloat16,
+                                                                      torch.float32)
+    fwd, bwd = oracle_of(c, go=go)
+    got = dict(loss=float(loss.detach()), dh=h.grad.float().cpu().numpy(), dw=w.grad.float().cpu().numpy(),
+               dgate=g.grad.float().cpu().numpy())
+    assert_parity(got, fwd, bwd, f"mixed dtypes {path}")
