@@ -5,6 +5,8 @@ a failure names a shape that fails every time.
 
 Bar (north star): loss within 1e-3 relative, dH / dW / dBias / dGate within 2e-2 relative Frobenius.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -150,3 +152,134 @@ def test_large_vocabulary(path, monkeypatch):
     got = gpu_run(c, go=go)
     fwd, bwd = oracle_of(c, go=go)
     assert_parity(got, fwd, bwd, f"large vocabulary {path}")
+
+
+def _wide_cases(count, seed=7):
+    """Seeded cases over every path and regime: N 1-2999 (and the 256 edges), K any multiple of 8 up to 2112 (and
+    8, 2064), V 2-5999 (and the 256 edges), v_real in [2, V], logit scales from flat (W ~ N(0, 0.05^2)) to peaked
+    (0.5: exact-pass rows), gates mixed / zero / 0.999, targets uniform or in the first 8 ids. N * V * K <= 4e9."""
+    r = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        n = int(r.choice([1, 2, 255, 256, 257, 511, 513]) if r.random() < 0.2 else r.integers(1, 3000))
+        k = int(r.choice([8, 16, 56, 64, 72, 2064, 1040]) if r.random() < 0.2 else 8 * r.integers(1, 265))
+        v = int(r.choice([2, 255, 256, 257, 511, 512, 513, 767]) if r.random() < 0.2 else r.integers(2, 6000))
+        if n * v * k > 4e9:
+            continue
+        vr = int(r.integers(2, v + 1)) if r.random() < 0.4 else None
+        bias = bool(r.random() < 0.7) or vr is not None
+        path = str(r.choice(["one_pass", "blocks256", "blocks512", "blocks768", "recompute"]))
+        h32 = bool(r.random() < 0.25)
+        ws = float(r.choice([0.05, 0.05, 0.2, 0.5]))
+        gm = str(r.choice(["mixed", "mixed", "zero", "one"]))
+        ym = str(r.choice(["uniform", "uniform", "small"]))
+        out.append((n, k, v, vr, bias, path, h32, ws, gm, ym, 50000 + len(out)))
+    return out
+
+
+def _fp32_floors(c, fwd, go):
+    """Absolute error terms that fp32 itself puts on each output, from the one quantity a relative bar cannot see:
+    the difference x_y - lse_n of two fp32 numbers of size |lse_n|, whose error is a few ulps of |lse_n| (taken as
+    8 * 2^-23 * max(1, |lse_n|) = delta_n) however small the difference. It shifts row n's loss by up to delta_n and
+    the target entry of G's row, go * wgt_n * (p_y - 1), by up to e_n = go * wgt_n * delta_n: in dH by e_n |W_y|, in
+    dW by e_n |h_n|, in dBias by e_n, and dGate = go (p_y - hit) / P by about 2 go delta_n p_y / P. These terms are
+    about 1e-5 of the gradient of an ordinary row; they matter only where p_y is within about 1e-4 of 1, where
+    G's target entry is itself that small. torch's fp32 eager formula computes p_y = exp(x_y - lse) the same way."""
+    lse = np.asarray(fwd["lse"], np.float64)
+    wgt = np.asarray(fwd["wgt"], np.float64)
+    py = np.asarray(fwd["py"], np.float64)
+    P = np.asarray(fwd["P"], np.float64)
+    delta = 8.0 * 2.0 ** -23 * np.maximum(1.0, np.abs(lse))
+    e = go * wgt * delta
+    wy = np.linalg.norm(c["w"].double().numpy()[c["y"].numpy()], axis=1)
+    hn = np.linalg.norm(c["h"].double().numpy(), axis=1)
+    dg = np.where(P >= 1e-30, 2.0 * go * delta * py / np.maximum(P, 1e-30), 0.0)
+    return dict(loss=float(delta.sum()), dh=float(np.sqrt(((e * wy) ** 2).sum())), dw=float((e * hn).sum()),
+                dbias=float(e.sum()), dgate=float(np.sqrt((dg ** 2).sum())))
+
+
+def _wide_check(case):
+    """The bar plus the fp32 terms of _fp32_floors: loss within 1e-3 relative + floor, each gradient within 2e-2
+    relative Frobenius + floor + 1e-30 (a gradient whose oracle norm is below fp32's normal range, 1.2e-38, e.g.
+    a row with wgt = 1e-41, comes out as 0)."""
+    from memarch_amd import fused_ops
+    n, k, v, vr, bias, path, h32, ws, gm, ym, seed = case
+    fused_ops.RECOMPUTE = path == "recompute"
+    fused_ops.BLOCK_ROWS = {"blocks256": 256, "blocks512": 512, "blocks768": 768}.get(path, 0)
+    c = random_case(n, k, v, vr, bias, seed=seed, w_scale=ws, gate_mode=gm, y_mode=ym)
+    go = 1.0 / n
+    got = gpu_run(c, go=go, h_dtype=torch.float32 if h32 else torch.bfloat16)
+    fwd, bwd = oracle_of(c, go=go)
+    fl = _fp32_floors(c, fwd, go)
+    lref = float(fwd["loss_sum"])
+    assert abs(got["loss"] - lref) <= 1e-3 * abs(lref) + fl["loss"], ("loss", got["loss"], lref, fl["loss"])
+    for x in ("dh", "dw", "dgate", "dbias"):
+        if got.get(x) is None:
+            continue
+        ref = np.linalg.norm(bwd[x])
+        err = np.linalg.norm(np.asarray(got[x], np.float64) - bwd[x])
+        assert np.isfinite(got[x]).all() and err <= 2e-2 * ref + fl[x] + 1e-30, (x, err, ref, fl[x])
+
+
+def test_wide_sweep():
+    """Many seeded cases in one test (MEMARCH_AMD_WIDE_SWEEP cases, default 400; 2800 ran clean with the sibling
+    sweeps below at 400 each), every failure collected before the assertion. Each case's line is printed before
+    it runs."""
+    from memarch_amd import fused_ops
+    count = int(os.environ.get("MEMARCH_AMD_WIDE_SWEEP", "400"))
+    saved = fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS
+    fails = []
+    try:
+        for case in _wide_cases(count):
+            print(f"wide sweep {case}", flush=True)
+            try:
+                _wide_check(case)
+            except AssertionError as e:
+                fails.append((case, str(e)[:300]))
+    finally:
+        fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS = saved
+    assert not fails, fails[:10]
+
+
+def test_wide_sibling_sweeps():
+    """linear_ce_sparse and chunk_ce over MEMARCH_AMD_WIDE_SWEEP_SIBLINGS seeded cases each (default 60; 400 each
+    ran clean), the generators and bars of test_sparse_sweep / test_chunk_ce_sweep."""
+    import test_gpu_ce as ce
+    import test_gpu_chunk_ce as cc
+    from memarch_amd import fused_ops
+    count = int(os.environ.get("MEMARCH_AMD_WIDE_SWEEP_SIBLINGS", "60"))
+    saved = fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS
+    fails = []
+    try:
+        for case in _sibling_cases(count, 8):
+            n, k, v, kc, scale, _, path, seed = case
+            print(f"wide sparse {case}", flush=True)
+            fused_ops.RECOMPUTE = path == "recompute"
+            fused_ops.BLOCK_ROWS = 256 if path == "blocks256" else 0
+            try:
+                c = ce._case(n, k, v, kc=kc, seed=seed, v_scale=scale)
+                h = c["h"].cuda().bfloat16().requires_grad_()
+                w = c["w"].cuda().requires_grad_()
+                cval = c["cval"].cuda().requires_grad_()
+                loss = fused_ops.linear_ce_sparse(h, w, c["y"].cuda(), c["cand"].cuda(), cval)
+                (loss / n).backward()
+                torch.cuda.synchronize()
+                fwd, bwd = ce._oracle(c, go=1.0 / n)
+                ce._check(f"wide sparse {case}", float(loss.detach()), fwd,
+                          dict(dh=h.grad, dw=w.grad, dcval=cval.grad), bwd)
+            except AssertionError as e:
+                fails.append((case, str(e)[:300]))
+        fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS = saved
+        for case in _sibling_cases(count, 9):
+            n, k, v, _, _, bias, _, seed = case
+            print(f"wide chunk_ce {case}", flush=True)
+            try:
+                c = cc._case(n, k, v, seed=seed, bias=bias)
+                lse, ly, h, w, b = cc._run(c)
+                fwd, g = cc._oracle(c)
+                cc._check(f"wide chunk_ce {case}", lse, ly, h, w, b, fwd, g)
+            except AssertionError as e:
+                fails.append((case, str(e)[:300]))
+    finally:
+        fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS = saved
+    assert not fails, fails[:10]
