@@ -103,6 +103,9 @@ def _args():
     ap.add_argument("--peaked", type=float, default=0.0,
                     help="fraction of rows given a logit 50-100 above their e_n (the one-pass path's exact fallback); "
                          "reports the rows it rewrote per step")
+    ap.add_argument("--induct-len", type=int, default=0,
+                    help="--op induct: tokens per text (0: the configuration's own; above 8192 the long-text path, "
+                         "mce_induct_ws), same text count and distributions")
     return ap.parse_args()
 
 
@@ -317,13 +320,16 @@ def cpu_baseline_sibling(cfg, inp, rows, chunk, op, eager_ce_part, eager_ce_spar
 
 def bench_induct(args):
     """The keys-and-locks producer (`_induct_raw`, full2.py:1499-1535; locks = 3, the longest firing lock kept)
-    on the token texts of the configuration (config 2: 32 texts x 1024 tokens), timed with torch events on the
-    current stream. It is a per-text sort in LDS: the HBM roofline is reported for its algorithmic bytes
-    (x in, cand / on / bk out: 8 + 24 + 3 + 8 bytes per token), not as its bound."""
+    on the token texts of the configuration (config 2: 32 texts x 1024 tokens; --induct-len T: 32 texts of T tokens
+    drawn the same way, e.g. the 16384 of pg19_needle.py:177), timed with torch events on the current stream. It is
+    a per-text sort in LDS (above 8192 tokens, over a workspace with LDS chunk rounds): the HBM roofline is reported
+    for its algorithmic bytes (x in, cand / on / bk out: 8 + 24 + 3 + 8 bytes per token), not as its bound."""
     from memarch_amd import _lib, induct
-    from memarch_amd.workloads import CONFIGS, token_stream
+    from memarch_amd.workloads import CONFIGS, scaled, token_stream
     from oracle.induct_oracle import sorted_scan
     cfg = CONFIGS[args.config]
+    if args.induct_len > 0:
+        cfg = scaled(cfg, seq=args.induct_len)
     dev = torch.device("cuda", 0)
     x_np = token_stream(cfg)[:, :-1]
     x = torch.from_numpy(x_np.copy()).to(dev)
@@ -346,10 +352,12 @@ def bench_induct(args):
         "data": f"synthetic (seeded config {cfg.index} token texts)",
         "config": {"workload": f"_induct_raw on config {cfg.index}'s texts", "texts": int(x.shape[0]),
                    "seq": int(x.shape[1]), "locks": 3},
-        "roofline": {"bound": "hbm", "kernel": "k_induct", "achieved": round(nbytes / dt / 1e9, 2),
+        "roofline": {"bound": "hbm", "kernel": "k_induct" if x.shape[1] <= 8192 else "k_induct_long",
+                     "achieved": round(nbytes / dt / 1e9, 2),
                      "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(nbytes / dt / PEAK_HBM, 6),
                      "bytes_per_launch": nbytes, "traffic": None,
-                     "note": "LDS sort bound: one workgroup per text"},
+                     "note": "LDS sort bound: one workgroup per text" if x.shape[1] <= 8192 else
+                             "sort bound: one workgroup per text, wide stages over its workspace in L2"},
     }
     if args.cpu_rows > 0:
         # all texts of the configuration, repeated until about 2 s of CPU work have been timed

@@ -13,7 +13,8 @@
  *   c1[b,t]     = sum_k cand*on, or c1_none when no lock is on (the reference uses 0, full2.py:1563)
  * Conventions: x is int64 [B, T] row-major with token ids in [-2^50, 2^50); outputs are int64 (cand, src [B,T,locks];
  * bk, c1 [B,T]) or uint8 0/1 (on [B,T,locks], the layout of a torch.bool tensor); any output may be NULL to skip it.
- * T <= mce_induct_max_len() (8192). The call is asynchronous on `stream` and allocates nothing.
+ * mce_induct takes T <= mce_induct_max_len() (8192, a text held in LDS); mce_induct_ws takes T up to 2^24 on a
+ * caller-sized workspace (mce_induct_ws_bytes). Every call is asynchronous on `stream` and allocates nothing.
  */
 #ifndef MCE_INDUCT_H
 #define MCE_INDUCT_H
@@ -43,6 +44,20 @@ MCE_INDUCT_API int mce_induct(const int64_t* x, int64_t B, int64_t T, int locks,
 
 /* Longest text mce_induct accepts. No counterpart in the reference (which has no length limit). */
 MCE_INDUCT_API int mce_induct_max_len(void);
+
+/* Workspace bytes mce_induct_ws needs for B texts of T tokens: 0 when T <= mce_induct_max_len() (no workspace); above
+ * it, per text, 12 bytes per position of T rounded up to a power of two (sort keys and positions) plus 4 * locks + 8
+ * per position (links and class ids); 0 also for arguments the call rejects (T > 2^24, B <= 0, locks outside 1-3).
+ * No counterpart in the reference. */
+MCE_INDUCT_API size_t mce_induct_ws_bytes(int64_t B, int64_t T, int locks);
+
+/* mce_induct for texts of any length up to 2^24 tokens, as `_induct_raw` (full2.py:1499-1535) takes them (the
+ * reference trains on 16384-token texts, pg19_needle.py:177): T <= mce_induct_max_len() runs mce_induct (ws unused,
+ * may be NULL); longer texts need ws (256-byte aligned, >= mce_induct_ws_bytes(B, T, locks) bytes, its contents on
+ * entry unused and on return unspecified). Calls that overlap on one workspace race. */
+MCE_INDUCT_API int mce_induct_ws(const int64_t* x, int64_t B, int64_t T, int locks, int longest,
+                                 const int64_t* bucket, int64_t nbucket, int64_t c1_none, int64_t* cand, uint8_t* on,
+                                 int64_t* src, int64_t* bk, int64_t* c1, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,8 @@ SIGNATURES = {
     # include/mce_induct.h
     "mce_induct": (_INT, [_P, _I, _I, _INT, _INT, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
     "mce_induct_max_len": (_INT, []),
+    "mce_induct_ws_bytes": (_S, [_I, _I, _INT]),
+    "mce_induct_ws": (_INT, [_P, _I, _I, _INT, _INT, _P, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P]),
     # include/mce_swiglu.h
     "mce_swiglu_fwd": (_INT, [_P, _I, _I, _INT, _P, _P]),
     "mce_swiglu_bwd": (_INT, [_P, _P, _INT, _I, _I, _INT, _P, _P]),

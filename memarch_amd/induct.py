@@ -1,4 +1,5 @@
-"""Keys-and-locks pointer candidates on MI355X (libmce.so `mce_induct`).
+"""Keys-and-locks pointer candidates on MI355X (libmce.so `mce_induct`, and `mce_induct_ws` for texts longer than
+the 8192 tokens one workgroup holds in LDS).
 
 Mirror of memarch's `FullLM2._induct_raw` (full2.py:1499-1535) and of the mixture producer in `FullLM2.forward`
 (full2.py:1559-1566). The reference method reads its configuration from the model: with `lock_w` (INDUCT=lock)
@@ -12,6 +13,8 @@ import torch
 from . import _lib
 from .fused_ops import _check_cuda, _ptr, _stream
 
+_LONG_MAX = 1 << 24  # longest text of mce_induct_ws
+
 
 def _launch(x, locks, longest, bucket, c1_none, want):
     if x.dim() != 2:
@@ -20,8 +23,8 @@ def _launch(x, locks, longest, bucket, c1_none, want):
         raise ValueError(f"locks={locks} must be 1, 2 or 3")
     B, T = x.shape
     lib = _lib.load()
-    if T > lib.mce_induct_max_len():
-        raise ValueError(f"texts of at most {lib.mce_induct_max_len()} tokens are supported, got T={T}")
+    if T > _LONG_MAX:
+        raise ValueError(f"texts of at most {_LONG_MAX} tokens are supported, got T={T}")
     _check_cuda(x, bucket)
     dev = x.device
     xl = x.detach().to(torch.int64).contiguous()
@@ -32,9 +35,16 @@ def _launch(x, locks, longest, bucket, c1_none, want):
                src=torch.empty(B, T, locks, **i64) if "src" in want else None,
                bk=torch.empty(B, T, **i64) if "bk" in want else None,
                c1=torch.empty(B, T, **i64) if "c1" in want else None)
-    _lib.call("mce_induct", _ptr(xl), B, T, locks, int(bool(longest)), _ptr(bl), 0 if bl is None else bl.numel(),
-              c1_none, _ptr(out["cand"]), _ptr(out["on"]), _ptr(out["src"]), _ptr(out["bk"]), _ptr(out["c1"]),
-              _stream(dev))
+    args = (_ptr(xl), B, T, locks, int(bool(longest)), _ptr(bl), 0 if bl is None else bl.numel(), c1_none,
+            _ptr(out["cand"]), _ptr(out["on"]), _ptr(out["src"]), _ptr(out["bk"]), _ptr(out["c1"]))
+    if T <= lib.mce_induct_max_len():
+        _lib.call("mce_induct", *args, _stream(dev))
+    else:
+        # longer texts: the sort runs over a workspace (caching allocator, so 256-byte aligned), freed on return
+        # while the kernel may still read it, which the allocator orders by the stream
+        nbytes = lib.mce_induct_ws_bytes(B, T, locks)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _lib.call("mce_induct_ws", *args, _ptr(ws), nbytes, _stream(dev))
     return out
 
 

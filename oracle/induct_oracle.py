@@ -45,11 +45,13 @@ def brute_force(x, V, locks=3, longest=True, want_src=False):
     return (cand, on, src) if want_src else (cand, on)
 
 
-def sorted_scan(x, V, locks=3, longest=True):
+def sorted_scan(x, V, locks=3, longest=True, want_src=False):
+    """(cand, on[, src]) by the stable-argsort formulation; src = last + 1 where a lock fires, else 0 (as in
+    `brute_force`)."""
     x = np.asarray(x, np.int64)
     B, T = x.shape
     rows = np.arange(B)[:, None]
-    cands, ons = [], []
+    cands, ons, srcs = [], [], []
     for key in _keys(x, V, locks):
         order = np.argsort(key, axis=1, kind="stable")
         ks = np.take_along_axis(key, order, 1)
@@ -61,10 +63,12 @@ def sorted_scan(x, V, locks=3, longest=True):
         src = np.minimum(last + 1, T - 1)
         cands.append(np.where(ok, np.take_along_axis(x, src, 1), 0))
         ons.append(ok)
+        srcs.append(np.where(ok, src, 0))
     if longest:
         for k in range(locks - 1):
             ons[k] = ons[k] & ~np.stack(ons[k + 1:], 0).any(0)
-    return np.stack(cands, -1), np.stack(ons, -1)
+    out = (np.stack(cands, -1), np.stack(ons, -1))
+    return out + (np.stack(srcs, -1),) if want_src else out
 
 
 def buckets(x, bucket):

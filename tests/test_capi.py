@@ -114,3 +114,28 @@ def test_induct_argument_checks(lib):
     assert lib.mce_induct(p, 2, 16, 3, 1, p, 0, 0, p, p, p, p, p, None) == 1         # empty bucket table
     assert lib.mce_induct(None, 0, 16, 3, 1, None, 0, 0, None, None, None, None, None, None) == 0   # no texts
     assert lib.mce_induct(None, 2, 16, 3, 1, None, 0, 0, p, p, p, p, p, None) == 1   # null x
+
+
+def test_induct_long_argument_checks(lib):
+    """mce_induct_ws: the workspace size per text (12 bytes per position of T rounded up to a power of two plus
+    4 * locks + 8 per position, each array 256-byte aligned) and every rejection before a HIP call."""
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf)
+    a = (p + 255) & ~255                                         # 256-byte aligned inside buf
+    assert lib.mce_induct_ws_bytes(2, 8192, 3) == 0               # held in LDS: no workspace
+    assert lib.mce_induct_ws_bytes(2, 16384, 3) == 2 * (8 + 4 + 4 * 3 + 8) * 16384
+    assert lib.mce_induct_ws_bytes(1, 8193, 1) == 8 * 16384 + 4 * 16384 + 33024 + 65792
+    assert lib.mce_induct_ws_bytes(1, (1 << 24) + 1, 3) == 0      # above the long path's limit
+    assert lib.mce_induct_ws_bytes(0, 20000, 3) == 0
+    assert lib.mce_induct_ws_bytes(1, 20000, 4) == 0
+    need = lib.mce_induct_ws_bytes(2, 9000, 3)
+    args = lambda T, locks=3, ws=a, nb=need, x=p, B=2: (x, B, T, locks, 1, None, 0, 0, p, p, p, p, p, ws, nb, None)
+    assert lib.mce_induct_ws(*args(9000, ws=None)) == 1           # a long text needs the workspace
+    assert lib.mce_induct_ws(*args(9000, nb=need - 1)) == 1       # too small
+    assert lib.mce_induct_ws(*args(9000, ws=a + 16)) == 1         # not 256-byte aligned
+    assert lib.mce_induct_ws(*args((1 << 24) + 1)) == 1           # above the limit
+    assert lib.mce_induct_ws(*args(9000, locks=0)) == 1
+    assert lib.mce_induct_ws(*args(9000, x=None)) == 1            # null x
+    assert lib.mce_induct_ws(*args(9000, B=0, x=None, ws=None)) == 0   # no texts
+    assert lib.mce_induct_ws(*args(16, locks=4, ws=None)) == 1    # T <= 8192: mce_induct's checks
+    assert lib.mce_induct_ws(*args(16, x=None, ws=None)) == 1

@@ -103,3 +103,54 @@ def test_induct_mix_matches_numpy_and_grads():
     ref = np.zeros((3, 7))
     np.add.at(ref, (kk[ob.any(-1)], bkn[ob.any(-1)]), (dgn * gn * (1 - gn))[ob.any(-1)])
     np.testing.assert_allclose(mix_w.grad.cpu().numpy(), ref, rtol=1e-4, atol=1e-6)
+
+
+def _long_texts(seed, B, T, V):
+    """Zipf(1.2) tokens below V with 15% of positions overwritten by copies of earlier spans (lengths 3-12), so the
+    pair and triple locks fire throughout a long text."""
+    r = np.random.default_rng(seed)
+    x = np.minimum(r.zipf(1.2, (B, T)) - 1, V - 1).astype(np.int64)
+    for b in range(B):
+        done = 0
+        while done < 0.15 * T:
+            n = int(r.integers(3, 13))
+            dst = int(r.integers(n + 1, T - n)) if T > 2 * n + 2 else 0
+            srcp = int(r.integers(0, dst - n)) if dst > n else 0
+            x[b, dst:dst + n] = x[b, srcp:srcp + n]
+            done += n
+    return x
+
+
+@pytest.mark.parametrize("B,T,V", [(1, 8193, 50257), (2, 12000, 50257), (3, 16384, 50257), (2, 20000, 7),
+                                   (1, 70000, 50257)], ids=lambda v: str(v))
+@pytest.mark.parametrize("locks,longest", [(3, True), (2, False), (1, True)])
+def test_long_texts_exact(B, T, V, locks, longest):
+    """Texts longer than one workgroup's LDS holds (mce_induct_ws): the sort over the workspace with LDS chunk
+    rounds, up to five wide stages per k at T = 70000 (131072 padded positions), against the argsort oracle; every
+    output bit-exact (cand, on, src, bk, c1)."""
+    print(f"induct long B={B} T={T} V={V} locks={locks} longest={longest}", flush=True)
+    x = _long_texts(B * 31 + T + V, B, T, V)
+    bucket = np.arange(40) // 6
+    cand, on, bk, src, c1 = _gpu(x, locks, longest, bucket)
+    cs, os_, ss = io.sorted_scan(x, V, locks, longest, want_src=True)
+    np.testing.assert_array_equal(on, os_)
+    np.testing.assert_array_equal(cand, cs)
+    np.testing.assert_array_equal(src, ss)
+    np.testing.assert_array_equal(bk, io.buckets(x, bucket))
+    np.testing.assert_array_equal(c1, io.c1_of(cs, os_, none=-1))
+    if locks > 1:
+        assert on[..., 1:].any(), "the copied spans should fire the longer locks"
+
+
+def test_long_texts_large_token_ids():
+    """Ids up to 2^40 in a long text: the oracle runs on the ids' ranks (a relabelling keeps every equality) and
+    the candidates map back through the id table."""
+    r = np.random.default_rng(5)
+    pool = np.sort(r.choice(1 << 40, 11, replace=False)).astype(np.int64)
+    idx = _long_texts(6, 2, 9000, 11)
+    x = pool[idx]
+    cand, on, _, src, c1 = _gpu(x, 3, True)
+    ci, oi, si = io.sorted_scan(idx, 11, 3, want_src=True)
+    np.testing.assert_array_equal(on, oi)
+    np.testing.assert_array_equal(src, si)
+    np.testing.assert_array_equal(cand, np.where(si > 0, pool[ci], 0))

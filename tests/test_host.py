@@ -81,8 +81,8 @@ def test_induct_host_checks():
     from memarch_amd import induct
     with pytest.raises(ValueError, match="GPU only"):
         induct.induct_raw(torch.zeros(2, 8, dtype=torch.long))
-    with pytest.raises(ValueError, match="at most 8192"):
-        induct.induct_raw(torch.zeros(1, 8193, dtype=torch.long, device="meta"))
+    with pytest.raises(ValueError, match="at most 16777216"):
+        induct.induct_raw(torch.zeros(1, (1 << 24) + 1, dtype=torch.long, device="meta"))
     with pytest.raises(ValueError, match="locks"):
         induct.pointer_candidate(torch.zeros(1, 8, dtype=torch.long, device="meta"), locks=4)
 

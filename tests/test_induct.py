@@ -49,9 +49,10 @@ def test_all_locks_on_mode_and_src(seed):
     """INDUCT=1 (two locks, every firing lock on, full2.py:1531-1532) and the src output (want_src)."""
     x, V = _texts(seed)
     cb, ob, sb = io.brute_force(x, V, 2, longest=False, want_src=True)
-    cs, os_ = io.sorted_scan(x, V, 2, longest=False)
+    cs, os_, ss = io.sorted_scan(x, V, 2, longest=False, want_src=True)
     np.testing.assert_array_equal(ob, os_)
     np.testing.assert_array_equal(cb, cs)
+    np.testing.assert_array_equal(sb, ss)
     t = np.arange(x.shape[1])[None, :, None]
     assert np.all(sb <= t)                                            # causal
     np.testing.assert_array_equal(np.take_along_axis(x[..., None].repeat(2, -1), sb, 1)[ob], cb[ob])
@@ -72,3 +73,15 @@ def test_tiny_texts(T):
     assert not ob[:, 0].any()                                         # nothing precedes t = 0
     if T == 3:
         assert ob[0, 2, 1] and cb[0, 2, 1] == 4 and ob[1, 2, 0] and cb[1, 2, 0] == 2
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_sorted_scan_src_three_locks(seed):
+    """sorted_scan's src (the GPU tests' reference for long texts) equals brute force's with three locks, longest
+    lock winning."""
+    x, V = _texts(seed + 10)
+    cb, ob, sb = io.brute_force(x, V, 3, want_src=True)
+    cs, os_, ss = io.sorted_scan(x, V, 3, want_src=True)
+    np.testing.assert_array_equal(ob, os_)
+    np.testing.assert_array_equal(cb, cs)
+    np.testing.assert_array_equal(sb, ss)
