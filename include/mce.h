@@ -27,7 +27,7 @@
  *   - H is [N, K] (ldh), W is [V, K] (ldw). K, ldh and ldw must be multiples of 8; H and W 16-byte aligned.
  *   - y is int64 [N]; gate and hit are fp32 [N], or both NULL (plain cross-entropy, the `linear_ce` of
  *     fused_ops.py:39-63,170-172). With the mixture, a target outside [0, V_real) has probability 0 (py = 0).
- *   - cand is int64 [N, kc], cval fp32 [N, kc], 0 <= kc <= 8.
+ *   - cand is int64 [N, kc], cval fp32 [N, kc], 0 <= kc <= 64.
  *   - bias may be NULL (no bias; e.g. the `_head_w` layout of full2.py:1842-1851 that folds the bias into W).
  *   - N = 0 (an empty batch) is valid: the [N]-sized and [N, *]-sized pointers may then be NULL; the calls write
  *     loss_sum = 0 and zero dW / dBias where asked, as the reference's chunk loop over no rows leaves them.
@@ -90,8 +90,9 @@ MCE_API int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
  * counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving or evaluation loops, harnesses that forbid hipMalloc). Its scratch is a fixed 64 MiB
  * device array inside the library, one copy per GPU, held until the process ends; a shape whose mce_fwd
- * workspace (mce_fwd_ws_bytes(N, K, V)) exceeds 64 MiB -- e.g. N > ~21000 rows at V = 50304, N > ~8100 at
- * V = 131072 -- is rejected with MCE_ESCRATCH before any GPU work. The call allocates nothing, records no memset,
+ * workspace without the sparse candidates' slots (mce_fwd_ws_bytes(N, K, V) less 256 bytes per row) exceeds
+ * 64 MiB -- N > 21236 rows at V = 50304, N > 8183 at V = 131072 -- is rejected with MCE_ESCRATCH before any GPU
+ * work. The call allocates nothing, records no memset,
  * and needs nothing cleared beforehand. All calls on one GPU share that GPU's scratch: calls that overlap in time
  * on one GPU (different streams, or other host threads) race and must be ordered by the caller.
  */
@@ -101,7 +102,7 @@ MCE_API int mce_fwd_noalloc(const uint16_t* H, int64_t ldh, const uint16_t* W, i
                     float* loss_sum, void* stream);
 
 /*
- * Forward of plain cross-entropy with a sparse additive logit bias (kc candidates per row, kc <= 8; kc = 0 is
+ * Forward of plain cross-entropy with a sparse additive logit bias (kc candidates per row, kc <= 64; kc = 0 is
  * plain cross-entropy). Replaces `_LinearCESparse.forward` (fused_ops.py:71-91) minus its gradient GEMMs: the
  * logits GEMM (fused_ops.py:82), the `scatter_add_` of the bias (fused_ops.py:84) and the loss half of
  * `_ce_grad_kernel` (fused_ops.py:15-30). Outputs as mce_fwd (wgt_rows is 1, or 0 for an ignored row); uses the mce_fwd
@@ -237,7 +238,7 @@ MCE_API int mce_fwd_train(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t l
 
 /*
  * Forward of the training path with a sparse logit bias (plain cross-entropy): logits[n, cand[n, j]] += cval[n, j]
- * (j < kc <= 8; repeated ids add up; ids outside [0, V_real) are ignored), as mce_fwd_sparse; otherwise as
+ * (j < kc <= 64; repeated ids add up; ids outside [0, V_real) are ignored), as mce_fwd_sparse; otherwise as
  * mce_fwd_train (the candidates' E' entries come from their biased logits), followed by mce_bwd_train and
  * mce_bwd_train_dcval. Replaces `_LinearCESparse.forward` (fused_ops.py:71-91): the logits GEMM, the scatter of b
  * into the bf16 logits (fused_ops.py:84), `_ce_grad_kernel` and the gradient GEMMs.

@@ -780,7 +780,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
 // Sparse additive logit bias (`linear_ce_sparse`, fused_ops.py:66-101; the eager form full2.py:1920-1922): row
 // n adds cval[n, k] to the logit of vocabulary id cand[n, k] for k < kc. Repeated ids add up (scatter_add);
 // ids outside [0, V_real) are ignored.
-constexpr int MAX_KC = 8;  // sparse candidates per row
+constexpr int MAX_KC = 64;  // sparse candidates per row (the reference's phrasebook passes 32, prior_top.py:4)
 
 // Total sparse bias of row n on vocabulary id c (0 when c is not a candidate).
 __device__ __forceinline__ float sparse_bias(const int64_t* cand, const float* cval, int kc, int64_t n, int64_t c) {
@@ -1170,7 +1170,7 @@ __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__
     }
   }
   if (fix_col != nullptr)
-    for (; f < MAX_KC; ++f) fix_col[n * MAX_KC + f] = -1;
+    for (; f < kc; ++f) fix_col[n * MAX_KC + f] = -1;  // k_bwd_grad reads the first kc slots
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1256,6 +1256,22 @@ __device__ __forceinline__ f32x16 transpose_block(const uint32_t (&pk)[8], const
 
 constexpr int GRAD_LDS_BYTES = LDS_BYTES + BM * 4;  // operand ring + bias slot
 
+// Sparse fix-ups f0 .. f0 + FIX_CHUNK - 1 of row n for k_bwd_grad (slots of fix_col / fix_val below nfix): the
+// column as a local index of the lane's half of the wave's 128 vocabulary rows (-1: none there) and the value.
+constexpr int FIX_CHUNK = 8;
+__device__ __forceinline__ void load_fix(int (&scol)[FIX_CHUNK], float (&sval)[FIX_CHUNK],
+                                         const int* __restrict__ fix_col, const float* __restrict__ fix_val,
+                                         int64_t n, int f0, int nfix, int64_t N, int64_t vw, int lh) {
+#pragma unroll
+  for (int f = 0; f < FIX_CHUNK; ++f) {
+    const bool ok = f0 + f < nfix && n < N;
+    const int c = ok ? fix_col[n * MAX_KC + f0 + f] : -1;
+    const int64_t d = (int64_t)c - vw - 4 * lh;
+    scol[f] = (c >= 0 && d >= 0 && d < 128) ? (int)d : -1;
+    sval[f] = ok ? fix_val[n * MAX_KC + f0 + f] : 0.f;
+  }
+}
+
 template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int* __restrict__ ty,
@@ -1307,20 +1323,11 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int64_t nb = n0 + wn * 128 + nj * 32;  // first row n of the block
-    // sparse fix-ups of row nb + lr (nfix > 0 only with a sparse bias), as local indices like yl
-    int scol[MAX_KC];
-    float sval[MAX_KC];
-    if (nfix > 0) {
-      const int64_t n = nb + lr;
-#pragma unroll
-      for (int f = 0; f < MAX_KC; ++f) {
-        const bool ok = f < nfix && n < N;
-        const int c = ok ? fix_col[n * MAX_KC + f] : -1;
-        const int64_t d = (int64_t)c - vw - 4 * lh;
-        scol[f] = (c >= 0 && d >= 0 && d < 128) ? (int)d : -1;
-        sval[f] = ok ? fix_val[n * MAX_KC + f] : 0.f;
-      }
-    }
+    // sparse fix-ups of row nb + lr (nfix > 0 only with a sparse bias), as local indices like yl, FIX_CHUNK at a
+    // time: with nfix <= FIX_CHUNK the one chunk is loaded here once, else each chunk is reloaded for every mi
+    int scol[FIX_CHUNK];
+    float sval[FIX_CHUNK];
+    if (nfix > 0) load_fix(scol, sval, fix_col, fix_val, nb + lr, 0, nfix, N, vw, lh);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       float g[16];
@@ -1335,9 +1342,10 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           g[r] = c == yl[nj] ? fv[nj] : g[r];
         }
       }
-      if (nfix > 0) {
+      for (int f0 = 0; f0 < nfix; f0 += FIX_CHUNK) {
+        if (nfix > FIX_CHUNK) load_fix(scol, sval, fix_col, fix_val, nb + lr, f0, nfix, N, vw, lh);
 #pragma unroll
-        for (int f = 0; f < MAX_KC; ++f)
+        for (int f = 0; f < FIX_CHUNK; ++f)
           if (__builtin_amdgcn_ballot_w64((scol[f] >> 5) == mi) != 0) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -2057,15 +2065,16 @@ struct FwdWs {
   size_t bytes;
 };
 // Forward workspace: per-half-tile (max, sum-exp) partials [2*tiles_v][N], target logits [N], candidate
-// logits [N][MAX_KC] (sparse bias only), the counter and list of the rows whose lse the exact pass rewrites.
-FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V) {
+// logits [N][kslots] (kslots = kc of the call; mce_fwd_ws_bytes sizes MAX_KC), the counter and list of the rows
+// whose lse the exact pass rewrites.
+FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V, int kslots) {
   const int64_t T = 2 * cdiv(V, BM);
   FwdWs w{};
   size_t off = 0;
   w.part_m = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.part_s = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N);
-  w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * MAX_KC);
+  w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * kslots);
   w.xcount = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
   w.xlist = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * N);
   w.sum_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, SUM_CHUNK));
@@ -2357,7 +2366,7 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
     return launch_status();
   }
   if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
-  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V, kc);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   if ((rc = fwd_launch(w, H, ldh, W, ldw, bias, y, gate, hit, cand, cval, kc, N, K, V, V_real, w.xy, loss_rows,
                        lse_rows, wgt_rows, dgr_rows, st)))
@@ -2781,7 +2790,7 @@ int mce_last_hip_error(void) { return g_last_hip_error; }
 size_t mce_fwd_ws_bytes(int64_t N, int64_t K, int64_t V) {
   (void)K;
   if (N < 0 || V <= 0) return 0;
-  return fwd_ws_layout(nullptr, N, V).bytes;
+  return fwd_ws_layout(nullptr, N, V, MAX_KC).bytes;
 }
 
 size_t mce_bwd_ws_bytes(int64_t N, int64_t K, int64_t V) {
@@ -2803,7 +2812,7 @@ int mce_fwd_noalloc(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
                     float* loss_sum, void* stream) {
   int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
   if (rc) return rc;
-  if (fwd_ws_layout(nullptr, N, V).bytes > SCRATCH_BYTES) return MCE_ESCRATCH;
+  if (fwd_ws_layout(nullptr, N, V, 0).bytes > SCRATCH_BYTES) return MCE_ESCRATCH;  // no sparse candidates
   void* ws = nullptr;
   if ((rc = scratch_for_stream(reinterpret_cast<hipStream_t>(stream), &ws))) return rc;
   return fwd_impl(H, ldh, W, ldw, bias, y, gate, hit, nullptr, nullptr, 0, N, K, V, V_real, loss_rows, lse_rows,
@@ -2843,7 +2852,7 @@ int mce_lse_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, 
   if (rc) return rc;
   if (N == 0) return MCE_OK;
   if (!y || !lse_rows || !ly_rows || !ws) return MCE_EINVAL;
-  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V);
+  const FwdWs w = fwd_ws_layout(reinterpret_cast<char*>(ws), N, V, 0);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   return fwd_launch(w, H, ldh, W, ldw, bias, y, nullptr, nullptr, nullptr, nullptr, 0, N, K, V, V_real, ly_rows,
                     nullptr, lse_rows, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream));

@@ -26,7 +26,7 @@ import torch
 from . import _lib
 
 _BF16 = torch.bfloat16
-MAX_KC = 8   # sparse candidates per row of linear_ce_sparse (the library's limit)
+MAX_KC = 64  # sparse candidates per row of linear_ce_sparse (the library's limit)
 RECOMPUTE = os.environ.get("MEMARCH_AMD_RECOMPUTE", "0") == "1"   # True: the two-pass (recompute) backward
 BLOCK_ROWS = int(os.environ.get("MEMARCH_AMD_BLOCK_ROWS", "0"))   # rows per block of the one-pass path (0: library)
 GRAD_H, GRAD_W, GRAD_BIAS = 1, 2, 4   # MCE_GRAD_* of include/mce.h

@@ -117,7 +117,9 @@ SPARSE = [
     # (N, K, V, kc, value scale)
     (256, 128, 512, 3, 2.0),
     (300, 72, 1000, 1, 1.0),
-    (777, 520, 2051, 8, 3.0),     # the largest kc
+    (777, 520, 2051, 8, 3.0),
+    (600, 256, 3000, 32, 3.0),    # the 32 of the reference's phrasebook (tools/phr/prior_top.py:4, full2.py:1589)
+    (300, 520, 1500, 64, 2.0),    # the largest kc (more than the 8 fix-ups k_bwd_grad holds at once)
     (129, 2064, 1024, 2, 8.0),    # candidates dominate their rows
     (200, 256, 800, 4, -20.0),    # candidates pushed far below the rest
     (160, 128, 600, 2, 70.0),     # candidates far above: rows whose lse exceeds e_n by over 60 take the exact pass

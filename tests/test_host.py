@@ -53,9 +53,9 @@ def test_reference_signatures_ce_and_sparse():
 def test_sparse_validation_before_any_launch():
     meta = dict(device="meta")
     h, w, y = torch.randn(4, 8, **meta), torch.randn(16, 8, **meta), torch.zeros(4, dtype=torch.long, **meta)
-    with pytest.raises(ValueError, match="at most 8"):
-        fused_ops._forward(None, h, w, None, y, None, None, None, torch.zeros(4, 9, dtype=torch.long, **meta),
-                           torch.zeros(4, 9, **meta))
+    with pytest.raises(ValueError, match="at most 64"):
+        fused_ops._forward(None, h, w, None, y, None, None, None, torch.zeros(4, 65, dtype=torch.long, **meta),
+                           torch.zeros(4, 65, **meta))
     with pytest.raises(ValueError, match="must both be"):
         fused_ops._forward(None, h, w, None, y, None, None, None, torch.zeros(4, 3, dtype=torch.long, **meta),
                            torch.zeros(4, 2, **meta))

@@ -71,14 +71,17 @@ def test_noalloc_matches_mce_fwd_on_two_calls():
 
 
 def test_noalloc_rejects_shapes_beyond_the_scratch():
-    """The size check runs before any GPU call, so this needs no GPU: at V = 50304 a 21023-row forward fits in the
-    64 MiB scratch and a 21024-row one does not."""
+    """The size check runs before any GPU call, so this needs no GPU: at V = 50304 a 21236-row forward fits in the
+    64 MiB scratch and a 21237-row one does not. The scratch holds mce_fwd's workspace without the slots of sparse
+    candidate logits (this forward has none), which mce_fwd_ws_bytes sizes for 64 per row."""
     lib = _lib.load()
-    assert lib.mce_fwd_ws_bytes(21023, 2048, 50304) <= SCRATCH_BYTES < lib.mce_fwd_ws_bytes(21024, 2048, 50304)
+    slots = lambda n: (4 * 64 * n + 255) // 256 * 256
+    ws = lambda n: lib.mce_fwd_ws_bytes(n, 2048, 50304) - slots(n)
+    assert ws(21236) <= SCRATCH_BYTES < ws(21237)
     buf = ctypes.create_string_buffer(1 << 12)
     p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256
     args = lambda n: (p, 2048, p, 2048, None, p, p, p, n, 2048, 50304, 50257, p, p, p, p, p, None)
-    assert lib.mce_fwd_noalloc(*args(21024)) == MCE_ESCRATCH
+    assert lib.mce_fwd_noalloc(*args(21237)) == MCE_ESCRATCH
     assert lib.mce_fwd_noalloc(*args(1 << 20)) == MCE_ESCRATCH
     assert lib.mce_fwd_noalloc(*args(-1)) == 1                      # argument checks come first
     assert b"scratch" in lib.mce_error_string(MCE_ESCRATCH)
