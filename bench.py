@@ -103,6 +103,8 @@ def _args():
     ap.add_argument("--peaked", type=float, default=0.0,
                     help="fraction of rows given a logit 50-100 above their e_n (the one-pass path's exact fallback); "
                          "reports the rows it rewrote per step")
+    ap.add_argument("--sparse-kc", type=int, default=3,
+                    help="--op linear_ce_sparse: candidates per row (1-64; the reference's phrasebook passes 32)")
     ap.add_argument("--induct-len", type=int, default=0,
                     help="--op induct: tokens per text (0: the configuration's own; above 8192 the long-text path, "
                          "mce_induct_ws), same text count and distributions")
@@ -283,11 +285,20 @@ def peak_rows(inp, frac, vid=1000, seed=5):
     return rows
 
 
+SPARSE_KC = 3  # candidates per row of --op linear_ce_sparse (--sparse-kc)
+
+
 def sparse_bias(y, c1, v_real, gen=None):
-    """Three candidates per row for the sparse logit bias: the pointer candidate (0 where none), the target and
-    the next id, with values ~ N(0, 1) (the shape `_induct_raw`'s tongue bias has: 2-3 ids per row)."""
-    cand = torch.stack([c1.clamp(min=0), y, (y + 1) % v_real], 1)
-    val = torch.randn(cand.shape, generator=gen if gen is not None else torch.Generator().manual_seed(7))
+    """SPARSE_KC candidates per row for the sparse logit bias: the pointer candidate (0 where none), the target and
+    the next id (the shape `_induct_raw`'s tongue bias has: 2-3 ids per row), then, with --sparse-kc above 3, ids
+    drawn from the 4096 most frequent (the phrasebook's top continuations, 32 per context, full2.py:1582-1591);
+    values ~ N(0, 1)."""
+    g = gen if gen is not None else torch.Generator().manual_seed(7)
+    cand = torch.stack([c1.clamp(min=0), y, (y + 1) % v_real], 1)[:, :SPARSE_KC]
+    if SPARSE_KC > 3:
+        more = torch.randint(0, min(v_real, 4096), (y.shape[0], SPARSE_KC - 3), generator=g)
+        cand = torch.cat([cand, more.to(cand.device)], 1)
+    val = torch.randn(cand.shape, generator=g)
     return cand, val
 
 
@@ -645,7 +656,12 @@ def bench_swiglu(args):
 
 
 def main():
+    global SPARSE_KC
     args = _args()
+    if not 1 <= args.sparse_kc <= 64:
+        print(f"--sparse-kc {args.sparse_kc} is outside 1-64", file=sys.stderr)
+        sys.exit(2)
+    SPARSE_KC = args.sparse_kc
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the fused op is single-GPU in this build, so --gpus {args.gpus} "
               "is refused (the op would shard over rows, each GPU running it on its N/G rows)", file=sys.stderr)
@@ -809,7 +825,8 @@ def main():
         "dtype": "bf16", "data": f"synthetic (seeded config {cfg.index} distributions, random-init weights)",
         "config": {"workload": f"config {cfg.index}: " + ("fused linear+CE+pointer" if args.op == "fused_ce" else
                                                              args.op) + " fwd+bwd, one batch per step",
-                   "N": n, "d": d, "V": v, "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32"},
+                   "N": n, "d": d, "V": v, "V_real": cfg.v_real, "operands": "bf16", "accumulate": "fp32",
+                   **({"kc": SPARSE_KC} if args.op == "linear_ce_sparse" else {})},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(ach / 1e12, 2),
                      "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16, 4),
                      "flops_per_launch": kflops, "launches_per_step": launches, "avg_launch_ms": round(avg_ms, 4),

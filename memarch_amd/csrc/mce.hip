@@ -789,13 +789,25 @@ __device__ __forceinline__ float sparse_bias(const int64_t* cand, const float* c
     if (cand[n * kc + k] == c) b += cval[n * kc + k];
   return b;
 }
-// Is cand[n, k] a valid id that does not occur earlier in the row?
-__device__ __forceinline__ bool first_valid(const int64_t* cand, int kc, int64_t n, int k, int64_t Vreal) {
-  const int64_t c = cand[n * kc + k];
-  if (c < 0 || c >= Vreal) return false;
-  for (int j = 0; j < k; ++j)
-    if (cand[n * kc + j] == c) return false;
-  return true;
+// x of lane j (64-bit, as two 32-bit shuffles)
+__device__ __forceinline__ int64_t shfl_i64(int64_t x, int j) {
+  const int lo = __shfl((int)(uint32_t)(uint64_t)x, j), hi = __shfl((int)(uint32_t)((uint64_t)x >> 32), j);
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+// A row's candidates with lane k < kc holding cand[n, k] (ck) and cval[n, k] (vk), -1 and 0 on the other lanes:
+// the total bias on ck (sum of the values of every slot with the same id, in slot order) and the first slot with
+// that id. Every lane of the wave takes part.
+__device__ __forceinline__ void cand_summary(int64_t ck, float vk, int kc, int lane, float& btot, int& first) {
+  btot = 0.f;
+  first = lane;
+  for (int j = 0; j < kc; ++j) {
+    const int64_t cj = shfl_i64(ck, j);
+    const float vj = __shfl(vk, j);
+    if (cj == ck) {
+      btot += vj;
+      if (j < first) first = j;
+    }
+  }
 }
 
 // h_n . w_c over K (fp32 products of the bf16 values), reduced over the wave; every lane gets the sum.
@@ -811,33 +823,78 @@ __device__ __forceinline__ float row_dot(const uint16_t* hr, const uint16_t* wr,
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
   return s;
 }
+// Four of them against one h row, their loads issued together (the sums in row_dot's order).
+__device__ __forceinline__ void row_dot4(const uint16_t* hr, const uint16_t* const (&wr)[4], int64_t K, int lane,
+                                         float (&s)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) s[q] = 0.f;
+  for (int64_t k = (int64_t)lane * 8; k < K; k += 512) {
+    const u16x8 a = *reinterpret_cast<const u16x8*>(hr + k);
+    u16x8 b[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) b[q] = *reinterpret_cast<const u16x8*>(wr[q] + k);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[q] = __builtin_fmaf(bf16_to_f32(a[e]), bf16_to_f32(b[q][e]), s[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s[q] += __shfl_xor(s[q], off);
+}
 
 // Per-row logits at the target and at the sparse candidates (h . w + bias, fp32 dot products of the bf16 rows):
 //   xy[n]    = x(n, y_n) + the sparse bias on y_n     (-inf when y_n is outside [0, V_real))
 //   xc[n, k] = x(n, cand[n, k]) without sparse bias   (-inf for ids outside [0, V_real); only when kc > 0)
-// One wave per row. The tile kernels compute the same sums in another order; the two agree to fp32 rounding.
+//   cb[n, k] = the total sparse bias on cand[n, k] where k is the first slot of a valid id, else NaN (kc > 0)
+// One wave per row; lane k holds candidate k for the row's summary (kc <= 64 = the wave), and the candidates' dot
+// products run four at a time. The tile kernels compute the same sums in another order; the two agree to fp32
+// rounding.
 __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__ H, int64_t ldh,
                                                     const uint16_t* __restrict__ W, int64_t ldw,
                                                     const float* __restrict__ bias, const int64_t* __restrict__ y,
                                                     const int64_t* __restrict__ cand, const float* __restrict__ cval,
                                                     int kc, int64_t N, int64_t K, int64_t Vreal,
                                                     float* __restrict__ xy, float* __restrict__ xc,
-                                                    int* __restrict__ zero = nullptr) {
+                                                    float* __restrict__ cb, int* __restrict__ zero = nullptr) {
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *zero = 0;  // k_fwd_merge's exact-row counter
   if (n >= N) return;
   const uint16_t* hr = H + n * ldh;
   const int64_t yn = y[n];
+  float by = 0.f;  // the sparse bias on the target (slot order, as sparse_bias sums it)
+  if (kc > 0) {
+    const int64_t ck = lane < kc ? cand[n * kc + lane] : -1;
+    const float vk = lane < kc ? cval[n * kc + lane] : 0.f;
+    float btot;
+    int first;
+    cand_summary(ck, vk, kc, lane, btot, first);
+    for (int j = 0; j < kc; ++j)
+      if (shfl_i64(ck, j) == yn) by += __shfl(vk, j);
+    if (lane < kc) cb[n * kc + lane] = (ck >= 0 && ck < Vreal && first == lane) ? btot : __builtin_nanf("");
+  }
   float x = -INFINITY;
-  if (yn >= 0 && yn < Vreal)
-    x = row_dot(hr, W + yn * ldw, K, lane) + (bias != nullptr ? bias[yn] : 0.f) + sparse_bias(cand, cval, kc, n, yn);
+  if (yn >= 0 && yn < Vreal) x = row_dot(hr, W + yn * ldw, K, lane) + (bias != nullptr ? bias[yn] : 0.f) + by;
   if (lane == 0) xy[n] = x;
-  for (int k = 0; k < kc; ++k) {
-    const int64_t c = cand[n * kc + k];
-    float xk = -INFINITY;
-    if (c >= 0 && c < Vreal) xk = row_dot(hr, W + c * ldw, K, lane) + (bias != nullptr ? bias[c] : 0.f);
-    if (lane == 0) xc[n * kc + k] = xk;
+  for (int k0 = 0; k0 < kc; k0 += 4) {
+    const uint16_t* wr[4];
+    int64_t c[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c[q] = k0 + q < kc ? cand[n * kc + k0 + q] : -1;
+      wr[q] = W + ((c[q] >= 0 && c[q] < Vreal) ? c[q] : 0) * ldw;  // an ignored slot reads row 0 and is dropped
+    }
+    float sq[4];
+    row_dot4(hr, wr, K, lane, sq);
+    if (lane == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (k0 + q < kc)
+          xc[n * kc + k0 + q] =
+              (c[q] >= 0 && c[q] < Vreal) ? sq[q] + (bias != nullptr ? bias[c[q]] : 0.f) : -INFINITY;
+    }
   }
 }
 
@@ -850,9 +907,8 @@ __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__
 // cancel each other and leave rounding noise, so a row whose corrected sum is not above 1/16 of the terms removed is
 // appended to exact_list (its lse, loss and wgt are then rewritten by k_exact_tiles / k_exact_rows).
 __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ part_m, const float* __restrict__ part_s,
-                                                   const float* __restrict__ xy, const int64_t* __restrict__ cand,
-                                                   const float* __restrict__ cval, const float* __restrict__ xc,
-                                                   int kc, int64_t Vreal, const float* __restrict__ gate,
+                                                   const float* __restrict__ xy, const float* __restrict__ cb,
+                                                   const float* __restrict__ xc, int kc, const float* __restrict__ gate,
                                                    const float* __restrict__ hit, int64_t N, int T,
                                                    float* __restrict__ loss_rows, float* __restrict__ lse_rows,
                                                    float* __restrict__ wgt_rows, float* __restrict__ dgr_rows,
@@ -909,12 +965,11 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
       if (kc > 0) {
         float Mp = M;
         for (int k = 0; k < kc; ++k)
-          if (first_valid(cand, kc, n, k, Vreal))
-            Mp = fmaxf(Mp, xc[n * kc + k] + sparse_bias(cand, cval, kc, n, cand[n * kc + k]));
+          if (!__builtin_isnan(cb[n * kc + k])) Mp = fmaxf(Mp, xc[n * kc + k] + cb[n * kc + k]);
         float Sp = M == -INFINITY ? 0.f : S * expf(M - Mp), removed = 0.f;
         for (int k = 0; k < kc; ++k)
-          if (first_valid(cand, kc, n, k, Vreal)) {
-            const float x = xc[n * kc + k], B = sparse_bias(cand, cval, kc, n, cand[n * kc + k]);
+          if (!__builtin_isnan(cb[n * kc + k])) {
+            const float x = xc[n * kc + k], B = cb[n * kc + k];
             // exp(x + B - M') - exp(x - M'); expm1 keeps small |B| exact (and would overflow for large B)
             Sp += B < 20.f ? expf(x - Mp) * expm1f(B) : expf(x + B - Mp) - expf(x - Mp);
             if (B < 0.f) removed += expf(x - Mp);
@@ -1142,9 +1197,11 @@ __global__ __launch_bounds__(256) void k_exact_rows(const int* __restrict__ coun
 }
 
 // Sparse fix-ups for k_bwd_grad, which writes go*wgt*exp(x - lse) from the logits without the sparse bias and
-// handles the target itself: entry (n, f) names a distinct valid candidate c != y_n of row n (fix_col, -1 when
-// unused) and its gradient go*wgt*exp(x_c + B_c - lse) (fix_val). dcval[n, k] = the logit gradient at
-// cand[n, k] (the reference's G.gather(1, cand)), 0 for ignored ids.
+// handles the target itself: row n's entries are its distinct valid candidates c != y_n, sorted by column
+// (fix_col, INT32_MAX in the slots after them, up to kc) with their gradients go*wgt*exp(x_c + B_c - lse)
+// (fix_val). dcval[n, k] = the logit gradient at cand[n, k] (the reference's G.gather(1, cand)), 0 for ignored ids.
+// One wave per row, lane k for candidate k (kc <= 64): the total bias, the first slot of each id and the sorted
+// position of each entry come from shuffles across the lanes.
 __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__ y, const int64_t* __restrict__ cand,
                                                      const float* __restrict__ cval, int kc,
                                                      const float* __restrict__ xy, const float* __restrict__ xc,
@@ -1152,25 +1209,35 @@ __global__ __launch_bounds__(256) void k_sparse_rows(const int64_t* __restrict__
                                                      const float* __restrict__ wgt_rows, const float* __restrict__ go,
                                                      int64_t N, int64_t Vreal, int* __restrict__ fix_col,
                                                      float* __restrict__ fix_val, float* __restrict__ dcval) {
-  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const float cn = go[0] * wgt_rows[n], lse = lse_rows[n];
   const int64_t yn = y[n];
-  int f = 0;
-  for (int k = 0; k < kc; ++k) {
-    const int64_t c = cand[n * kc + k];
-    float g = 0.f;
-    if (c >= 0 && c < Vreal)
-      g = c == yn ? cn * (expf(xy[n] - lse) - 1.f) : cn * expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - lse);
-    if (dcval != nullptr) dcval[n * kc + k] = g;
-    if (fix_col != nullptr && c != yn && first_valid(cand, kc, n, k, Vreal)) {
-      fix_col[n * MAX_KC + f] = (int)c;
-      fix_val[n * MAX_KC + f] = g;
-      ++f;
-    }
+  const int64_t ck = lane < kc ? cand[n * kc + lane] : -1;
+  const float vk = lane < kc ? cval[n * kc + lane] : 0.f;
+  float btot;
+  int first;
+  cand_summary(ck, vk, kc, lane, btot, first);
+  const bool valid = lane < kc && ck >= 0 && ck < Vreal;
+  float g = 0.f;
+  if (valid) g = ck == yn ? cn * (expf(xy[n] - lse) - 1.f) : cn * expf(xc[n * kc + lane] + btot - lse);
+  if (dcval != nullptr && lane < kc) dcval[n * kc + lane] = g;
+  if (fix_col == nullptr) return;
+  // entries: the first slot of each valid id other than the target; distinct ids, so the ranks are distinct
+  const bool entry = valid && ck != yn && first == lane;
+  int rank = 0;
+  for (int j = 0; j < kc; ++j) {
+    const int64_t cj = shfl_i64(ck, j);
+    const bool ej = __shfl((int)entry, j) != 0;
+    if (ej && cj < ck) ++rank;
   }
-  if (fix_col != nullptr)
-    for (; f < kc; ++f) fix_col[n * MAX_KC + f] = -1;  // k_bwd_grad reads the first kc slots
+  const int count = __popcll(__builtin_amdgcn_ballot_w64(entry));
+  if (entry) {
+    fix_col[n * MAX_KC + rank] = (int)ck;
+    fix_val[n * MAX_KC + rank] = g;
+  }
+  if (lane >= count && lane < kc) fix_col[n * MAX_KC + lane] = INT32_MAX;  // k_bwd_grad reads the first kc slots
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -1256,20 +1323,18 @@ __device__ __forceinline__ f32x16 transpose_block(const uint32_t (&pk)[8], const
 
 constexpr int GRAD_LDS_BYTES = LDS_BYTES + BM * 4;  // operand ring + bias slot
 
-// Sparse fix-ups f0 .. f0 + FIX_CHUNK - 1 of row n for k_bwd_grad (slots of fix_col / fix_val below nfix): the
-// column as a local index of the lane's half of the wave's 128 vocabulary rows (-1: none there) and the value.
-constexpr int FIX_CHUNK = 8;
-__device__ __forceinline__ void load_fix(int (&scol)[FIX_CHUNK], float (&sval)[FIX_CHUNK],
-                                         const int* __restrict__ fix_col, const float* __restrict__ fix_val,
-                                         int64_t n, int f0, int nfix, int64_t N, int64_t vw, int lh) {
-#pragma unroll
-  for (int f = 0; f < FIX_CHUNK; ++f) {
-    const bool ok = f0 + f < nfix && n < N;
-    const int c = ok ? fix_col[n * MAX_KC + f0 + f] : -1;
-    const int64_t d = (int64_t)c - vw - 4 * lh;
-    scol[f] = (c >= 0 && d >= 0 && d < 128) ? (int)d : -1;
-    sval[f] = ok ? fix_val[n * MAX_KC + f0 + f] : 0.f;
+// The first of row n's fix-ups (k_sparse_rows: sorted by column, INT32_MAX after the last) whose column is at
+// least lo: a binary search over the row's nfix slots (nfix <= 64: at most 7 steps).
+__device__ __forceinline__ int fix_lower_bound(const int* __restrict__ fix_col, int64_t n, int nfix, int64_t lo) {
+  int a = 0, b = nfix;
+  while (a < b) {
+    const int m = (a + b) >> 1;
+    if ((int64_t)fix_col[n * MAX_KC + m] < lo)
+      a = m + 1;
+    else
+      b = m;
   }
+  return a;
 }
 
 template <bool KF>
@@ -1323,11 +1388,9 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int64_t nb = n0 + wn * 128 + nj * 32;  // first row n of the block
-    // sparse fix-ups of row nb + lr (nfix > 0 only with a sparse bias), as local indices like yl, FIX_CHUNK at a
-    // time: with nfix <= FIX_CHUNK the one chunk is loaded here once, else each chunk is reloaded for every mi
-    int scol[FIX_CHUNK];
-    float sval[FIX_CHUNK];
-    if (nfix > 0) load_fix(scol, sval, fix_col, fix_val, nb + lr, 0, nfix, N, vw, lh);
+    // sparse fix-ups of row nb + lr (nfix > 0 only with a sparse bias): the run of its sorted entries whose columns
+    // fall in this lane's 128 vocabulary rows (from vw + 4*lh; usually none or one), found once per row
+    const int f0 = (nfix > 0 && nb + lr < N) ? fix_lower_bound(fix_col, nb + lr, nfix, vw + 4 * lh) : nfix;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       float g[16];
@@ -1342,17 +1405,20 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
           g[r] = c == yl[nj] ? fv[nj] : g[r];
         }
       }
-      for (int f0 = 0; f0 < nfix; f0 += FIX_CHUNK) {
-        if (nfix > FIX_CHUNK) load_fix(scol, sval, fix_col, fix_val, nb + lr, f0, nfix, N, vw, lh);
+      // as local indices like yl: element (mi, r) is local index mi*32 + 8*(r/4) + r%4; an entry of the other
+      // lane half (bit 2 of the local index set) matches no element
+      for (int f = f0; f < nfix; ++f) {
+        const int64_t fi = (nb + lr) * MAX_KC + f;
+        const int64_t d = (int64_t)fix_col[fi] - (vw + 4 * lh);
+        if (d >= 128) break;  // sorted: the rest lie past this lane's rows (INT32_MAX ends the list)
+        if ((d >> 5) == mi) {
+          const float val = fix_val[fi];
 #pragma unroll
-        for (int f = 0; f < FIX_CHUNK; ++f)
-          if (__builtin_amdgcn_ballot_w64((scol[f] >> 5) == mi) != 0) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int c = mi * 32 + 8 * (r >> 2) + (r & 3);
-              g[r] = c == scol[f] ? sval[f] : g[r];
-            }
+          for (int r = 0; r < 16; ++r) {
+            const int c = mi * 32 + 8 * (r >> 2) + (r & 3);
+            g[r] = c == (int)d ? val : g[r];
           }
+        }
       }
       uint32_t pk[8];
 #pragma unroll
@@ -1447,8 +1513,8 @@ __device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(pack_bf
 // logit when the target lies outside tile 0; also clears the flags and the ncount flagged-row counters.
 __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_m, const float* __restrict__ part_s,
                                                  const float* __restrict__ xy, const int64_t* __restrict__ y,
-                                                 const int64_t* __restrict__ cand, const float* __restrict__ cval,
-                                                 const float* __restrict__ xc, int kc, int64_t Vreal, int64_t N,
+                                                 const int64_t* __restrict__ cand, const float* __restrict__ cb,
+                                                 const float* __restrict__ xc, int kc, int64_t N,
                                                  int64_t Np, float* __restrict__ lse_est, int* __restrict__ flag,
                                                  int* __restrict__ counts, int ncount) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1479,13 +1545,12 @@ __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_
     // and the candidates is the bound
     bool neg = false;
     float mx = x;
-    for (int k = 0; k < kc; ++k)
-      if (first_valid(cand, kc, n, k, Vreal)) {
-        const int64_t c = cand[n * kc + k];
-        const float B = sparse_bias(cand, cval, kc, n, c);
-        if (c < BM && B < 0.f) neg = true;
-        mx = fmaxf(mx, xc[n * kc + k] + B);
-      }
+    for (int k = 0; k < kc; ++k) {
+      const float B = cb[n * kc + k];  // NaN: not the first slot of a valid id
+      if (__builtin_isnan(B)) continue;
+      if (cand[n * kc + k] < BM && B < 0.f) neg = true;
+      mx = fmaxf(mx, xc[n * kc + k] + B);
+    }
     if (neg) l = mx;
   }
   lse_est[n] = l;
@@ -1575,7 +1640,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
 // with a sparse bias also the entries of the row's candidates; flagged rows get a_n = wgt_n and are appended to
 // flag_list for the exact pass (k_gather_rows, k_exact_train, k_exact_fix). Rows N .. Np-1 get a_n = 0.
 __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ y, const float* __restrict__ xy,
-                                                    const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                    const int64_t* __restrict__ cand, const float* __restrict__ cb,
                                                     const float* __restrict__ xc, int kc,
                                                     const float* __restrict__ lse_est,
                                                     const float* __restrict__ lse_rows,
@@ -1607,8 +1672,9 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   // x_y already includes its bias)
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
-    if (c == yn || !first_valid(cand, kc, n, k, Vreal)) continue;
-    G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - e));
+    const float B = cb[n * kc + k];
+    if (c == yn || __builtin_isnan(B)) continue;
+    G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + B - e));
   }
 }
 
@@ -1690,7 +1756,7 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
 // row logits of k_row_logits (x_y with its sparse bias, x_c without), into G. One thread per entry.
 __global__ __launch_bounds__(256) void k_exact_fix(const int* __restrict__ count, const int* __restrict__ list,
                                                    const int64_t* __restrict__ y, const float* __restrict__ xy,
-                                                   const int64_t* __restrict__ cand, const float* __restrict__ cval,
+                                                   const int64_t* __restrict__ cand, const float* __restrict__ cb,
                                                    const float* __restrict__ xc, int kc,
                                                    const float* __restrict__ lse_rows, int64_t Np,
                                                    int64_t Vreal, uint16_t* __restrict__ G) {
@@ -1701,8 +1767,9 @@ __global__ __launch_bounds__(256) void k_exact_fix(const int* __restrict__ count
   if (yn >= 0 && yn < Vreal) G[cm_index(n, yn, Np)] = to_bf16(expf(xy[n] - l) - 1.f);
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
-    if (c == yn || !first_valid(cand, kc, n, k, Vreal)) continue;
-    G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + sparse_bias(cand, cval, kc, n, c) - l));
+    const float B = cb[n * kc + k];
+    if (c == yn || __builtin_isnan(B)) continue;
+    G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + B - l));
   }
 }
 
@@ -2060,7 +2127,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 struct FwdWs {
-  float *part_m, *part_s, *xy, *xc, *sum_part;
+  float *part_m, *part_s, *xy, *xc, *cb, *sum_part;
   int *xcount, *xlist;
   size_t bytes;
 };
@@ -2075,6 +2142,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V, int kslots) {
   w.part_s = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * T * N);
   w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N);
   w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * kslots);
+  w.cb = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * N * kslots);
   w.xcount = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int));
   w.xlist = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * N);
   w.sum_part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * cdiv(N, SUM_CHUNK));
@@ -2091,7 +2159,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V, int kslots) {
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
   uint16_t *G, *Wt, *Ht;
-  float *dbias_part, *xy, *part, *xc, *fix_val, *tval;
+  float *dbias_part, *xy, *part, *xc, *cb, *fix_val, *tval;
   int *fix_col, *ty;
   int64_t np, vp;
   size_t bytes;
@@ -2111,6 +2179,7 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.tval = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
   w.part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * TAIL_SLOTS * BM * BN);
   w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
+  w.cb = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
   w.fix_col = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * w.np * MAX_KC);
   w.fix_val = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
   w.bytes = off;
@@ -2328,7 +2397,7 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
-                     kc, N, K, V_real, xy, w.xc, w.xcount);
+                     kc, N, K, V_real, xy, w.xc, w.cb, w.xcount);
   if ((rc = launch_status())) return rc;
   {
     ProfScope prof(PROF_FWD_TILES, st);
@@ -2340,8 +2409,8 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
                          tn, w.part_m, w.part_s);
   }
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, cand, cval,
-                     w.xc, kc, V_real, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, nullptr,
+  hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, w.cb, w.xc,
+                     kc, gate, hit, N, 2 * tv, loss_rows, lse_rows, wgt_rows, dgr_rows, nullptr,
                      kc > 0 ? w.xcount : nullptr, w.xlist);
   if ((rc = launch_status())) return rc;
   if (kc == 0) return MCE_OK;
@@ -2397,13 +2466,13 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
-                     kc, N, K, V_real, w.xy, w.xc);
+                     kc, N, K, V_real, w.xy, w.xc, w.cb);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_target_fix, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, y, w.xy, lse_rows, wgt_rows, ycoef,
                      go, N, V_real, w.ty, w.tval);
   if ((rc = launch_status())) return rc;
   if (kc > 0) {
-    hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, y, cand, cval, kc, w.xy, w.xc,
+    hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, y, cand, cval, kc, w.xy, w.xc,
                        lse_rows, wgt_rows, go, N, V_real, w.fix_col, w.fix_val, dCval);
     if ((rc = launch_status())) return rc;
   }
@@ -2440,7 +2509,7 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
 struct TrainWs {
   int64_t np, vp, nb, nblk;
   uint16_t *G, *Ht, *uperm, *Wt;
-  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *lse_est, *arow, *upart, *part, *dbias_part, *sum_part;
+  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *cb, *lse_est, *arow, *upart, *part, *dbias_part, *sum_part;
   int *flag, *flag_list, *counts, *xlist;
   size_t bytes;
 };
@@ -2483,6 +2552,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   w.p0s = reinterpret_cast<float*>(take(sizeof(float) * 2 * np));
   w.xy = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.xc = reinterpret_cast<float*>(take(sizeof(float) * np * MAX_KC));
+  w.cb = reinterpret_cast<float*>(take(sizeof(float) * np * MAX_KC));
   w.lse_est = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.arow = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.flag = reinterpret_cast<int*>(take(sizeof(int) * np));
@@ -2603,7 +2673,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     if ((rc = launch_status())) return rc;
   }
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand,
-                     cval, kc, N, K, V_real, w.xy, w.xc);
+                     cval, kc, N, K, V_real, w.xy, w.xc, w.cb);
   if ((rc = launch_status())) return rc;
   {
     // e_n: the first vocabulary tile (one tile row of k_fwd_tiles over all rows) and the target logit
@@ -2616,8 +2686,8 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
                          w.p0m, w.p0s);
     if ((rc = launch_status())) return rc;
   }
-  hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, cval,
-                     w.xc, kc, V_real, N, w.np, w.lse_est, w.flag, w.counts, (int)(2 * w.np / BLK));
+  hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, w.cb,
+                     w.xc, kc, N, w.np, w.lse_est, w.flag, w.counts, (int)(2 * w.np / BLK));
   if ((rc = launch_status())) return rc;
   const float s_max = g_train_s_max.load(std::memory_order_relaxed);
   for (int64_t b = 0; b < w.nblk; ++b) {
@@ -2637,8 +2707,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     if ((rc = launch_status())) return rc;
     int* xcount = w.counts + w.np / BLK + b;
     hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(rows, 32)), dim3(256), 0, st, w.part_m, w.part_s,
-                       w.xy + row0, at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, V_real,
-                       at(gate, row0), at(hit, row0), rows, 2 * tv, loss_rows + row0, lse_rows + row0,
+                       w.xy + row0, w.cb + row0 * kc, w.xc + row0 * kc, kc, at(gate, row0), at(hit, row0), rows, 2 * tv, loss_rows + row0, lse_rows + row0,
                        wgt_rows + row0, at(dgr_rows, row0), nullptr, kc > 0 ? xcount : nullptr, w.xlist);
     if ((rc = launch_status())) return rc;
     if (kc > 0 && (rc = launch_exact(H + row0 * ldh, ldh, W, ldw, bias, at(cand, row0 * kc), at(cval, row0 * kc), kc,
@@ -2646,7 +2715,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
                                      loss_rows + row0, lse_rows + row0, wgt_rows + row0, st)))
       return rc;
     hipLaunchKernelGGL(k_train_rows, dim3((unsigned)(rp / 256)), dim3(256), 0, st, y + row0, w.xy + row0,
-                       at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, w.lse_est + row0,
+                       at(cand, row0 * kc), w.cb + row0 * kc, w.xc + row0 * kc, kc, w.lse_est + row0,
                        lse_rows + row0, wgt_rows + row0, w.flag + row0, rows, rp, V_real, w.arow + row0,
                        w.counts + b, w.flag_list, w.G);
     if ((rc = launch_status())) return rc;
@@ -2662,7 +2731,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
                          w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     if ((rc = launch_status())) return rc;
     hipLaunchKernelGGL(k_exact_fix, dim3((unsigned)(rp / 256)), dim3(256), 0, st, w.counts + b, w.flag_list, y + row0,
-                       w.xy + row0, at(cand, row0 * kc), at(cval, row0 * kc), w.xc + row0 * kc, kc, lse_rows + row0,
+                       w.xy + row0, at(cand, row0 * kc), w.cb + row0 * kc, w.xc + row0 * kc, kc, lse_rows + row0,
                        rp, V_real, w.G);
     if ((rc = launch_status())) return rc;
     if (b + 1 < w.nblk) {
@@ -2978,7 +3047,7 @@ int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval
   if (!y || !lse_rows || !wgt_rows || !go || !dCval || !ws) return MCE_EINVAL;
   const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V, block_rows);
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
                      y, cand, cval, kc, w.xy, w.xc, lse_rows, wgt_rows, go, N, V_real, nullptr, nullptr, dCval);
   return launch_status();
 }

@@ -366,7 +366,7 @@ def linear_ce(h, w, y, chunk=4096):
 
 @torch.compiler.disable
 def linear_ce_sparse(h, w, y, cand, b, chunk=4096):
-    """linear_ce with the sparse logit bias logits[n, cand[n, j]] += b[n, j], j < k <= 8 (fused_ops.py:99-101)."""
+    """linear_ce with the sparse logit bias logits[n, cand[n, j]] += b[n, j], j < k <= 64 (fused_ops.py:99-101)."""
     return _LinearCESparse.apply(h.reshape(-1, h.shape[-1]), w, y.reshape(-1),
                                  cand.reshape(-1, cand.shape[-1]).long(), b.reshape(-1, b.shape[-1]), chunk)
 

@@ -72,10 +72,10 @@ def test_noalloc_matches_mce_fwd_on_two_calls():
 
 def test_noalloc_rejects_shapes_beyond_the_scratch():
     """The size check runs before any GPU call, so this needs no GPU: at V = 50304 a 21236-row forward fits in the
-    64 MiB scratch and a 21237-row one does not. The scratch holds mce_fwd's workspace without the slots of sparse
-    candidate logits (this forward has none), which mce_fwd_ws_bytes sizes for 64 per row."""
+    64 MiB scratch and a 21237-row one does not. The scratch holds mce_fwd's workspace without the two arrays of
+    sparse-candidate slots (this forward has none), which mce_fwd_ws_bytes sizes for 64 per row."""
     lib = _lib.load()
-    slots = lambda n: (4 * 64 * n + 255) // 256 * 256
+    slots = lambda n: 2 * ((4 * 64 * n + 255) // 256 * 256)
     ws = lambda n: lib.mce_fwd_ws_bytes(n, 2048, 50304) - slots(n)
     assert ws(21236) <= SCRATCH_BYTES < ws(21237)
     buf = ctypes.create_string_buffer(1 << 12)
