@@ -80,15 +80,16 @@ def _sibling_cases(count, seed):
         n = int(r.integers(1, 1537))
         k = int(8 * r.integers(1, 265))
         v = int(r.integers(2, 3073))
-        out.append((n, k, v, int(r.integers(1, 9)), float(r.choice([0.5, 2.0, 4.0])), bool(r.random() < 0.5),
+        out.append((n, k, v, int(r.choice([1, 2, 3, 4, 5, 6, 7, 8, 16, 32, 64])), float(r.choice([0.5, 2.0, 4.0])),
+                    bool(r.random() < 0.5),
                     str(r.choice(["one_pass", "blocks256", "recompute"])), 2000 + i))
     return out
 
 
 @pytest.mark.parametrize("case", _sibling_cases(12, 2027), ids=lambda c: "N{}_K{}_V{}_kc{}_s{}_{}".format(*c[:5], c[6]))
 def test_sparse_sweep(case, monkeypatch):
-    """linear_ce_sparse on seeded random shapes: kc random up to 8, candidates with repeats, the target and ignored
-    ids (tests/test_gpu_ce.py's generator), on both paths and in row blocks."""
+    """linear_ce_sparse on seeded random shapes: kc from 1-8, 16, 32 and 64, candidates with repeats, the target
+    and ignored ids (tests/test_gpu_ce.py's generator), on both paths and in row blocks."""
     import test_gpu_ce as ce
     from memarch_amd import fused_ops
     n, k, v, kc, scale, _, path, seed = case
