@@ -1,4 +1,4 @@
-"""The ops under torch.autocast(bf16), where the reference's training loop runs them (fastloop.py:409; the
+"""The ops under torch.autocast(bf16) and inside torch.compile, where the reference's training loop runs them
 reference's autograd Functions take no autocast decorator, and neither do these): forward and backward inside the
 autocast region give results bit-identical to the same calls outside it, for every public op of the path, with
 fp32 h (the dtype autocast leaves on tensors that no autocast op produced) and with bf16 h."""
@@ -81,3 +81,31 @@ def test_autocast_swiglu():
         torch.cuda.synchronize()
         outs.append((y.detach(), x.grad))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("op", ["mix", "chunk_ce"])
+def test_inside_torch_compile(op):
+    """A step compiled by torch.compile that calls the op (the reference's model is compiled around its loss head,
+    which torch.compiler.disable keeps out of the graph, fused_ops.py:165, full2.py:1842): the graph breaks at the
+    op and the step's loss and gradients equal the eager step's bit for bit (aot_eager: no code generation)."""
+    from memarch_amd import chunk_ce, fused_ops
+    x = _inputs()
+
+    def step(h, w, gate):
+        hn = h * torch.rsqrt((h * h).mean(-1, keepdim=True) + 1e-6)
+        if op == "mix":
+            return fused_ops.linear_ce_mix(hn, w, x["y"], gate, x["hit"]) / h.shape[0]
+        lse, ly = chunk_ce.chunk_ce(hn, w, None, x["y"])
+        return (lse - ly).mean()
+
+    outs = []
+    for fn in (step, torch.compile(step, backend="aot_eager")):
+        h = x["h"].clone().requires_grad_()
+        w = x["w"].clone().requires_grad_()
+        gate = x["gate"].clone().requires_grad_()
+        loss = fn(h, w, gate)
+        loss.backward()
+        torch.cuda.synchronize()
+        outs.append((loss.detach(), h.grad, w.grad, gate.grad))
+    for a, b in zip(*outs):
+        assert (a is None and b is None) or torch.equal(a, b)
