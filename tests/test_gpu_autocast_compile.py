@@ -1,7 +1,8 @@
 """The ops under torch.autocast(bf16) and inside torch.compile, where the reference's training loop runs them
-reference's autograd Functions take no autocast decorator, and neither do these): forward and backward inside the
-autocast region give results bit-identical to the same calls outside it, for every public op of the path, with
-fp32 h (the dtype autocast leaves on tensors that no autocast op produced) and with bf16 h."""
+(fastloop.py:409; the reference's autograd Functions take no autocast decorator, and neither do these): forward and
+backward inside the autocast region give results bit-identical to the same calls outside it, for every public op of
+the path, with fp32 h (the dtype autocast leaves on tensors that no autocast op produced) and with bf16 h; a step
+compiled around the op matches the eager step."""
 import pytest
 import torch
 
