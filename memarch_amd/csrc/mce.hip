@@ -823,11 +823,13 @@ __device__ __forceinline__ float row_dot(const uint16_t* hr, const uint16_t* wr,
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
   return s;
 }
-// Four of them against one h row, their loads issued together (the sums in row_dot's order).
+// Four of them against one h row, their loads issued together (the sums in row_dot's order); the K loop is
+// unrolled so that the loads of several of its steps are in flight at once (a gather of W rows is latency-bound).
 __device__ __forceinline__ void row_dot4(const uint16_t* hr, const uint16_t* const (&wr)[4], int64_t K, int lane,
                                          float (&s)[4]) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) s[q] = 0.f;
+#pragma unroll 4
   for (int64_t k = (int64_t)lane * 8; k < K; k += 512) {
     const u16x8 a = *reinterpret_cast<const u16x8*>(hr + k);
     u16x8 b[4];
