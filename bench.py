@@ -81,6 +81,9 @@ def _args():
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
     ap.add_argument("--calibrate-mfma", action="store_true",
                     help="time the MFMA-rate probe (register tile without global memory traffic) and exit")
+    ap.add_argument("--calibrate-tiles", action="store_true",
+                    help="MFMA rate of two-workgroups-per-CU tiles with the forward's epilogue, in lockstep and "
+                         "offset by half a tile (what overlapping the epilogue wins), and exit")
     ap.add_argument("--calibrate-stream", action="store_true",
                     help="time a 2 GiB streaming copy (plain and non-temporal) and exit")
     ap.add_argument("--op", choices=("fused_ce",) + SIBLING_OPS + ("induct", "swiglu"), default="fused_ce",
@@ -519,7 +522,64 @@ def _probe_lib():
     lib.mce_probe_copy.restype = ctypes.c_int
     lib.mce_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_void_p]
+    lib.mce_probe_tiles.restype = ctypes.c_int
+    lib.mce_probe_tiles.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
+
+
+def calibrate_tiles():
+    """What overlapping the tile epilogue with MFMA work wins under the board's power limit: the tile probe (two
+    workgroups of 4 waves per CU, 4 x 2 accumulator blocks per wave, 128 K16 slices from LDS, then the training
+    forward's epilogue over the accumulators; no global memory) over a grid of 128 waves of tiles, run with the two
+    workgroups of each CU starting together and offset by half a tile (the second half of the first wave runs half
+    tiles, so one workgroup's epilogue runs beside the other's MFMAs), and mode 2 of
+    --calibrate-mfma (the same tile and reads, no epilogue) at the same MFMA work. The clock takes some 20 ms of MFMA
+    load to settle, so about 100 ms of warm-up launches come first, then the three runs interleaved over 5 rounds
+    (median per run), timed with torch events on the probe's stream."""
+    lib = _probe_lib()
+    dev = torch.device("cuda", 0)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    waves = 128
+    blocks = 2 * cus * waves
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    out2 = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    full = 4 * 128 * 8 * 32768                       # MFMA FLOP of a full tile (4 waves)
+    steps = 128 * waves                              # mode 2: the same MFMA work per CU
+
+    def tiles(lo, hi):
+        rc = lib.mce_probe_tiles(blocks, lo, hi, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st.cuda_stream))
+        if rc:
+            raise RuntimeError(f"mce_probe_tiles returned {rc}")
+
+    def mode2():
+        rc = lib.mce_probe_mfma(2, cus, steps, ctypes.c_void_p(out2.data_ptr()), ctypes.c_void_p(st.cuda_stream))
+        if rc:
+            raise RuntimeError(f"mce_probe_mfma returned {rc}")
+
+    runs = [("full tiles (the two workgroups of a CU start together)", lambda: tiles(0, 0), blocks * full),
+            ("offset by half a tile", lambda: tiles(cus, 2 * cus), (blocks - cus) * full + cus * full // 2),
+            ("mode 2, no epilogue", mode2, cus * 4 * steps * 16 * 32768)]
+    for _ in range(20):
+        tiles(0, 0)
+    torch.cuda.synchronize()
+    secs = {name: [] for name, _, _ in runs}
+    for _ in range(5):
+        for name, fn, _ in runs:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            fn()
+            e1.record(st)
+            e1.synchronize()
+            secs[name].append(e0.elapsed_time(e1) * 1e-3)
+    assert torch.isfinite(out).all().item() and torch.isfinite(out2).all().item()
+    res = []
+    for name, _, flop in runs:
+        sec = sorted(secs[name])[2]
+        res.append({"run": name, "ms": round(sec * 1e3, 3), "tflops": round(flop / sec / 1e12, 1),
+                    "frac": round(flop / sec / PEAK_BF16, 4)})
+    print(json.dumps({"calibration": "tile epilogue overlap (two workgroups per CU, no global memory)",
+                      "tile_waves": waves, "workgroups": blocks, "peak": PEAK_BF16, "runs": res}), flush=True)
 
 
 def calibrate_stream():
@@ -674,6 +734,9 @@ def main():
         return
     if args.calibrate_stream:
         calibrate_stream()
+        return
+    if args.calibrate_tiles:
+        calibrate_tiles()
         return
     if args.op == "swiglu":
         bench_swiglu(args)

@@ -14,6 +14,13 @@
 //                          AGPRs), 6 fragments read from LDS per 8 MFMAs, 8 waves per workgroup (512 threads), the
 //                          same MFMA work per launch as modes 0 and 1.
 // Each thread writes the sum of its accumulators to out[thread], so the MFMAs are not dead code.
+//
+// The tile probe (mce_probe_tiles) adds the forward tile kernel's structure to mode 2: a grid of workgroups of one
+// tile each (two workgroups of 4 waves per CU, 4 x 2 blocks per wave, at most 256 registers), 128 K16 slices
+// (K = 2048) ended by the logits-gradient epilogue of the training forward over the wave's accumulators (per element
+// an FMA, an exp2, a sum and half a bf16 pack; no global stores). With a range of blocks running half a tile the two
+// workgroups of a CU start half a tile apart, so one's epilogue runs beside the other's MFMAs; without it they start
+// together. Against mode 2 (the same tile without the epilogue) the rates give what the epilogue costs.
 // The copy (k_probe_copy) moves n 16-byte vectors with a grid-stride loop, 4 vectors per thread in flight, plain or
 // non-temporal loads and stores.
 #include <hip/hip_runtime.h>
@@ -201,6 +208,110 @@ __global__ __launch_bounds__(512) void k_probe_lds2w(int steps, float* __restric
   out[(int64_t)blockIdx.x * 512 + t] = sum;
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+constexpr int TILE_STEPS = 128;  // K16 slices per tile (K = 2048)
+
+// The training forward's epilogue over NI x NJ accumulator blocks: e = exp2(x log2e - lb) summed into s and packed
+// to bf16 pairs (xored into the returned word, so the packs are not dead code).
+template <int NI, int NJ>
+__device__ __forceinline__ uint32_t tile_epilogue(f32x16 (&acc)[NI][NJ], float lb, float& s) {
+  uint32_t keep = 0;
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const float x0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i][j][e], 1.4426950408889634f, -lb));
+        const float x1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i][j][e + 1], 1.4426950408889634f, -lb));
+        s += x0;
+        s += x1;
+        keep ^= __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x0, x1}, bf16x2));
+
+      }
+  return keep;
+}
+template <int NI, int NJ>
+__device__ __forceinline__ void zero(f32x16 (&acc)[NI][NJ]) {
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+}
+
+__device__ void fill_lds(uint32_t* lds, uint32_t seed, int t, int nt) {
+  uint32_t h = seed * 2654435761u + 1u;
+  for (int i = t; i < 16384; i += nt) {
+    h = xorshift(h);
+    lds[i] = (h & MANT_SIGN) | EXP_BASE;
+  }
+  __syncthreads();
+}
+
+// n K16 slices (n even) of a 4 x 2 tile from LDS, as k_probe_lds2w
+__device__ __forceinline__ void slices42(f32x16 (&acc)[4][2], const u32x4* line, int wave, int lane, int n) {
+  // lines (s % 8) * 7 + f + 2 wave (< 64, no wrap): one base register and immediate offsets per read
+  auto at = [&](int s, int f) { return ((s & 7) * 7 + f + wave * 2) * 64 + lane; };
+  u32x4 a0[4], b0[2], a1[4], b1[2];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) a0[f] = line[at(0, f)];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) b0[f] = line[at(0, 4 + f)];
+  for (int s = 0; s < n; s += 2) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) a1[f] = line[at(s + 1, f)];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) b1[f] = line[at(s + 1, 4 + f)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma(a0[i], b0[j], acc[i][j]);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) a0[f] = line[at(s + 2, f)];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) b0[f] = line[at(s + 2, 4 + f)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mfma(a1[i], b1[j], acc[i][j]);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+  }
+}
+
+// One 4 x 2 tile per wave per workgroup, two workgroups per CU; blocks [half_lo, half_hi) run half a tile, so that
+// the two workgroups of a CU (blocks b and b + CUs in the first wave of the grid) stay half a tile apart
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2))) void k_probe_tiles(
+    int half_lo, int half_hi, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint32_t lds[16384];
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  fill_lds(lds, (uint32_t)blockIdx.x * 256u + t, t, 256);
+  const u32x4* line = reinterpret_cast<const u32x4*>(lds);
+  const bool half = (int)blockIdx.x >= half_lo && (int)blockIdx.x < half_hi;
+  f32x16 acc[4][2];
+  zero(acc);
+  if (half)
+    slices42(acc, line, wave, lane, TILE_STEPS / 2);
+  else
+    slices42(acc, line, wave, lane, TILE_STEPS);
+  float s = 0.f;
+  const uint32_t keep = tile_epilogue(acc, 1.f, s);
+  out[(int64_t)blockIdx.x * 256 + t] = s + (float)(keep & 1u);
+}
+
 template <bool NT>
 __global__ __launch_bounds__(256) void k_probe_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
                                                    int64_t n) {
@@ -241,6 +352,17 @@ extern "C" __attribute__((visibility("default"))) int mce_probe_copy(const void*
     hipLaunchKernelGGL(k_probe_copy<true>, dim3((unsigned)blocks), dim3(256), 0, st, s, d, n);
   else
     hipLaunchKernelGGL(k_probe_copy<false>, dim3((unsigned)blocks), dim3(256), 0, st, s, d, n);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// Tile probe (above): a grid of `blocks` workgroups of 256 threads, one 4 x 2 tile per wave, blocks
+// [half_lo, half_hi) half a tile. out holds blocks * 256 floats. Returns 0, 1 for bad arguments, 2 for a launch
+// error. MFMA work: 4 * 128 * 8 * 32768 FLOP per full workgroup, half that per half one.
+extern "C" __attribute__((visibility("default"))) int mce_probe_tiles(int blocks, int half_lo, int half_hi, float* out,
+                                                                      hipStream_t st) {
+  if (blocks < 1 || blocks > (1 << 24) || out == nullptr || half_lo < 0 || half_hi < half_lo || half_hi > blocks)
+    return 1;
+  hipLaunchKernelGGL(k_probe_tiles, dim3((unsigned)blocks), dim3(256), 0, st, half_lo, half_hi, out);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 

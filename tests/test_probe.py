@@ -1,4 +1,4 @@
-"""The measurement probes behind `bench.py --calibrate-mfma` and `--calibrate-stream` (memarch_amd/csrc/probe.hip,
+"""The measurement probes behind `bench.py --calibrate-mfma`, `--calibrate-tiles` and `--calibrate-stream` (probe.hip,
 libmce_probe.so): they load, reject bad arguments on the host (before any HIP call, so no GPU is needed), and on the
 GPU the MFMA probe's three modes produce the accumulator sums their operands determine (the same finite values on two
 launches) and the copy copies, plain and non-temporal, with a ragged length."""
@@ -22,6 +22,8 @@ def probe():
     lib.mce_probe_copy.restype = ctypes.c_int
     lib.mce_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_void_p]
+    lib.mce_probe_tiles.restype = ctypes.c_int
+    lib.mce_probe_tiles.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
@@ -34,6 +36,9 @@ def test_rejects_bad_arguments(probe):
     for src, dst, n, blocks in ((None, b, 4, 1), (a, None, 4, 1), (a, b, 0, 1), (a, b, 4, 0), (a, b, 4, (1 << 20) + 1),
                                 (ctypes.c_void_p(24), b, 4, 1), (a, ctypes.c_void_p(40), 4, 1)):
         assert probe.mce_probe_copy(src, dst, n, blocks, 1, None) == 1, (src, dst, n, blocks)
+    for blocks, lo, hi, ptr in ((0, 0, 0, out), (4, 0, 0, None), (4, 3, 2, out), (4, -1, 2, out), (4, 2, 5, out),
+                                ((1 << 24) + 1, 0, 0, out)):
+        assert probe.mce_probe_tiles(blocks, lo, hi, ptr, None) == 1, (blocks, lo, hi)
 
 
 @pytest.mark.gpu
@@ -54,6 +59,24 @@ def test_probe_runs(probe, mode):
     assert torch.isfinite(got[0]).all()
     assert torch.equal(got[0], got[1])
     assert got[0].abs().sum() > 0
+
+
+@pytest.mark.gpu
+def test_probe_tiles(probe):
+    """The tile probe, lockstep and with half tiles: finite sums, the same on two launches."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    print("probe tiles", flush=True)
+    out = torch.full((16 * 256,), float("nan"), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    for lo, hi in ((0, 0), (4, 12)):
+        got = []
+        for _ in range(2):
+            assert probe.mce_probe_tiles(16, lo, hi, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st)) == 0
+            torch.cuda.synchronize()
+            got.append(out.clone().cpu())
+            out.fill_(float("nan"))
+        assert torch.isfinite(got[0]).all() and torch.equal(got[0], got[1])
 
 
 @pytest.mark.gpu
