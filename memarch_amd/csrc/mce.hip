@@ -2157,7 +2157,8 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V, int kslots) {
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
 //   dbias_part [2*Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split
 //   tails), ty int32 / tval fp32 [Np] (k_target_fix)
-//   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), fix_col int32 / fix_val fp32 [Np][MAX_KC]
+//   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), cb [Np][MAX_KC] fp32 (their total biases, NaN past
+//   the first slot of an id), fix_col int32 / fix_val fp32 [Np][MAX_KC]
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
   uint16_t *G, *Wt, *Ht;
