@@ -154,3 +154,40 @@ def test_long_texts_large_token_ids():
     np.testing.assert_array_equal(on, oi)
     np.testing.assert_array_equal(src, si)
     np.testing.assert_array_equal(cand, np.where(si > 0, pool[ci], 0))
+
+
+@pytest.mark.parametrize("T", [1024, 16384], ids=["lds", "long"])
+def test_no_host_sync_and_graph_capture(T):
+    """Both paths issue no host synchronisation (torch.cuda.set_sync_debug_mode("error"), as the loss head is
+    audited), and a call captured in a HIP graph replays bit-identically to eager calls on new texts."""
+    from memarch_amd import induct
+    print(f"induct sync/graph T={T}", flush=True)
+    texts = [torch.from_numpy(_long_texts(900 + i, 3, T, 50257)).cuda() for i in range(3)]
+    bucket = torch.arange(40, device="cuda") // 6
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        induct.induct_raw(texts[0], 3, True, bucket, want_src=True)
+        induct.pointer_candidate(texts[0], 2, False, none=-1)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    x = texts[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        induct.induct_raw(x, 3, True, bucket, want_src=True)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = induct.induct_raw(x, 3, True, bucket, want_src=True)
+    torch.cuda.synchronize()
+    for t in texts[1:] + texts[:1]:
+        x.copy_(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = induct.induct_raw(t, 3, True, bucket, want_src=True)
+        torch.cuda.synchronize()
+        for a, r in zip(outs, ref):
+            assert torch.equal(a, r)
