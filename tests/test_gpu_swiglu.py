@@ -134,3 +134,48 @@ def test_rejects_cpu_and_odd_width():
         swiglu(torch.zeros(2, 8))
     with pytest.raises(ValueError):
         swiglu(torch.zeros(2, 7, device="cuda"))
+
+
+def test_no_host_sync_and_graph_capture():
+    """Forward + backward issue no host synchronisation (torch.cuda.set_sync_debug_mode("error")), and a step
+    captured in a HIP graph replays bit-identically to eager steps on new values."""
+    from memarch_amd import swiglu as sw
+    print("swiglu sync/graph", flush=True)
+    g = torch.Generator().manual_seed(12)
+    vals = [torch.randn(257, 2 * 1536, generator=g).cuda().bfloat16() for _ in range(3)]
+    gos = [torch.randn(257, 1536, generator=g).cuda().bfloat16() for _ in range(3)]
+
+    def step(x, go):
+        y = sw.swiglu(x)
+        y.backward(go)
+        return y
+
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        step(vals[0].clone().requires_grad_(), gos[0])
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    x = vals[0].clone().requires_grad_()
+    go = gos[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(x, go)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    x.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = step(x, go)
+    torch.cuda.synchronize()
+    for v, o in zip(vals[1:] + vals[:1], gos[1:] + gos[:1]):
+        with torch.no_grad():
+            x.copy_(v)
+            go.copy_(o)
+        graph.replay()
+        torch.cuda.synchronize()
+        xe = v.clone().requires_grad_()
+        ye = step(xe, o)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ye) and torch.equal(x.grad, xe.grad)
