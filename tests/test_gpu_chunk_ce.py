@@ -113,3 +113,45 @@ def test_chunk_ce_only_ly_used():
     (ly * c["gy"].cuda()).sum().backward()
     want = c["gy"].numpy()[:, None].astype(np.float64) * orc.bf16_round(c["w"].numpy())[c["y"].numpy()]
     assert orc.rel_fro(h.grad.float().cpu().numpy(), want) <= GRAD_RTOL
+
+
+def test_masked_bias_rare_pass():
+    """The rare-word pass of `_short_logp` (full2.py:1893-1896): chunk_ce over the full head with a bias holding -inf
+    for the short vocabulary's ids (br = b + sv_mask), on rows whose targets are partly those ids. Those rows' ly is
+    -inf and torch.where(hit, ly - lse, 0) gives them zero upstream gradients on both outputs; the rare rows get
+    (g_ly, g_lse) = (u, -u) from logp = ly - lse. lse, the finite ly and every gradient match the oracle; the masked
+    targets' ly is exactly -inf, the masked columns' dBias exactly 0, and no gradient holds a NaN."""
+    from memarch_amd.chunk_ce import chunk_ce
+    n, k, v = 500, 256, 3000
+    c = _case(n, k, v, seed=71)
+    g = torch.Generator().manual_seed(72)
+    masked = torch.randperm(v, generator=g)[:1000]
+    c["b"][masked] = float("-inf")
+    rare = torch.rand(n, generator=g) < 0.5
+    free = torch.ones(v, dtype=torch.bool)
+    free[masked] = False
+    free = torch.nonzero(free).flatten()
+    c["y"] = torch.where(rare, free[torch.randint(0, len(free), (n,), generator=g)],
+                         masked[torch.randint(0, len(masked), (n,), generator=g)])
+    u = torch.randn(n, generator=g)
+    c["gy"] = torch.where(rare, u, torch.zeros(n))
+    c["gl"] = torch.where(rare, -u, torch.zeros(n))
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    b = c["b"].cuda().requires_grad_()
+    lse, ly = chunk_ce(h, w, b, c["y"].cuda(), 4096)
+    hit = rare.cuda()
+    logp = torch.where(hit, ly - lse, torch.zeros_like(ly))
+    (logp * u.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    fwd, gr = _oracle(c)
+    lyn, rn = ly.detach().cpu().numpy(), rare.numpy()
+    assert np.all(np.isneginf(lyn[~rn])) and np.all(np.isfinite(lyn[rn]))
+    assert np.isfinite(lse.detach().cpu().numpy()).all()
+    assert orc.rel_fro(lse.detach().cpu().numpy(), fwd["lse"]) <= LOSS_RTOL
+    assert orc.rel_fro(lyn[rn], fwd["xy"][rn]) <= LOSS_RTOL
+    for name, got, ref in (("dh", h.grad, gr["dh"]), ("dw", w.grad, gr["dw"]), ("db", b.grad, gr["dbias"])):
+        gg = got.float().cpu().numpy()
+        assert np.isfinite(gg).all(), name
+        assert orc.rel_fro(gg, ref) <= GRAD_RTOL, (name, orc.rel_fro(gg, ref))
+    assert np.all(b.grad.cpu().numpy()[masked.numpy()] == 0)
