@@ -19,12 +19,6 @@ accumulation), with every input resident in HBM before the timed region. Prints 
 `--calibrate-copy` instead times a plain 1 GiB device-to-device copy (the reference kernel for scaling the
 FETCH_SIZE / WRITE_SIZE counters) and prints its size.
 
-`--calibrate-mfma` instead measures the bf16 MFMA rate that the contraction kernels' register tile sustains on this
-board with no global memory traffic (memarch_amd/csrc/probe.hip): from registers only, and with the mainloop's LDS
-fragment reads; the upper bound the contraction kernels' rates are read against. `--calibrate-stream` times a
-streaming copy of 2 GiB (the same probe library, plain and non-temporal accesses): the HBM bandwidth a kernel
-reaches on this board, which the HBM-bound kernels (SwiGLU, the weight cast) are read against.
-
 `--op swiglu` instead measures the SwiGLU gate kernels (memarch fused_ops.py:175-228) on the FFN of the same
 d = 2048 model (rows = N = 32768, H = 4d = 8192, bf16, lm.py:45-50): one line with the forward + backward HBM
 throughput against the 8 TB/s roofline (algorithmic bytes: forward reads gu and writes out, 3 rows x H
@@ -79,13 +73,6 @@ def _args():
     ap.add_argument("--stage-reps", type=int, default=0,
                     help="extra isolated timed repetitions of each C-ABI stage after the timed steps (0: none)")
     ap.add_argument("--calibrate-copy", action="store_true", help="time a 1 GiB device copy and exit")
-    ap.add_argument("--calibrate-mfma", action="store_true",
-                    help="time the MFMA-rate probe (register tile without global memory traffic) and exit")
-    ap.add_argument("--calibrate-tiles", action="store_true",
-                    help="MFMA rate of two-workgroups-per-CU tiles with the forward's epilogue, in lockstep and "
-                         "offset by half a tile (what overlapping the epilogue wins), and exit")
-    ap.add_argument("--calibrate-stream", action="store_true",
-                    help="time a 2 GiB streaming copy (plain and non-temporal) and exit")
     ap.add_argument("--op", choices=("fused_ce",) + SIBLING_OPS + ("induct", "swiglu"), default="fused_ce",
                     help="fused_ce: the north-star operator (default); linear_ce, linear_ce_sparse, chunk_ce: its "
                          "siblings (fused_ops.py:39-101, full2.py:753-836) on the same inputs; induct: the "
@@ -103,6 +90,12 @@ def _args():
                     help="timed replays of the same step captured in a HIP graph, reported beside the line (0: skip)")
     ap.add_argument("--gpu-reference-steps", type=int, default=3,
                     help="timed steps of the reference's method restated with torch ops on the same GPU (0: skip)")
+    ap.add_argument("--folded-steps", type=int, default=5,
+                    help="timed steps of the caller's folded call shape (--layout folded) after the biased line's "
+                         "steps, reported as folded_ms_per_step (0: skip)")
+    ap.add_argument("--library-steps", type=int, default=5,
+                    help="timed calls of each full-size library GEMM of the step's three contractions, reported as "
+                         "library_ceiling (0: skip)")
     ap.add_argument("--peaked", type=float, default=0.0,
                     help="fraction of rows given a logit 50-100 above their e_n (the one-pass path's exact fallback); "
                          "reports the rows it rewrote per step")
@@ -270,6 +263,67 @@ def gpu_reference_method(inp, v_real, steps, chunk=4096):
     out["method"] = ("fused_ops.py:138-162 in torch ops: 4096-row chunks, bf16 GEMMs (hipBLASLt), fp32 row pass "
                      "with materialised logits; gemms_only: the same chunked GEMMs without the row pass")
     return out
+
+
+def library_ceiling(n, d, v, reps):
+    """The three contractions of the step as full-size library GEMMs (torch.mm on bf16 operands: hipBLASLt), on
+    seeded random operands of the configuration's shapes: the logits h W^T ([n, d] x [d, v], bf16 out; the
+    reference's `hc @ wd.T`, fused_ops.py:150), dH = G W ([n, v] x [v, d], bf16 out; `logits @ wd`,
+    fused_ops.py:153) and dW = G^T h ([v, n] x [n, d], fp32 out where torch.mm takes out_dtype, else bf16;
+    `logits.T @ hc`, fused_ops.py:154). Each is run twice untimed, then `reps` times, each call timed with torch
+    events on the current stream; the median call gives TFLOP/s on its 2 n v d FLOP."""
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev).manual_seed(11)
+    h = torch.randn(n, d, device=dev, generator=gen).bfloat16()
+    w = (torch.randn(v, d, device=dev, generator=gen) * 0.02).bfloat16()
+    g = (torch.randn(n, v, device=dev, generator=gen) * 1e-3).bfloat16()
+    dh = torch.empty(n, d, device=dev, dtype=torch.bfloat16)
+    dw = torch.empty(v, d, device=dev, dtype=torch.float32)
+    dw_dtype = "fp32"
+    try:
+        torch.mm(g[:256, :512].T, h[:256], out_dtype=torch.float32, out=dw[:512])
+    except (RuntimeError, TypeError):
+        dw_dtype = "bf16"
+    runs = {
+        "logits": ("[%d,%d] x [%d,%d]^T, bf16 out" % (n, d, v, d), lambda: torch.mm(h, w.T, out=g)),
+        "dh": ("[%d,%d] x [%d,%d], bf16 out" % (n, v, v, d), lambda: torch.mm(g, w, out=dh)),
+        "dw": ("[%d,%d]^T x [%d,%d], %s out" % (n, v, n, d, dw_dtype),
+               (lambda: torch.mm(g.T, h, out_dtype=torch.float32, out=dw)) if dw_dtype == "fp32"
+               else (lambda: torch.mm(g.T, h))),
+    }
+    out = {}
+    for name, (shape, fn) in runs.items():
+        for _ in range(2):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record()
+        for i in range(reps):
+            fn()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        ms = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))[reps // 2]
+        tf = 2.0 * n * v * d / (ms * 1e-3)
+        out[name] = {"shape": shape, "ms": round(ms, 4), "tflops": round(tf / 1e12, 1), "frac": round(tf / PEAK_BF16, 4)}
+    del h, w, g, dh, dw
+    torch.cuda.empty_cache()
+    out["method"] = ("torch.mm (hipBLASLt) at full size on seeded bf16 operands, median of the timed calls, right "
+                     "after the fused op's steps in the same process")
+    return out
+
+
+def make_folded(inp, cfg):
+    """The caller's own call shape on the `_head_w` layout (full2.py:1842-1851,1860): hn' = [hn, 1, 0 x 15] in bf16
+    as [B, T, d + 16], W' = [W, bias, 0 x 15] (fp32 master) as [V, d + 16], y, g, hit as [B, T]; the padded ids get
+    the bias -1e4 in that column (their softmax weight underflows to exactly 0)."""
+    n, d, v = cfg.n, cfg.d, cfg.v
+    dev = inp.h.device
+    bf = inp.bias.clone()
+    bf[cfg.v_real:] = -1e4
+    hf = torch.cat([inp.h, torch.ones(n, 1, device=dev), torch.zeros(n, 15, device=dev)], 1).bfloat16()
+    wf = torch.cat([inp.w, bf.bfloat16().float()[:, None], torch.zeros(v, 15, device=dev)], 1)
+    return {"hf": hf.reshape(cfg.texts, cfg.seq, d + 16).detach().requires_grad_(), "wf": wf.detach().requires_grad_(),
+            "yf": inp.y.reshape(cfg.texts, cfg.seq), "gf": inp.gate.reshape(cfg.texts, cfg.seq).detach().requires_grad_(),
+            "hitf": inp.hit.reshape(cfg.texts, cfg.seq)}
 
 
 def peak_rows(inp, frac, vid=1000, seed=5):
@@ -512,150 +566,6 @@ def calibrate_copy():
                       "launches": 5}), flush=True)
 
 
-def _probe_lib():
-    path = os.path.join(ROOT, "memarch_amd", "libmce_probe.so")
-    if not os.path.exists(path):
-        raise SystemExit(f"{path} is missing; build it with `python -m memarch_amd.build`")
-    lib = ctypes.CDLL(path)
-    lib.mce_probe_mfma.restype = ctypes.c_int
-    lib.mce_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    lib.mce_probe_copy.restype = ctypes.c_int
-    lib.mce_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                   ctypes.c_void_p]
-    lib.mce_probe_tiles.restype = ctypes.c_int
-    lib.mce_probe_tiles.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    return lib
-
-
-def calibrate_tiles():
-    """What overlapping the tile epilogue with MFMA work wins under the board's power limit: the tile probe (two
-    workgroups of 4 waves per CU, 4 x 2 accumulator blocks per wave, 128 K16 slices from LDS, then the training
-    forward's epilogue over the accumulators; no global memory) over a grid of 128 waves of tiles, run with the two
-    workgroups of each CU starting together and offset by half a tile (the second half of the first wave runs half
-    tiles, so one workgroup's epilogue runs beside the other's MFMAs), and mode 2 of
-    --calibrate-mfma (the same tile and reads, no epilogue) at the same MFMA work. The clock takes some 20 ms of MFMA
-    load to settle, so about 100 ms of warm-up launches come first, then the three runs interleaved over 5 rounds
-    (median per run), timed with torch events on the probe's stream."""
-    lib = _probe_lib()
-    dev = torch.device("cuda", 0)
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    waves = 128
-    blocks = 2 * cus * waves
-    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
-    out2 = torch.empty(cus * 512, dtype=torch.float32, device=dev)
-    st = torch.cuda.current_stream(dev)
-    full = 4 * 128 * 8 * 32768                       # MFMA FLOP of a full tile (4 waves)
-    steps = 128 * waves                              # mode 2: the same MFMA work per CU
-
-    def tiles(lo, hi):
-        rc = lib.mce_probe_tiles(blocks, lo, hi, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st.cuda_stream))
-        if rc:
-            raise RuntimeError(f"mce_probe_tiles returned {rc}")
-
-    def mode2():
-        rc = lib.mce_probe_mfma(2, cus, steps, ctypes.c_void_p(out2.data_ptr()), ctypes.c_void_p(st.cuda_stream))
-        if rc:
-            raise RuntimeError(f"mce_probe_mfma returned {rc}")
-
-    runs = [("full tiles (the two workgroups of a CU start together)", lambda: tiles(0, 0), blocks * full),
-            ("offset by half a tile", lambda: tiles(cus, 2 * cus), (blocks - cus) * full + cus * full // 2),
-            ("mode 2, no epilogue", mode2, cus * 4 * steps * 16 * 32768)]
-    for _ in range(20):
-        tiles(0, 0)
-    torch.cuda.synchronize()
-    secs = {name: [] for name, _, _ in runs}
-    for _ in range(5):
-        for name, fn, _ in runs:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(st)
-            fn()
-            e1.record(st)
-            e1.synchronize()
-            secs[name].append(e0.elapsed_time(e1) * 1e-3)
-    assert torch.isfinite(out).all().item() and torch.isfinite(out2).all().item()
-    res = []
-    for name, _, flop in runs:
-        sec = sorted(secs[name])[2]
-        res.append({"run": name, "ms": round(sec * 1e3, 3), "tflops": round(flop / sec / 1e12, 1),
-                    "frac": round(flop / sec / PEAK_BF16, 4)})
-    print(json.dumps({"calibration": "tile epilogue overlap (two workgroups per CU, no global memory)",
-                      "tile_waves": waves, "workgroups": blocks, "peak": PEAK_BF16, "runs": res}), flush=True)
-
-
-def calibrate_stream():
-    """A 2 GiB device-to-device copy by the probe kernel (grid-stride, 4 16-byte vectors per thread in flight),
-    plain and non-temporal, over a few grid sizes: a warm-up launch, then 5 timed launches each (median), timed
-    with torch events on the stream the probe is launched on."""
-    lib = _probe_lib()
-    dev = torch.device("cuda", 0)
-    nbytes = 1 << 31
-    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev)
-    dst = torch.empty_like(src)
-    st = torch.cuda.current_stream(dev)
-    rows = []
-    for nt in (0, 1):
-        for blocks in (4096, 8192, 32768):
-            def launch():
-                rc = lib.mce_probe_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes // 16,
-                                        blocks, nt, ctypes.c_void_p(st.cuda_stream))
-                if rc:
-                    raise RuntimeError(f"mce_probe_copy returned {rc}")
-            launch()
-            secs = []
-            for _ in range(5):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(st)
-                launch()
-                e1.record(st)
-                e1.synchronize()
-                secs.append(e0.elapsed_time(e1) * 1e-3)
-            sec = sorted(secs)[2]
-            rows.append({"nontemporal": bool(nt), "workgroups": blocks, "ms": round(sec * 1e3, 3),
-                         "GBps": round(2 * nbytes / sec / 1e9, 1), "frac": round(2 * nbytes / sec / PEAK_HBM, 4)})
-    assert torch.equal(src[:1 << 20], dst[:1 << 20])
-    print(json.dumps({"calibration": "streaming copy (read + write bytes)", "bytes_read": nbytes,
-                      "bytes_written": nbytes, "peak": PEAK_HBM, "runs": rows}), flush=True)
-
-
-def calibrate_mfma():
-    """The bf16 MFMA rate of the contraction kernels' register tile (a 4 x 4 block of 32x32x16 accumulators per wave,
-    random operands) with no global memory traffic, one workgroup of 4 waves per CU: mode 0 with the fragments in
-    registers, mode 1 reading them from LDS as the GEMM mainloop does; mode 2 the tile of a two-waves-per-SIMD design
-    (4 x 2 blocks per wave, 8 waves per workgroup) reading from LDS. A warm-up launch, then 3 timed launches of
-    about 30 ms each per mode, timed with torch events on the stream the probe is launched on."""
-    lib = _probe_lib()
-    dev = torch.device("cuda", 0)
-    blocks = torch.cuda.get_device_properties(dev).multi_processor_count
-    steps = 100000
-    out = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
-    st = torch.cuda.current_stream(dev)
-    modes = []
-    for mode, name in ((0, "registers"), (1, "lds fragment reads"),
-                       (2, "lds fragment reads, 4x2 blocks per wave, two waves per SIMD")):
-        def launch(n):
-            rc = lib.mce_probe_mfma(mode, blocks, n, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st.cuda_stream))
-            if rc:
-                raise RuntimeError(f"mce_probe_mfma returned {rc}")
-        launch(steps // 10)
-        torch.cuda.synchronize()
-        secs = []
-        for _ in range(3):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(st)
-            launch(steps)
-            e1.record(st)
-            e1.synchronize()
-            secs.append(e0.elapsed_time(e1) * 1e-3)
-        flop = blocks * 4 * steps * 16 * 32768
-        sec = sorted(secs)[1]
-        modes.append({"mode": mode, "operands": name, "ms": round(sec * 1e3, 3),
-                      "tflops": round(flop / sec / 1e12, 1), "frac": round(flop / sec / PEAK_BF16, 4)})
-    assert torch.isfinite(out).all().item()
-    print(json.dumps({"calibration": "bf16 MFMA rate without global memory traffic", "workgroups": blocks,
-                      "steps_per_wave": steps, "flop_per_launch": blocks * 4 * steps * 16 * 32768,
-                      "peak": PEAK_BF16, "modes": modes}), flush=True)
-
-
 def bench_swiglu(args):
     """Forward and backward of the SwiGLU gate at rows = 32768, H = 8192, bf16; each kernel timed with torch events
     on the current stream (the stream the C-ABI calls launch on)."""
@@ -729,15 +639,6 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
         return
-    if args.calibrate_mfma:
-        calibrate_mfma()
-        return
-    if args.calibrate_stream:
-        calibrate_stream()
-        return
-    if args.calibrate_tiles:
-        calibrate_tiles()
-        return
     if args.op == "swiglu":
         bench_swiglu(args)
         return
@@ -768,24 +669,18 @@ def main():
     cand, cval = sparse_bias(inp.y.cpu(), inp.c1.cpu(), cfg.v_real)
     cand, cval = cand.to(dev), cval.to(dev).requires_grad_()
     folded = args.op == "fused_ce" and args.layout == "folded"
-    if folded:
-        # _head_w (full2.py:1842-1851): hn' = [hn, 1, 0 x 15] in bf16, W' = [W, bias, 0 x 15]; the padded ids get
-        # the bias -1e4 in that column (their softmax weight underflows to exactly 0)
-        bf = inp.bias.clone()
-        bf[cfg.v_real:] = -1e4
-        hf = torch.cat([inp.h, torch.ones(n, 1, device=dev), torch.zeros(n, 15, device=dev)], 1).bfloat16()
-        hf = hf.reshape(cfg.texts, cfg.seq, d + 16).detach().requires_grad_()
-        wf = torch.cat([inp.w, bf.bfloat16().float()[:, None], torch.zeros(v, 15, device=dev)], 1)
-        wf = wf.detach().requires_grad_()
-        yf = inp.y.reshape(cfg.texts, cfg.seq)
-        gf = inp.gate.reshape(cfg.texts, cfg.seq).detach().requires_grad_()
-        hitf = inp.hit.reshape(cfg.texts, cfg.seq)
+    fold = make_folded(inp, cfg) if folded else None
+
+    def folded_step(f):
+        f["hf"].grad = f["wf"].grad = f["gf"].grad = None
+        loss = fused_ops.linear_ce_mix(f["hf"], f["wf"], f["yf"], f["gf"], f["hitf"])
+        (loss / n).backward()
+        return loss
 
     def step():
         h.grad = w.grad = b.grad = gate.grad = cval.grad = None
         if folded:
-            hf.grad = wf.grad = gf.grad = None
-            loss = fused_ops.linear_ce_mix(hf, wf, yf, gf, hitf)
+            return folded_step(fold)
         elif args.op == "linear_ce":
             loss = fused_ops.linear_ce(h, w, inp.y)
         elif args.op == "linear_ce_sparse":
@@ -923,6 +818,26 @@ def main():
     if args.graph_steps > 0 and args.peaked == 0:
         print("[bench] the same step replayed from a HIP graph", file=sys.stderr, flush=True)
         res["graph_ms_per_step"] = graph_time(step, args.graph_steps)
+    if args.folded_steps > 0 and args.op == "fused_ce" and not folded and args.path == "one-pass" and args.peaked == 0:
+        print("[bench] the caller's folded call shape", file=sys.stderr, flush=True)
+        h.grad = w.grad = b.grad = gate.grad = None
+        f = make_folded(inp, cfg)
+        for _ in range(2):
+            folded_step(f)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(args.folded_steps):
+            folded_step(f)
+        torch.cuda.synchronize()
+        res["folded_ms_per_step"] = round((time.perf_counter() - t) / args.folded_steps * 1e3, 3)
+        res["folded_over_biased"] = round(res["folded_ms_per_step"] / res["ms_per_step"], 4)
+        del f
+        torch.cuda.empty_cache()
+    if args.library_steps > 0 and args.op == "fused_ce" and not folded:
+        print("[bench] full-size library GEMMs of the three contractions", file=sys.stderr, flush=True)
+        h.grad = w.grad = b.grad = gate.grad = None
+        torch.cuda.empty_cache()
+        res["library_ceiling"] = library_ceiling(n, d, v, args.library_steps)
     if args.gpu_reference_steps > 0 and args.op == "fused_ce":
         print("[bench] the reference's method in torch ops on the GPU", file=sys.stderr, flush=True)
         h.grad = w.grad = b.grad = gate.grad = None

@@ -90,7 +90,8 @@ MCE_API int mce_fwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
  * counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving or evaluation loops, harnesses that forbid hipMalloc). Its scratch is a fixed 64 MiB
  * device array inside the library, one copy per GPU, held until the process ends; a shape whose mce_fwd
- * workspace without the sparse candidates' slots (mce_fwd_ws_bytes(N, K, V) less 256 bytes per row) exceeds
+ * workspace without the sparse candidates' slots (mce_fwd_ws_bytes(N, K, V) less 512 bytes per row: two fp32
+ * values for each of 64 candidate slots) exceeds
  * 64 MiB -- N > 21236 rows at V = 50304, N > 8183 at V = 131072 -- is rejected with MCE_ESCRATCH before any GPU
  * work. The call allocates nothing, records no memset,
  * and needs nothing cleared beforehand. All calls on one GPU share that GPU's scratch: calls that overlap in time
@@ -220,7 +221,8 @@ MCE_API int64_t mce_train_block_rows(int64_t N, int64_t K, int64_t V, int64_t bl
  * fp32 [1]); with more than one block also the partial sums of the gradients `want` asks for over the rows of all
  * blocks but the last, for go = 1: dH_part rows [0, R) (bf16 when dh_bf16, else fp32; row stride lddh), dW_part
  * fp32 [V, K] (row stride lddw), dBias_part fp32 [V], where R = (blocks - 1) * mce_train_block_rows(...). With one
- * block they are not touched and may be NULL. W is the bf16 weight [V, ldw]: read, or, when the fp32 weight W32
+ * block they are not touched and may be NULL. dH_part, when used, is 16-byte aligned and lddh a multiple of 8 (bf16)
+ * or 4 (fp32), else MCE_EALIGN. W is the bf16 weight [V, ldw]: read, or, when the fp32 weight W32
  * [V, ldw32] is given (16-byte aligned, ldw32 % 4 == 0), written by this call as bf16(W32) (round to nearest even,
  * the cast of fused_ops.py:142) in the same pass that forms W^T. Replaces `_LinearCEMix.forward`
  * (fused_ops.py:138-157): the chunk
@@ -256,7 +258,8 @@ MCE_API int mce_fwd_train_sparse(const uint16_t* H, int64_t ldh, uint16_t* W, in
  * go * sum_n G[n, :] and dGate = go * dgr_rows; each output may be NULL, but the set of dH / dW / dBias must be the
  * forward's `want`. With more than one block the forward's partial sums are read (dH_part rows are scaled into dH;
  * dW_part / dBias_part are added in the last block's epilogues) and are left unchanged, so a second backward of the
- * same forward gives the same result; an output may also be its own partial sum (in place). Replaces
+ * same forward gives the same result; an output may also be its own partial sum (in place). dH and dH_part are
+ * 16-byte aligned with lddh a multiple of 8 (bf16) or 4 (fp32), else MCE_EALIGN. Replaces
  * `_LinearCEMix.backward` (fused_ops.py:159-162): `gh * go`, `gw * go`, `dg * go`, and the last chunk's GEMMs.
  */
 MCE_API int mce_bwd_train(const uint16_t* H, int64_t ldh, const float* go, const float* dgr_rows, int64_t N,

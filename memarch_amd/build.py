@@ -1,8 +1,7 @@
-"""Build recipe for the HIP library `libmce.so` (gfx950 only), and for `libmce_probe.so`, the MFMA-rate probe that
-bench.py --calibrate-mfma runs (a measurement aid, not part of the operator's C ABI).
+"""Build recipe for the HIP library `libmce.so` (gfx950 only).
 
-Run `python -m memarch_amd.build` (or `__graft_entry__.build()`). The libraries are written in-tree next to this
-file so that they travel with the source tree; they are plain C-ABI shared objects loaded through ctypes.
+Run `python -m memarch_amd.build` (or `__graft_entry__.build()`). The library is written in-tree next to this file
+so that it travels with the source tree; it is a plain C-ABI shared object loaded through ctypes.
 """
 import os
 import subprocess
@@ -12,8 +11,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRCS = [os.path.join(HERE, "csrc", f) for f in ("mce.hip", "induct.hip", "swiglu.hip")]
 LIB = os.path.join(HERE, "libmce.so")
-PROBE_SRCS = [os.path.join(HERE, "csrc", "probe.hip")]
-PROBE_LIB = os.path.join(HERE, "libmce_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops off: hipcc may otherwise emit packed fp32 VALU ops on its own.
@@ -26,10 +23,9 @@ FLAGS = [
 
 
 def build(verbose=False):
-    """Compile libmce.so and libmce_probe.so from source every time it is called; raises CalledProcessError on
-    failure. Returns the path of libmce.so."""
+    """Compile libmce.so from source every time it is called; raises CalledProcessError on failure. Returns its
+    path."""
     _compile(SRCS, LIB, verbose)
-    _compile(PROBE_SRCS, PROBE_LIB, verbose)
     return LIB
 
 

@@ -782,6 +782,13 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
 // ids outside [0, V_real) are ignored.
 constexpr int MAX_KC = 64;  // sparse candidates per row (the reference's phrasebook passes 32, prior_top.py:4)
 
+// Marker of k_row_logits' cb for a slot that is not the first of a valid id: a signalling-NaN bit pattern. Arithmetic
+// never yields it (an fp32 add quiets a signalling NaN), so a first slot whose total bias is itself NaN (a NaN cval,
+// or +inf and -inf on one id) is not mistaken for it: that NaN reaches the row's lse and loss, as the reference's
+// scatter_add makes the row NaN (full2.py:1920-1922). Consumers compare the bits.
+constexpr uint32_t CB_SKIP_BITS = 0x7FA0F00Du;
+__device__ __forceinline__ bool cb_skip(float b) { return __float_as_uint(b) == CB_SKIP_BITS; }
+
 // Total sparse bias of row n on vocabulary id c (0 when c is not a candidate).
 __device__ __forceinline__ float sparse_bias(const int64_t* cand, const float* cval, int kc, int64_t n, int64_t c) {
   float b = 0.f;
@@ -849,7 +856,8 @@ __device__ __forceinline__ void row_dot4(const uint16_t* hr, const uint16_t* con
 // Per-row logits at the target and at the sparse candidates (h . w + bias, fp32 dot products of the bf16 rows):
 //   xy[n]    = x(n, y_n) + the sparse bias on y_n     (-inf when y_n is outside [0, V_real))
 //   xc[n, k] = x(n, cand[n, k]) without sparse bias   (-inf for ids outside [0, V_real); only when kc > 0)
-//   cb[n, k] = the total sparse bias on cand[n, k] where k is the first slot of a valid id, else NaN (kc > 0)
+//   cb[n, k] = the total sparse bias on cand[n, k] where k is the first slot of a valid id, else the CB_SKIP_BITS
+//              marker (kc > 0)
 // One wave per row; lane k holds candidate k for the row's summary (kc <= 64 = the wave), and the candidates' dot
 // products run four at a time. The tile kernels compute the same sums in another order; the two agree to fp32
 // rounding.
@@ -875,7 +883,7 @@ __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__
     cand_summary(ck, vk, kc, lane, btot, first);
     for (int j = 0; j < kc; ++j)
       if (shfl_i64(ck, j) == yn) by += __shfl(vk, j);
-    if (lane < kc) cb[n * kc + lane] = (ck >= 0 && ck < Vreal && first == lane) ? btot : __builtin_nanf("");
+    if (lane < kc) cb[n * kc + lane] = (ck >= 0 && ck < Vreal && first == lane) ? btot : __uint_as_float(CB_SKIP_BITS);
   }
   float x = -INFINITY;
   if (yn >= 0 && yn < Vreal) x = row_dot(hr, W + yn * ldw, K, lane) + (bias != nullptr ? bias[yn] : 0.f) + by;
@@ -967,10 +975,10 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
       if (kc > 0) {
         float Mp = M;
         for (int k = 0; k < kc; ++k)
-          if (!__builtin_isnan(cb[n * kc + k])) Mp = fmaxf(Mp, xc[n * kc + k] + cb[n * kc + k]);
+          if (!cb_skip(cb[n * kc + k])) Mp = fmaxf(Mp, xc[n * kc + k] + cb[n * kc + k]);
         float Sp = M == -INFINITY ? 0.f : S * expf(M - Mp), removed = 0.f;
         for (int k = 0; k < kc; ++k)
-          if (!__builtin_isnan(cb[n * kc + k])) {
+          if (!cb_skip(cb[n * kc + k])) {
             const float x = xc[n * kc + k], B = cb[n * kc + k];
             // exp(x + B - M') - exp(x - M'); expm1 keeps small |B| exact (and would overflow for large B)
             Sp += B < 20.f ? expf(x - Mp) * expm1f(B) : expf(x + B - Mp) - expf(x - Mp);
@@ -1548,8 +1556,8 @@ __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_
     bool neg = false;
     float mx = x;
     for (int k = 0; k < kc; ++k) {
-      const float B = cb[n * kc + k];  // NaN: not the first slot of a valid id
-      if (__builtin_isnan(B)) continue;
+      const float B = cb[n * kc + k];
+      if (cb_skip(B)) continue;  // not the first slot of a valid id
       if (cand[n * kc + k] < BM && B < 0.f) neg = true;
       mx = fmaxf(mx, xc[n * kc + k] + B);
     }
@@ -1675,7 +1683,7 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
     const float B = cb[n * kc + k];
-    if (c == yn || __builtin_isnan(B)) continue;
+    if (c == yn || cb_skip(B)) continue;
     G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + B - e));
   }
 }
@@ -1770,7 +1778,7 @@ __global__ __launch_bounds__(256) void k_exact_fix(const int* __restrict__ count
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
     const float B = cb[n * kc + k];
-    if (c == yn || __builtin_isnan(B)) continue;
+    if (c == yn || cb_skip(B)) continue;
     G[cm_index(n, c, Np)] = to_bf16(expf(xc[n * kc + k] + B - l));
   }
 }
@@ -2127,6 +2135,11 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int fold_nr(int64_t tiles_n) { return tiles_n >= 8 ? 1 : (int)cdiv(8, tiles_n); }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// dH and dH_part of the training path (k_scale_rows moves them 16 bytes at a time): null, or 16-byte aligned with a
+// row stride of whole 16-byte units (8 bf16 or 4 fp32 values)
+inline bool dh_aligned(const void* p, int64_t ld, int bf16) {
+  return p == nullptr || (aligned16(p) && ld % (bf16 ? 8 : 4) == 0);
+}
 
 struct FwdWs {
   float *part_m, *part_s, *xy, *xc, *cb, *sum_part;
@@ -2157,7 +2170,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V, int kslots) {
 //   Wt  [Vp/256][K][256]  bf16 (W^T, K-blocked),  Ht [Np/256][K][256] bf16 (H^T, K-blocked)
 //   dbias_part [2*Np/256][Vp] fp32, xy [Np] fp32 (target logits), part [TAIL_SLOTS][256][256] fp32 (K-split
 //   tails), ty int32 / tval fp32 [Np] (k_target_fix)
-//   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), cb [Np][MAX_KC] fp32 (their total biases, NaN past
+//   sparse bias only: xc [Np][MAX_KC] fp32 (candidate logits), cb [Np][MAX_KC] fp32 (their total biases, CB_SKIP_BITS past
 //   the first slot of an id), fix_col int32 / fix_val fp32 [Np][MAX_KC]
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
@@ -2656,11 +2669,12 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   }
   if (!y || !loss_rows || !lse_rows || !wgt_rows || (gate && !dgr_rows) || !ws) return MCE_EINVAL;
   const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V, block_rows);
-  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const bool more = w.nblk > 1;  // blocks before the last one write the partial sums
   if (more && (((want & MCE_GRAD_H) && (!dH_part || lddh < K)) || ((want & MCE_GRAD_W) && (!dW_part || lddw < K)) ||
                ((want & MCE_GRAD_BIAS) && !dBias_part)))
     return MCE_EINVAL;
+  if (more && (want & MCE_GRAD_H) && !dh_aligned(dH_part, lddh, dh_bf16)) return MCE_EALIGN;
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)(w.vp / BM), tn = (int)cdiv(N, BN);
   const Operand Wop{W, ldw, V, K, 0};
   const bool kf = K % BK == 0;
@@ -2760,6 +2774,7 @@ int bwd_train_impl(const uint16_t* H, int64_t ldh, const float* go, const float*
   if (rc) return rc;
   if (block_rows < 0 || (dH && lddh < K) || (dW && lddw < K)) return MCE_EINVAL;
   if ((dH || dW || dBias || dGate) && go == nullptr) return MCE_EINVAL;
+  if (dH && (!dh_aligned(dH, lddh, dh_bf16) || !dh_aligned(dH_part, lddh, dh_bf16))) return MCE_EALIGN;
   if (N == 0) {
     if (dW) {
       hipLaunchKernelGGL(k_fill2d_f32, dim3((unsigned)cdiv(V * K, 256)), dim3(256), 0, st, dW, lddw, V, K, 0.f);

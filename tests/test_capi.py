@@ -140,3 +140,30 @@ def test_induct_long_argument_checks(lib):
     assert lib.mce_induct_ws(*args(9000, B=0, x=None, ws=None)) == 0   # no texts
     assert lib.mce_induct_ws(*args(16, locks=4, ws=None)) == 1    # T <= 8192: mce_induct's checks
     assert lib.mce_induct_ws(*args(16, x=None, ws=None)) == 1
+
+
+def test_training_dh_alignment_checks(lib):
+    """dH and dH_part of the training path are moved 16 bytes at a time: a misaligned pointer or a row stride that
+    is not a whole number of 16-byte units is rejected with MCE_EALIGN before any HIP call."""
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256
+    ws = 16        # a workspace too small: a call that passes the alignment checks returns MCE_EWORKSPACE, before
+                   # any HIP call
+
+    def bwd(dh, lddh, bf16=1, part=None):
+        return lib.mce_bwd_train(p, 8, p, p, 600, 8, 32, 256, part, None, None, dh, bf16, lddh, None, 8, None, None,
+                                 p, ws, None)
+
+    assert bwd(p + 2, 8) == 2                    # misaligned dH
+    assert bwd(p, 12) == 2                       # bf16 rows 24 bytes apart
+    assert bwd(p, 10, bf16=0) == 2               # fp32 rows 40 bytes apart
+    assert bwd(p, 8, part=p + 4) == 2            # misaligned dH_part
+    assert bwd(p, 12, bf16=0) == 3               # fp32 rows 48 bytes apart are fine
+
+    def fwd(part, lddh, bf16=1, block_rows=256):
+        return lib.mce_fwd_train(p, 8, p, 8, None, 0, None, p, p, p, 600, 8, 32, 32, block_rows, 1, p, p, p, p, p,
+                                 part, bf16, lddh, None, 8, None, p, ws, None)
+
+    assert fwd(p + 2, 8) == 2                    # three blocks: dH_part is used
+    assert fwd(p, 12) == 2
+    assert fwd(p + 2, 8, block_rows=0) == 3      # one block: dH_part is not used

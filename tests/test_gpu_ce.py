@@ -234,3 +234,35 @@ def test_sparse_dominant_candidate_negative_bias(mode, monkeypatch):
     print(f"lse max abs err {np.abs(lse - fwd['lse']).max():.2e}", flush=True)
     assert np.abs(lse - fwd["lse"]).max() <= 1e-3
     _check(f"dominant candidate {mode}", loss, fwd, dict(dh=h.grad, dw=w.grad, dcval=b.grad), bwd)
+
+
+@pytest.mark.parametrize("mode", ["one_pass", "recompute", "blocks"])
+def test_sparse_nan_value_makes_its_row_nan(mode, monkeypatch):
+    """A NaN sparse value (row 5) and +inf and -inf summed on one id (row 300) make the total bias of a candidate
+    NaN: as with the reference's scatter_add (full2.py:1920-1922), those rows' lse and loss are NaN, the loss sum is
+    NaN, and every other row is unaffected."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", mode == "recompute")
+    if mode == "blocks":
+        monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256)
+    c = _case(600, 128, 900, 3, seed=33)
+    c["cand"][5, 0], c["cand"][300, 1], c["cand"][300, 2] = 17, 40, 40
+    c["cval"][5, 0] = float("nan")
+    c["cval"][300, 1], c["cval"][300, 2] = float("inf"), float("-inf")
+    print(f"nan sparse value, {mode}", flush=True)
+    h, w, y = c["h"].cuda().bfloat16(), c["w"].cuda(), c["y"].cuda()
+    cand, cval = c["cand"].cuda(), c["cval"].cuda()
+    rows = fused_ops.forward_rows(h, w, y, None, None, cand=cand, cval=cval)
+    loss_rows, lse = rows["loss_rows"].cpu(), rows["lse"].cpu()
+    bad = torch.zeros(600, dtype=torch.bool)
+    bad[[5, 300]] = True
+    assert torch.isnan(loss_rows[bad]).all() and torch.isnan(lse[bad]).all()
+    assert torch.isfinite(loss_rows[~bad]).all()
+    keep = (~bad).numpy()
+    ck = {k: (v[~bad] if isinstance(v, torch.Tensor) and v.shape[:1] == (600,) else v) for k, v in c.items()}
+    fwd, _ = _oracle(ck)
+    assert orc.rel_fro(loss_rows[~bad].numpy(), fwd["loss_rows"]) <= LOSS_RTOL
+    assert orc.rel_fro(lse[keep].numpy(), fwd["lse"]) <= LOSS_RTOL
+    hg, wg, bg = h.clone().requires_grad_(), w.clone().requires_grad_(), cval.clone().requires_grad_()
+    loss = fused_ops.linear_ce_sparse(hg, wg, y, cand, bg)
+    assert torch.isnan(loss).item()
