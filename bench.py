@@ -44,11 +44,14 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 
 # C-ABI call -> stage. One-pass path (default): mce_fwd_train (row blocks: logits tiles, merge, and every block
 # but the last its dH / dW contractions), mce_bwd_train (the last block's contractions); recompute path: mce_fwd,
-# mce_bwd_logits_grad, mce_bwd_dhidden, mce_bwd_dweight.
+# then mce_bwd_blocked (per row block: the logits recomputed into G, its dH rows, dW and dBias accumulated) or, for
+# chunk_ce, mce_lse_fwd and mce_bwd_lse_blocked; --stage-reps times the separate steps mce_bwd_logits_grad,
+# mce_bwd_dhidden, mce_bwd_dweight.
 STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_sparse": "fwd",
                  "mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
                  "mce_bwd_dweight": "dweight", "mce_fwd_sparse": "fwd", "mce_bwd_logits_grad_sparse": "logits_grad",
-                 "mce_lse_fwd": "fwd", "mce_bwd_lse_grad": "logits_grad"}
+                 "mce_lse_fwd": "fwd", "mce_bwd_lse_grad": "logits_grad", "mce_bwd_blocked": "bwd",
+                 "mce_bwd_lse_blocked": "bwd"}
 # kernel classes of mce_prof_stop (include/mce.h) -> kernel name; each class runs one N x V x d contraction per step
 PROF_KERNELS = ("k_fwd_train<true>", "k_fwd_tiles<true>", "k_bwd_grad<true>", "k_gemm<true, true, 1, 0>",
                 "k_gemm<false, true, 2, {nr}>")

@@ -190,6 +190,44 @@ MCE_API int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t l
             float* dBias, float* dGate, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The recompute backward in row blocks, with a workspace bounded by one block whatever N is. Each block of rows
+ * runs the three steps above on its own rows: the logits recomputed and its G written (mce_bwd_logits_grad), its
+ * dH rows (mce_bwd_dhidden), and its dW and dBias added to the earlier blocks' sums in the GEMM epilogues (the
+ * first block writes them). Blocks: `block_rows` rows each (rounded up to a multiple of 256 and evened out over
+ * the blocks), or, with block_rows = 0, as many as keep the whole workspace within 2 GiB: 16384-row blocks for
+ * 32768 rows at d = 2048, V = 50304; 5632-row blocks at V = 131072. mce_bwd_block_rows gives the rows per block
+ * (the last block holds the rest), mce_bwd_blocked_ws_bytes the workspace (256-byte aligned).
+ * No counterpart in the reference for the sizing functions.
+ */
+MCE_API int64_t mce_bwd_block_rows(int64_t N, int64_t K, int64_t V, int64_t block_rows);
+MCE_API size_t mce_bwd_blocked_ws_bytes(int64_t N, int64_t K, int64_t V, int64_t block_rows);
+
+/*
+ * The whole recompute backward, block by block, for the mixture (dgr_rows, dGate), plain cross-entropy and, with
+ * kc > 0 candidates, the sparse logit bias (dCval [N, kc], as mce_bwd_logits_grad_sparse; dgr_rows and dGate must
+ * then be NULL). dH (bf16 or fp32, row stride lddh), dW (fp32 [V, K], row stride lddw), dBias, dGate, dCval may each
+ * be NULL. Replaces `_LinearCEMix.backward` / `_LinearCESparse.backward` of the recompute design and, like the
+ * vocabulary-chunk loop of `_ChunkCE.backward` (full2.py:806-830), holds one block of G at a time.
+ */
+MCE_API int mce_bwd_blocked(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                            const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
+                            const float* wgt_rows, const float* dgr_rows, const float* go, int64_t N, int64_t K,
+                            int64_t V, int64_t V_real, int64_t block_rows, void* dH, int dh_bf16, int64_t lddh,
+                            float* dW, int64_t lddw, float* dBias, float* dGate, float* dCval, void* ws,
+                            size_t ws_bytes, void* stream);
+
+/*
+ * The whole backward of `chunk_ce` (full2.py:792-830), block by block: G = g_lse softmax + g_ly onehot per block
+ * (as mce_bwd_lse_grad), dH rows, and dW and dBias summed over the blocks. Replaces `_ChunkCE.backward`
+ * (full2.py:806-830), whose loop holds one vocabulary chunk of G at a time.
+ */
+MCE_API int mce_bwd_lse_blocked(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                                const int64_t* y, const float* lse_rows, const float* g_lse, const float* g_ly,
+                                int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows, void* dH,
+                                int dh_bf16, int64_t lddh, float* dW, int64_t lddw, float* dBias, void* ws,
+                                size_t ws_bytes, void* stream);
+
+/*
  * One-pass training path (mixture or plain cross-entropy, optionally a sparse bias). The reference computes its
  * gradients during the forward, 4096 rows at a time (fused_ops.py:148-155); so does this path, in row blocks,
  * without materialising logits and without a second pass over them. For each block the forward's tile kernel

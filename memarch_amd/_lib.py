@@ -36,6 +36,12 @@ SIGNATURES = {
     "mce_bwd_dweight": (_INT, [_P, _I, _I, _I, _I, _P, _I, _P, _S, _P]),
     "mce_bwd": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _P,
                        _S, _P]),
+    "mce_bwd_block_rows": (_I, [_I, _I, _I, _I]),
+    "mce_bwd_blocked_ws_bytes": (_S, [_I, _I, _I, _I]),
+    "mce_bwd_blocked": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _INT, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _INT, _I,
+                               _P, _I, _P, _P, _P, _P, _S, _P]),
+    "mce_bwd_lse_blocked": (_INT, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P,
+                                   _P, _S, _P]),
     "mce_train_ws_bytes": (_S, [_I, _I, _I, _I]),
     "mce_train_block_rows": (_I, [_I, _I, _I, _I]),
     "mce_fwd_train": (_INT, [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _INT, _P, _P, _P, _P, _P,

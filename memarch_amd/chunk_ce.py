@@ -6,15 +6,17 @@ arbitrary upstream gradients (g_lse, g_ly): the gradient of the logits is G = g_
 giving dh = G W, dW = G^T h and db = sum_n G in the dtypes of h, W and b (None for y and ch).
 
 All device work runs in libmce.so: the forward is the loss head's forward without the loss (mce_lse_fwd), the
-backward recomputes the logits tile by tile (mce_bwd_lse_grad) and runs the two gradient GEMMs of the loss head.
-The N x V logits are never stored and `ch` is accepted and ignored (tiling is internal). The int8 head
+backward (mce_bwd_lse_blocked) recomputes the logits tile by tile and runs the two gradient GEMMs of the loss head,
+one block of rows at a time, so its workspace holds G of one block (the reference's loop holds one vocabulary chunk
+of G, full2.py:806-830). The N x V logits are never stored and `ch` is accepted and ignored (tiling is internal;
+the row blocks follow fused_ops.BLOCK_ROWS). The int8 head
 (`int8mm.HEAD`) and the saved-logits mode (`CE_SAVE`) of the reference are not reproduced: this path always
 recomputes in bf16. A target outside [0, V) gives ly = -inf and no one-hot gradient (the reference's indexing
 W[y] raises for such a row).
 """
 import torch
 
-from . import _lib
+from . import _lib, fused_ops
 from .fused_ops import _BF16, _bf16_operand, _check_cuda, _ptr, _rows, _stream
 
 
@@ -62,23 +64,21 @@ class _ChunkCE(torch.autograd.Function):
         db = torch.empty(v, **f32) if (need_b and bf is not None) else None
         dh = dw = None
         if need_h or need_w or db is not None:
+            # block by block: one block of rows' G in the workspace at a time (fused_ops.BLOCK_ROWS rows, 0: the
+            # library's choice)
             lib = _lib.load()
-            ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)
+            ws_bytes = lib.mce_bwd_blocked_ws_bytes(n, kp, v, fused_ops.BLOCK_ROWS)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-            st = _stream(dev)
-            _lib.call("mce_bwd_lse_grad", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
-                      _ptr(lse), _ptr(gl), _ptr(gy), n, kp, v, v, _ptr(db), _ptr(ws), ws_bytes, st)
+            out_bf16 = hdt == _BF16
+            dhf = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev) if need_h else None
+            dwf = torch.empty(v, kp, **f32) if need_w else None
+            _lib.call("mce_bwd_lse_blocked", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
+                      _ptr(lse), _ptr(gl), _ptr(gy), n, kp, v, v, fused_ops.BLOCK_ROWS, _ptr(dhf), int(out_bf16), kp,
+                      _ptr(dwf), kp, _ptr(db), _ptr(ws), ws_bytes, _stream(dev))
             if need_h:
-                out_bf16 = hdt == _BF16
-                dh = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev)
-                _lib.call("mce_bwd_dhidden", _ptr(wd), wd.stride(0), n, kp, v, _ptr(dh), int(out_bf16), dh.stride(0),
-                          _ptr(ws), ws_bytes, st)
-                dh = dh[:, :k].to(hdt)
+                dh = dhf[:, :k].to(hdt)
             if need_w:
-                dw = torch.empty(v, kp, **f32)
-                _lib.call("mce_bwd_dweight", _ptr(hd), hd.stride(0), n, kp, v, _ptr(dw), dw.stride(0), _ptr(ws),
-                          ws_bytes, st)
-                dw = dw[:, :k].to(wdt)
+                dw = dwf[:, :k].to(wdt)
         if db is not None:
             db = db.to(bdt)
         return dh, dw, db, None, None

@@ -2130,6 +2130,9 @@ __global__ __launch_bounds__(256) void k_dbias_tiles(const float* __restrict__ u
 thread_local int g_last_hip_error = 0;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// p + off, or null for a null p (optional per-row arrays of a row block)
+template <typename T>
+inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
 // Row groups per tile for the dot products of k_gemm<.., DB> over a grid `tiles_n` tiles wide: the 8 row groups of a
 // tile row are spread over its first min(tiles_n, 8) tiles.
 inline int fold_nr(int64_t tiles_n) { return tiles_n >= 8 ? 1 : (int)cdiv(8, tiles_n); }
@@ -2185,19 +2188,23 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.np = cdiv(N, BLK) * BLK;
   w.vp = cdiv(V, BLK) * BLK;
   size_t off = 0;
-  w.G = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * w.np);
-  w.Wt = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.vp * K);
-  w.Ht = reinterpret_cast<uint16_t*>(base + off); off = align256(off + sizeof(uint16_t) * w.np * K);
-  w.dbias_part = reinterpret_cast<float*>(base + off);
-  off = align256(off + sizeof(float) * w.vp * (2 * w.np / BLK));
-  w.xy = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
-  w.ty = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * w.np);
-  w.tval = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np);
-  w.part = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * TAIL_SLOTS * BM * BN);
-  w.xc = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
-  w.cb = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
-  w.fix_col = reinterpret_cast<int*>(base + off); off = align256(off + sizeof(int) * w.np * MAX_KC);
-  w.fix_val = reinterpret_cast<float*>(base + off); off = align256(off + sizeof(float) * w.np * MAX_KC);
+  auto take = [&](size_t bytes) {  // base == nullptr: sizes only
+    char* p = base == nullptr ? nullptr : base + off;
+    off = align256(off + bytes);
+    return p;
+  };
+  w.G = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * w.np));
+  w.Wt = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * K));
+  w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.np * K));
+  w.dbias_part = reinterpret_cast<float*>(take(sizeof(float) * w.vp * (2 * w.np / BLK)));
+  w.xy = reinterpret_cast<float*>(take(sizeof(float) * w.np));
+  w.ty = reinterpret_cast<int*>(take(sizeof(int) * w.np));
+  w.tval = reinterpret_cast<float*>(take(sizeof(float) * w.np));
+  w.part = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * BM * BN));
+  w.xc = reinterpret_cast<float*>(take(sizeof(float) * w.np * MAX_KC));
+  w.cb = reinterpret_cast<float*>(take(sizeof(float) * w.np * MAX_KC));
+  w.fix_col = reinterpret_cast<int*>(take(sizeof(int) * w.np * MAX_KC));
+  w.fix_val = reinterpret_cast<float*>(take(sizeof(float) * w.np * MAX_KC));
   w.bytes = off;
   return w;
 }
@@ -2459,27 +2466,17 @@ int fwd_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, con
   return launch_sum(loss_rows, N, w.sum_part, loss_sum, st);
 }
 
-// Logits gradient of every variant: G into the workspace, plus dBias, dGate (mixture) and dCval
-// (sparse bias) when requested.
-int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
-              const int64_t* cand, const float* cval, int kc, const float* lse_rows, const float* wgt_rows,
-              const float* dgr_rows, const float* ycoef, const float* go, int64_t N, int64_t K, int64_t V,
-              int64_t V_real, float* dBias, float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
-  if (!rc) rc = check_bias(bias);
-  if (!rc) rc = check_sparse(cand, cval, kc, N);
-  if (rc) return rc;
-  if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
-  if (N > 0 && go == nullptr && ycoef == nullptr) return MCE_EINVAL;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (N == 0) {
-    if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
-    return launch_status();
-  }
-  if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows)) return MCE_EINVAL;
-  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
-  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+// The logits-gradient kernels of every variant on a laid-out backward workspace: G of the N rows into w.G, plus
+// dBias (= the column sums of G, plus dbias_in when given: an accumulation, dbias_in may be dBias), dGate (mixture)
+// and dCval (sparse bias) when requested. Arguments already checked.
+int grad_launch(const BwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
+                const float* wgt_rows, const float* dgr_rows, const float* ycoef, const float* go, int64_t N,
+                int64_t K, int64_t V, int64_t V_real, float* dBias, const float* dbias_in, float* dGate, float* dCval,
+                hipStream_t st) {
+  int rc;
   const int tv = (int)cdiv(V, BM), tn = (int)cdiv(N, BN);
+  const int64_t np = cdiv(N, BLK) * BLK;
   const Operand Wop{W, ldw, V, K, 0}, Hop{H, ldh, N, K, 0};
   hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand, cval,
                      kc, N, K, V_real, w.xy, w.xc, w.cb);
@@ -2496,22 +2493,151 @@ int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, co
     ProfScope prof(PROF_BWD_GRAD, st);
     if (K % BK == 0)
       hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G,
+                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, np, V, w.vp, V_real, tv, tn, w.G,
                          dBias ? w.dbias_part : nullptr);
     else
       hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, w.np, V, w.vp, V_real, tv, tn, w.G,
+                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, np, V, w.vp, V_real, tv, tn, w.G,
                          dBias ? w.dbias_part : nullptr);
   }
   if ((rc = launch_status())) return rc;
   if (dBias) {
     hipLaunchKernelGGL(k_dbias_reduce, dim3((unsigned)cdiv(V, 64)), dim3(256), 0, st, w.dbias_part, 2 * tn, w.vp, V,
-                       dBias);
+                       dBias, nullptr, dbias_in);
     if ((rc = launch_status())) return rc;
   }
   if (dGate) {
     hipLaunchKernelGGL(k_dgate, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, dgr_rows, go, N, dGate);
     if ((rc = launch_status())) return rc;
+  }
+  return MCE_OK;
+}
+
+// Arguments of the logits-gradient entry points (every variant)
+int check_grad(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+               const int64_t* cand, const float* cval, int kc, const float* go, const float* ycoef, int64_t N,
+               int64_t K, int64_t V, int64_t V_real, const float* dBias) {
+  int rc = check_common(H, ldh, W, ldw, N, K, V, V_real);
+  if (!rc) rc = check_bias(bias);
+  if (!rc) rc = check_sparse(cand, cval, kc, N);
+  if (rc) return rc;
+  if (dBias != nullptr && bias == nullptr) return MCE_EINVAL;
+  if (N > 0 && go == nullptr && ycoef == nullptr) return MCE_EINVAL;
+  return MCE_OK;
+}
+
+// Logits gradient of every variant: G into the workspace, plus dBias, dGate (mixture) and dCval
+// (sparse bias) when requested.
+int grad_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias, const int64_t* y,
+              const int64_t* cand, const float* cval, int kc, const float* lse_rows, const float* wgt_rows,
+              const float* dgr_rows, const float* ycoef, const float* go, int64_t N, int64_t K, int64_t V,
+              int64_t V_real, float* dBias, float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_grad(H, ldh, W, ldw, bias, cand, cval, kc, go, ycoef, N, K, V, V_real, dBias);
+  if (rc) return rc;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N == 0) {
+    if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
+    return launch_status();
+  }
+  if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows)) return MCE_EINVAL;
+  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), N, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  return grad_launch(w, H, ldh, W, ldw, bias, y, cand, cval, kc, lse_rows, wgt_rows, dgr_rows, ycoef, go, N, K, V,
+                     V_real, dBias, nullptr, dGate, dCval, st);
+}
+
+// The recompute backward in row blocks (mce_bwd_blocked, mce_bwd_lse_blocked): the backward workspace of one block
+// of `nb` rows (bwd_ws_layout), reused block after block, so that it stops growing with N. With block_rows = 0 the
+// rows per block are the most (a multiple of 256) for which that workspace fits in BWD_BLOCK_BUDGET, evened out over
+// the blocks they take; a request is rounded up to a multiple of 256.
+constexpr size_t BWD_BLOCK_BUDGET = size_t(2) << 30;
+int64_t bwd_block_rows(int64_t N, int64_t K, int64_t V, int64_t req) {
+  const int64_t np = cdiv(N, BLK) * BLK;
+  if (np == 0) return BLK;
+  int64_t cap;
+  if (req > 0) {
+    cap = cdiv(req, BLK) * BLK;
+  } else {
+    // the layout's size is affine in the rows: fixed part (W^T, the K-split tail slots) + a per-256-row part
+    const size_t b1 = bwd_ws_layout(nullptr, BLK, K, V).bytes, b2 = bwd_ws_layout(nullptr, 2 * BLK, K, V).bytes;
+    const size_t per = b2 - b1, fixed = b1 - per;
+    cap = BWD_BLOCK_BUDGET > fixed + per ? (int64_t)((BWD_BLOCK_BUDGET - fixed) / per) * BLK : BLK;
+  }
+  if (cap >= np) return np;
+  return cdiv(cdiv(np, cdiv(np, cap)), BLK) * BLK;
+}
+
+// dH rows, then dW (and nothing else) of one block whose G is in the workspace: dH rows [0, N) of the block into dH
+// (bf16 or fp32), dW = G^T H (+ dW_in when given: an accumulation, dW_in may be dW). Wt (W^T, K-blocked) must already
+// be in the workspace for dH.
+int block_contractions(const BwdWs& w, const uint16_t* H, int64_t ldh, int64_t N, int64_t K, int64_t V, void* dH,
+                       int dh_bf16, int64_t lddh, float* dW, int64_t lddw, const float* dW_in, hipStream_t st) {
+  int rc;
+  const int64_t np = cdiv(N, BLK) * BLK;
+  if (dH != nullptr) {
+    const Operand Aop{w.G, 0, N, w.vp, np * BLK, 1};
+    const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
+    const int nk = (int)(w.vp / BK);
+    rc = dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st, nullptr, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, nullptr, PROF_GEMM_DH)
+                 : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st, nullptr, nullptr, nullptr, nullptr,
+                                      nullptr, nullptr, nullptr, PROF_GEMM_DH);
+    if (rc) return rc;
+  }
+  if (dW == nullptr) return MCE_OK;
+  hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(np / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, H, ldh,
+                     N, K, w.Ht, nullptr, nullptr, nullptr, 1);
+  if ((rc = launch_status())) return rc;
+  const Operand Aop{w.G, np * BLK, V, np, CM_TILE, 2};
+  const Operand Bop{w.Ht, BLK, K, np, K * BLK, 0};
+  return launch_gemm<false>(Aop, Bop, (int)(np / BK), V, K, 4, dW, lddw, w.part, st, nullptr, nullptr, dW_in, nullptr,
+                            nullptr, nullptr, nullptr, PROF_GEMM_DW);
+}
+
+// The whole recompute backward of every variant, block by block: per block the logits gradient (grad_launch),
+// the block's dH rows and its dW, with dW and dBias accumulated over the blocks through the epilogues (the first
+// block writes them). go may be null when ycoef is given (chunk_ce: wgt_rows = g_lse, ycoef = g_ly).
+int bwd_blocked_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                     const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
+                     const float* wgt_rows, const float* dgr_rows, const float* ycoef, const float* go, int64_t N,
+                     int64_t K, int64_t V, int64_t V_real, int64_t block_rows, void* dH, int dh_bf16, int64_t lddh,
+                     float* dW, int64_t lddw, float* dBias, float* dGate, float* dCval, void* ws, size_t ws_bytes,
+                     void* stream) {
+  int rc = check_grad(H, ldh, W, ldw, bias, cand, cval, kc, go, ycoef, N, K, V, V_real, dBias);
+  if (rc) return rc;
+  if (block_rows < 0 || (dH && lddh < K) || (dW && lddw < K)) return MCE_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (N == 0) {
+    if (dW) {
+      hipLaunchKernelGGL(k_fill2d_f32, dim3((unsigned)cdiv(V * K, 256)), dim3(256), 0, st, dW, lddw, V, K, 0.f);
+      if ((rc = launch_status())) return rc;
+    }
+    if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
+    return launch_status();
+  }
+  if (!y || !lse_rows || !wgt_rows || !ws || (dGate && !dgr_rows) || (dCval && kc == 0)) return MCE_EINVAL;
+  const int64_t nb = bwd_block_rows(N, K, V, block_rows);
+  const BwdWs w = bwd_ws_layout(reinterpret_cast<char*>(ws), nb, K, V);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  if (dH) {
+    // Wt = W^T, K-blocked, once for all blocks
+    hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
+                       ldw, V, K, w.Wt);
+    if ((rc = launch_status())) return rc;
+  }
+  for (int64_t row0 = 0; row0 < N; row0 += nb) {
+    const int64_t rows = std::min(nb, N - row0);
+    const bool first = row0 == 0;
+    if ((rc = grad_launch(w, H + row0 * ldh, ldh, W, ldw, bias, y + row0, at(cand, row0 * kc), at(cval, row0 * kc),
+                          kc, lse_rows + row0, wgt_rows + row0, at(dgr_rows, row0), at(ycoef, row0), go, rows, K, V,
+                          V_real, dBias, first ? nullptr : dBias, at(dGate, row0), at(dCval, row0 * kc), st)))
+      return rc;
+    void* dh_rows = dH == nullptr ? nullptr
+                    : dh_bf16     ? (void*)(reinterpret_cast<uint16_t*>(dH) + row0 * lddh)
+                                  : (void*)(reinterpret_cast<float*>(dH) + row0 * lddh);
+    if ((rc = block_contractions(w, H + row0 * ldh, ldh, rows, K, V, dh_rows, dh_bf16, lddh, dW, lddw,
+                                 first ? nullptr : dW, st)))
+      return rc;
   }
   return MCE_OK;
 }
@@ -2587,9 +2713,6 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
 }
 
 std::atomic<float> g_train_s_max{TRAIN_S_MAX};  // test hook: mce_train_set_threshold
-
-template <typename T>
-inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
 
 // The gradient contractions of row block b: dH rows = s * a_n (E' W) into dH (bf16 or fp32, row stride lddh);
 // dW = s (E'^T (a . H) + dW_in) and dBias = s (E'^T a + dBias_in), with s = go[0] (1 when go is null); any output may
@@ -3011,6 +3134,39 @@ int mce_bwd(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, cons
   if (dH && (rc = mce_bwd_dhidden(W, ldw, N, K, V, dH, dh_bf16, lddh, ws, ws_bytes, stream))) return rc;
   if (dW && (rc = mce_bwd_dweight(H, ldh, N, K, V, dW, lddw, ws, ws_bytes, stream))) return rc;
   return MCE_OK;
+}
+
+int64_t mce_bwd_block_rows(int64_t N, int64_t K, int64_t V, int64_t block_rows) {
+  if (N < 0 || K <= 0 || V <= 0 || block_rows < 0) return 0;
+  return bwd_block_rows(N, K, V, block_rows);
+}
+
+size_t mce_bwd_blocked_ws_bytes(int64_t N, int64_t K, int64_t V, int64_t block_rows) {
+  if (N < 0 || K <= 0 || V <= 0 || block_rows < 0) return 0;
+  return bwd_ws_layout(nullptr, bwd_block_rows(N, K, V, block_rows), K, V).bytes;
+}
+
+int mce_bwd_blocked(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                    const int64_t* y, const int64_t* cand, const float* cval, int kc, const float* lse_rows,
+                    const float* wgt_rows, const float* dgr_rows, const float* go, int64_t N, int64_t K, int64_t V,
+                    int64_t V_real, int64_t block_rows, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
+                    float* dBias, float* dGate, float* dCval, void* ws, size_t ws_bytes, void* stream) {
+  if (N > 0 && go == nullptr) return MCE_EINVAL;
+  if (kc > 0 && (dgr_rows != nullptr || dGate != nullptr)) return MCE_EINVAL;  // the sparse bias is plain CE
+  return bwd_blocked_impl(H, ldh, W, ldw, bias, y, cand, cval, kc, lse_rows, wgt_rows, dgr_rows, nullptr, go, N, K,
+                          V, V_real, block_rows, dH, dh_bf16, lddh, dW, lddw, dBias, dGate, dCval, ws, ws_bytes,
+                          stream);
+}
+
+int mce_bwd_lse_blocked(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
+                        const int64_t* y, const float* lse_rows, const float* g_lse, const float* g_ly, int64_t N,
+                        int64_t K, int64_t V, int64_t V_real, int64_t block_rows, void* dH, int dh_bf16,
+                        int64_t lddh, float* dW, int64_t lddw, float* dBias, void* ws, size_t ws_bytes,
+                        void* stream) {
+  if (N > 0 && (g_lse == nullptr || g_ly == nullptr)) return MCE_EINVAL;
+  return bwd_blocked_impl(H, ldh, W, ldw, bias, y, nullptr, nullptr, 0, lse_rows, g_lse, nullptr, g_ly, nullptr, N,
+                          K, V, V_real, block_rows, dH, dh_bf16, lddh, dW, lddw, dBias, nullptr, nullptr, ws,
+                          ws_bytes, stream);
 }
 
 size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V, int64_t block_rows) {

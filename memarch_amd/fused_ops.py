@@ -259,29 +259,22 @@ def _backward(ctx, go, need_h, need_w, need_b, need_g, need_c=False):
             _lib.call("mce_bwd_train_dcval", _ptr(y64), _ptr(c64), _ptr(cv32), c64.shape[1], _ptr(lse), _ptr(wgt),
                       _ptr(go32), n, kp, v, v_real, state["block_rows"], _ptr(dcval), _ptr(tws), nb, st)
     elif need_h or need_w or need_g or dbias is not None or dcval is not None:
+        # the recompute backward, block by block (its workspace bounded by one block of rows)
         lib = _lib.load()
-        ws_bytes = lib.mce_bwd_ws_bytes(n, kp, v)
+        ws_bytes = lib.mce_bwd_blocked_ws_bytes(n, kp, v, BLOCK_ROWS)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        st = _stream(dev)
-        if c64 is not None:
-            _lib.call("mce_bwd_logits_grad_sparse", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf),
-                      _ptr(y64), _ptr(c64), _ptr(cv32), c64.shape[1], _ptr(lse), _ptr(wgt), _ptr(go32), n, kp, v,
-                      v_real, _ptr(dbias), _ptr(dcval), _ptr(ws), ws_bytes, st)
-        else:
-            _lib.call("mce_bwd_logits_grad", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64),
-                      _ptr(lse), _ptr(wgt), _ptr(dgr), _ptr(go32), n, kp, v, v_real, _ptr(dbias), _ptr(dgate),
-                      _ptr(ws), ws_bytes, st)
+        out_bf16 = hdt == _BF16
+        dhf = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev) if need_h else None
+        dwf = torch.empty(v, kp, **f32) if need_w else None
+        sparse = c64 is not None
+        _lib.call("mce_bwd_blocked", _ptr(hd), hd.stride(0), _ptr(wd), wd.stride(0), _ptr(bf), _ptr(y64), _ptr(c64),
+                  _ptr(cv32), c64.shape[1] if sparse else 0, _ptr(lse), _ptr(wgt), None if sparse else _ptr(dgr),
+                  _ptr(go32), n, kp, v, v_real, BLOCK_ROWS, _ptr(dhf), int(out_bf16), kp, _ptr(dwf), kp,
+                  _ptr(dbias), _ptr(dgate), _ptr(dcval), _ptr(ws), ws_bytes, _stream(dev))
         if need_h:
-            out_bf16 = hdt == _BF16
-            dh = torch.empty(n, kp, dtype=_BF16 if out_bf16 else torch.float32, device=dev)
-            _lib.call("mce_bwd_dhidden", _ptr(wd), wd.stride(0), n, kp, v, _ptr(dh), int(out_bf16), dh.stride(0),
-                      _ptr(ws), ws_bytes, st)
-            dh = dh[:, :k].to(hdt)
+            dh = dhf[:, :k].to(hdt)
         if need_w:
-            dw = torch.empty(v, kp, **f32)
-            _lib.call("mce_bwd_dweight", _ptr(hd), hd.stride(0), n, kp, v, _ptr(dw), dw.stride(0), _ptr(ws),
-                      ws_bytes, st)
-            dw = dw[:, :k].to(wdt)
+            dw = dwf[:, :k].to(wdt)
     if dgate is not None:
         dgate = dgate.to(gdt)
     if dbias is not None:

@@ -167,3 +167,37 @@ def test_training_dh_alignment_checks(lib):
     assert fwd(p + 2, 8) == 2                    # three blocks: dH_part is used
     assert fwd(p, 12) == 2
     assert fwd(p + 2, 8, block_rows=0) == 3      # one block: dH_part is not used
+
+
+def test_recompute_blocks_bound_the_workspace(lib):
+    """The blocked recompute backward (mce_bwd_blocked): rows per block (the whole workspace within 2 GiB) and a
+    workspace that stops growing with N beyond one block, against the unblocked one (G for all rows)."""
+    rows = lambda n, v, req=0: lib.mce_bwd_block_rows(n, 2048, v, req)
+    ws = lambda n, v, req=0: lib.mce_bwd_blocked_ws_bytes(n, 2048, v, req)
+    assert rows(32768, 50304) == 16384 and rows(16384, 50304) == 16384
+    assert rows(32768, 131072) == 5632
+    assert rows(777, 1000, 256) == 256 and rows(300, 1000) == 512
+    for v in (50304, 131072):
+        for n in (32768, 65536, 1 << 20):
+            assert ws(n, v) <= 2 ** 31
+        assert ws(65536, v) == ws(32768, v)       # the same block size: the same workspace
+        assert ws(32768, v) < lib.mce_bwd_ws_bytes(32768, 2048, v) / 1.8
+    assert ws(-1, 1000) == 0 and rows(10, 1000, -1) == 0
+
+
+def test_recompute_blocks_argument_checks(lib):
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256
+
+    def call(kc=0, dgr=None, go=p, block_rows=256, nb=16, lddh=8):
+        return lib.mce_bwd_blocked(p, 8, p, 8, None, p, p if kc else None, p if kc else None, kc, p, p, dgr, go, 600,
+                                   8, 32, 32, block_rows, p, 1, lddh, None, 8, None, None, None, p, nb, None)
+
+    assert call() == 3                           # workspace too small: every check passed, no HIP call made
+    assert call(kc=2, dgr=p) == 1                # the sparse bias is plain cross-entropy
+    assert call(go=None) == 1                    # no upstream gradient
+    assert call(block_rows=-1) == 1
+    assert call(lddh=4) == 1                     # lddh < K
+    assert call(kc=65) == 1
+    assert lib.mce_bwd_lse_blocked(p, 8, p, 8, None, p, p, None, p, 600, 8, 32, 32, 0, p, 1, 8, None, 8, None, p, 16,
+                                   None) == 1    # g_lse missing

@@ -126,16 +126,16 @@ SPARSE = [
 ]
 
 
-@pytest.mark.parametrize("mode", ["one_pass", "recompute", "fallback", "blocks"])
+@pytest.mark.parametrize("mode", ["one_pass", "recompute", "fallback", "blocks", "recompute_blocks"])
 @pytest.mark.parametrize("shape", SPARSE, ids=lambda s: "N{}_K{}_V{}_kc{}_s{}".format(*s))
 def test_linear_ce_sparse_parity(shape, mode, monkeypatch):
     """one_pass: mce_fwd_train_sparse (the candidates' E' entries from their biased logits, mce_bwd_train_dcval);
-    recompute: mce_fwd_sparse + mce_bwd_logits_grad_sparse; fallback: the one-pass path with every row flagged
-    from the host, so every E' row comes from the exact pass with the sparse bias added; blocks: the one-pass path
-    in 256-row blocks."""
+    recompute: mce_fwd_sparse + mce_bwd_blocked with the sparse bias (one block); fallback: the one-pass path with
+    every row flagged from the host, so every E' row comes from the exact pass with the sparse bias added; blocks:
+    the one-pass path in 256-row blocks; recompute_blocks: the recompute backward in 256-row blocks."""
     from memarch_amd import _lib, fused_ops
-    monkeypatch.setattr(fused_ops, "RECOMPUTE", mode == "recompute")
-    if mode == "blocks":
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", mode.startswith("recompute"))
+    if mode.endswith("blocks"):
         monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256)
     N, K, V, kc, scale = shape
     print(f"linear_ce_sparse {shape} {mode}", flush=True)
