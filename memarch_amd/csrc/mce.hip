@@ -382,6 +382,19 @@ __device__ __forceinline__ void mma16(f32x16 (&acc)[4][4], const bf16x8 (&a)[4],
     for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
 }
 
+// 32 wait states: the results of every MFMA issued before are written before the next instruction reads them (a
+// 32x32x16 bf16 MFMA needs fewer before a VALU read of its result). gemm_tile ends with it, because the
+// epilogues read the accumulators through acc_read, an inline asm that the compiler's hazard handling does not see.
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
+// An accumulator value read from its AGPR at this point of the program (an epilogue's use). Left to itself the
+// compiler copies all 256 accumulators of a wave into VGPRs at the start of an epilogue, which then needs every
+// VGPR and spills; an explicit read per use keeps a few values live at a time.
+__device__ __forceinline__ float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
 // Interleave the current scheduling region: one LDS read between two MFMAs (AM = 2: the 12 reads of a slice with
 // transposing A reads, three per four MFMAs).
 template <int AM = 0>
@@ -691,6 +704,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   if (kt < nk) gemm_stage<0, KF, DB, AM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   wait_vmcnt<0>();
   __syncthreads();
+  mfma_drain();
 }
 
 // Tile-rows per group of the logits tile kernels (k_fwd_tiles, k_bwd_grad, k_fwd_train): an XCD's 32 resident tiles
@@ -721,6 +735,7 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group,
 
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
 
+
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 // two floats -> two bf16 (round to nearest even) in one 32-bit word, lo in the low half (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -732,24 +747,86 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
 
 // ---------------------------------------------------------------------------------------------------------
+// The target logit x(n, y_n) from the logits tile's own accumulators, so that a row's lse and its target logit come
+// from the same fp32 sums (k_row_logits' dot product of the same row differs from them by fp32 rounding, which a
+// row whose p_y is near 1 would see in its loss). xy == null: not wanted.
+struct TargetArgs {
+  const int64_t* y;
+  const int64_t* cand;  // the sparse bias (kc > 0): the tile's logits are without it, so the target's is added
+  const float* cval;
+  int kc;
+  float* xy;
+};
+// Local index of row n's target among a lane's vocabulary rows of a wave (vw: the wave's first row; element (mi, r)
+// of lane half lh is row vw + mi*32 + 8(r/4) + 4lh + r%4, local index mi*32 + 8(r/4) + r%4), -1 when it is not
+// one of them: a row of the other lane half gives an index with bit 2 set (or a negative one), so exactly one lane
+// of the wave holds each target of its rows.
+__device__ __forceinline__ int target_local(const TargetArgs& ta, int64_t n, int64_t N, int64_t Vreal, int64_t vw,
+                                            int lh) {
+  if (ta.xy == nullptr || n >= N) return -1;
+  const int64_t yn = ta.y[n];
+  const int64_t d = yn - vw - 4 * lh;
+  return (yn >= 0 && yn < Vreal && d >= 0 && d < 128 && (d & 4) == 0) ? (int)d : -1;
+}
+// The lanes' target indices go through 1 KiB of LDS outside the operand ring and the bias slot (TSLOT_OFF; each
+// thread writes its own 4 bytes before the mainloop and reads them after it), so that no register holds them across
+// the mainloop. Slot [nj][thread].
+constexpr int TSLOT_OFF = LDS_BYTES + BM * 4;
+constexpr int FWD_LDS_BYTES = TSLOT_OFF + 4 * NTHREADS;
+__device__ __forceinline__ void stash_targets(const TargetArgs& ta, signed char* tslot, int64_t nbase, int64_t N,
+                                              int64_t Vreal, int64_t vw, int lr, int lh) {
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj)
+    tslot[nj * NTHREADS + threadIdx.x] = (signed char)target_local(ta, nbase + nj * 32 + lr, N, Vreal, vw, lh);
+}
+// After the mainloop (whose final barrier makes the slots visible): the lane holding row n's target
+// (n = nbase + nj*32 + lr) writes xy[n] = its logit + the row's sparse bias on the target, summed in slot order as
+// k_row_logits sums it. The selects run only for a block where a lane of the wave has its target.
+__device__ __forceinline__ void target_pass(const TargetArgs& ta, const f32x16 (&acc)[4][4],
+                                            const signed char* tslot, int64_t nbase, int lr) {
+  if (ta.xy == nullptr) return;
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) {
+    const int yl = tslot[nj * NTHREADS + threadIdx.x];  // -1 .. 127
+    if (__builtin_amdgcn_ballot_w64(yl >= 0) == 0) continue;
+    float x = 0.f;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      if (__builtin_amdgcn_ballot_w64((yl >> 5) == mi) == 0) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x = (mi * 32 + 8 * (r >> 2) + (r & 3)) == yl ? acc_read(acc[mi][nj][r]) : x;
+    }
+    if (yl >= 0) {
+      const int64_t n = nbase + nj * 32 + lr, yn = ta.y[n];
+      float by = 0.f;
+      for (int k = 0; k < ta.kc; ++k)
+        if (ta.cand[n * ta.kc + k] == yn) by += ta.cval[n * ta.kc + k];
+      ta.xy[n] = x + by;
+    }
+  }
+}
+
 // Forward tile: S^T[v, n] for a 256(v) x 256(n) tile. Each wave reduces its own 128 vocabulary rows, so the
 // partials are per half-tile: part_m / part_s [2*tiles_v][N] hold the max and sum of exp of row block
 // 2*tm + wm for every column n. No LDS and no barrier after the mainloop. KF: K is a multiple of BK.
 template <bool KF>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64_t N, int64_t V, int64_t Vreal,
-                 int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + BM * 4];
+                 int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s, TargetArgs ta) {
+  __shared__ __attribute__((aligned(1024))) char lds[FWD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const float btile = tile_bias(bias, v0, V);
+  signed char* tslot = reinterpret_cast<signed char*>(lds + TSLOT_OFF);
+  stash_targets(ta, tslot, n0 + wn * 128, N, Vreal, v0 + wm * 128, lr, lh);
   f32x16 acc[4][4];
   // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
   gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
                       reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+  target_pass(ta, acc, tslot, n0 + wn * 128, lr);
 
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
 #pragma unroll
@@ -758,7 +835,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r]);
+      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc_read(acc[mi][nj][r]));
     m = fmaxf(m, __shfl_xor(m, 32));
     float s = 0.f;
     if (m != -INFINITY) {
@@ -766,7 +843,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -mb));
+        for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(acc[mi][nj][r]), LOG2E, -mb));
     }
     s += __shfl_xor(s, 32);
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
@@ -988,25 +1065,30 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
         M = Mp;
         S = Sp;
       }
-      const float lse = M + logf(S);
-      lse_rows[n] = lse;
+      const float ls = logf(S);
+      lse_rows[n] = M + ls;
+      // lse - x_y as (M - x_y) + log S: M - x_y is exact where x_y is near M, so a row whose p_y is near 1 keeps
+      // its small loss instead of the fp32 rounding of lse itself (the one-pass path's M = e_n also cancels)
+      const float d = (M - xy[n]) + ls;
       if (gate == nullptr) {
         // plain cross-entropy: loss = lse - x_y; a target outside [0, V_real) (xy = -inf) is ignored.
         // (loss_rows == nullptr: only lse is wanted.)
         const bool ok = xy[n] != -INFINITY;
-        loss = ok ? lse - xy[n] : 0.f;
+        loss = ok ? d : 0.f;
         if (loss_rows != nullptr) {
           loss_rows[n] = loss;
           wgt_rows[n] = ok ? 1.f : 0.f;
         }
         if (dgr_rows != nullptr) dgr_rows[n] = 0.f;
       } else {
-        const float py = expf(xy[n] - lse);
+        const float py = expf(-d);
         const float g = gate[n], h = hit[n];
+        // P = (1 - g) py + g hit = 1 + q; -log P through log1p(q) while P is near 1
+        const float q = (1.f - g) * expm1f(-d) + g * (h - 1.f);
         const float P = (1.f - g) * py + g * h;
         const bool clamped = !(P >= CLAMP_P);  // torch clamp(min) passes the gradient where P >= min
         const float Pc = clamped ? CLAMP_P : P;
-        loss = -logf(Pc);
+        loss = clamped ? -logf(CLAMP_P) : (fabsf(q) < 0.5f ? -log1pf(q) : -logf(P));
         loss_rows[n] = loss;
         wgt_rows[n] = clamped ? 0.f : (1.f - g) * py / Pc;
         dgr_rows[n] = clamped ? 0.f : (py - h) / Pc;
@@ -1197,11 +1279,11 @@ __global__ __launch_bounds__(256) void k_exact_rows(const int* __restrict__ coun
     }
   }
   const int64_t n = list[j];
-  const float lse = m + logf(s);
+  const float ls = logf(s);
   const bool ok = xy[n] != -INFINITY;
-  lse_rows[n] = lse;
+  lse_rows[n] = m + ls;
   if (loss_rows != nullptr) {
-    loss_rows[n] = ok ? lse - xy[n] : 0.f;
+    loss_rows[n] = ok ? (m - xy[n]) + ls : 0.f;   // lse - x_y, as in k_fwd_merge
     wgt_rows[n] = ok ? 1.f : 0.f;
   }
 }
@@ -1406,7 +1488,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
       float g[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        g[r] = cn[nj] * __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -lb[nj]));
+        g[r] = cn[nj] * __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(acc[mi][nj][r]), LOG2E, -lb[nj]));
       // the selects run only when some lane of the wave has its target (or a candidate) in this block
       if (__builtin_amdgcn_ballot_w64((yl[nj] >> 5) == mi) != 0) {
 #pragma unroll
@@ -1575,8 +1657,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgp
 void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const float* __restrict__ lse_est,
                  int64_t N, int64_t Np, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, float s_max,
                  uint16_t* __restrict__ G, float* __restrict__ part_m, float* __restrict__ part_s,
-                 int* __restrict__ flag) {
-  __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
+                 int* __restrict__ flag, TargetArgs ta) {
+  __shared__ __attribute__((aligned(1024))) char lds[FWD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -1590,10 +1672,13 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
     le[nj] = n < N ? lse_est[n] : INFINITY;
     lb[nj] = le[nj] * LOG2E;
   }
+  signed char* tslot = reinterpret_cast<signed char*>(lds + TSLOT_OFF);
+  stash_targets(ta, tslot, n0 + wn * 128, N, Vreal, v0 + wm * 128, lr, lh);
 
   f32x16 acc[4][4];
   gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
                       reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+  target_pass(ta, acc, tslot, n0 + wn * 128, lr);
   uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
 #pragma unroll
@@ -1604,7 +1689,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
       float e[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -lb[nj]));
+        e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(acc[mi][nj][r]), LOG2E, -lb[nj]));
         s += e[r];
       }
       uint32_t pk[8];
@@ -1622,7 +1707,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[mi][nj][r]);
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, acc_read(acc[mi][nj][r]));
       m = fmaxf(m, __shfl_xor(m, 32));
       float ss = 0.f;
       if (m != -INFINITY) {
@@ -1630,7 +1715,8 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) ss += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][r], LOG2E, -mb));
+          for (int r = 0; r < 16; ++r)
+            ss += __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(acc[mi][nj][r]), LOG2E, -mb));
       }
       ss += __shfl_xor(ss, 32);
       if (robust) {
@@ -1676,7 +1762,7 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   arow[n] = w * expf(e - l);
   const int64_t yn = y[n];
   if (yn >= 0 && yn < Vreal) {
-    G[cm_index(n, yn, Np)] = to_bf16((expf(xy[n] - l) - 1.f) * expf(l - e));
+    G[cm_index(n, yn, Np)] = to_bf16(expm1f(xy[n] - l) * expf(l - e));
   }
   // sparse bias: each distinct valid candidate other than the target gets its true logit x_c + B_c (the target's
   // x_y already includes its bias)
@@ -1748,8 +1834,8 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
         uint32_t pk[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          pk[i] = pack_bf16x2(__builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][2 * i], LOG2E, -lb[nj])),
-                              __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][nj][2 * i + 1], LOG2E, -lb[nj])));
+          pk[i] = pack_bf16x2(__builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(acc[mi][nj][2 * i]), LOG2E, -lb[nj])),
+                              __builtin_amdgcn_exp2f(__builtin_fmaf(acc_read(acc[mi][nj][2 * i + 1]), LOG2E, -lb[nj])));
         if (ok) {
 #pragma unroll
           for (int sc = 0; sc < 2; ++sc)
@@ -1774,7 +1860,7 @@ __global__ __launch_bounds__(256) void k_exact_fix(const int* __restrict__ count
   if (i >= *count) return;
   const int64_t n = list[i], yn = y[n];
   const float l = lse_rows[n];
-  if (yn >= 0 && yn < Vreal) G[cm_index(n, yn, Np)] = to_bf16(expf(xy[n] - l) - 1.f);
+  if (yn >= 0 && yn < Vreal) G[cm_index(n, yn, Np)] = to_bf16(expm1f(xy[n] - l));
   for (int k = 0; k < kc; ++k) {
     const int64_t c = cand[n * kc + k];
     const float B = cb[n * kc + k];
@@ -1991,7 +2077,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          pt[(wm * 128 + out_row<AM>(mi, r, lh)) * BN + wn * 128 + nj * 32 + lr] = acc[mi][nj][r];
+          pt[(wm * 128 + out_row<AM>(mi, r, lh)) * BN + wn * 128 + nj * 32 + lr] = acc_read(acc[mi][nj][r]);
     return;
   }
   const float gs = go != nullptr ? go[0] : 1.f;
@@ -2044,9 +2130,9 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
           const int64_t j = n0 + wn * 128 + nj * 32 + lr;
           if (j < Nc) {
             if constexpr (OUT_BF16)
-              reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)(sc * acc[mi][nj][r]);
+              reinterpret_cast<__bf16*>(C)[i * ldc + j] = (__bf16)(sc * acc_read(acc[mi][nj][r]));
             else
-              reinterpret_cast<float*>(C)[i * ldc + j] = sc * (acc[mi][nj][r] + cv[q][r][nj]);
+              reinterpret_cast<float*>(C)[i * ldc + j] = sc * (acc_read(acc[mi][nj][r]) + cv[q][r][nj]);
           }
         }
       }
@@ -2424,12 +2510,13 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
   if ((rc = launch_status())) return rc;
   {
     ProfScope prof(PROF_FWD_TILES, st);
+    const TargetArgs ta{y, cand, cval, kc, xy};
     if (K % BK == 0)
       hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
-                         tn, w.part_m, w.part_s);
+                         tn, w.part_m, w.part_s, ta);
     else
       hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
-                         tn, w.part_m, w.part_s);
+                         tn, w.part_m, w.part_s, ta);
   }
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, w.cb, w.xc,
@@ -2818,12 +2905,13 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   {
     // e_n: the first vocabulary tile (one tile row of k_fwd_tiles over all rows) and the target logit
     const Operand Hop{H, ldh, N, K, 0};
+    const TargetArgs none{nullptr, nullptr, nullptr, 0, nullptr};  // k_fwd_train writes the target logits
     if (kf)
       hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
-                         w.p0m, w.p0s);
+                         w.p0m, w.p0s, none);
     else
       hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
-                         w.p0m, w.p0s);
+                         w.p0m, w.p0s, none);
     if ((rc = launch_status())) return rc;
   }
   hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, w.cb,
@@ -2836,13 +2924,14 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     const Operand Hop{H + row0 * ldh, ldh, rows, K, 0};
     {
       ProfScope prof(PROF_FWD_TRAIN, st);
+      const TargetArgs ta{y + row0, at(cand, row0 * kc), at(cval, row0 * kc), kc, w.xy + row0};
       if (kf)
         hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est + row0,
-                           rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s, w.flag + row0);
+                           rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s, w.flag + row0, ta);
       else
         hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias,
                            w.lse_est + row0, rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s,
-                           w.flag + row0);
+                           w.flag + row0, ta);
     }
     if ((rc = launch_status())) return rc;
     int* xcount = w.counts + w.np / BLK + b;

@@ -3,7 +3,8 @@ so both load variants of the mainloop), V and v_real drawn at random, with and w
 one-pass path in one block or in 256 / 512-row blocks, and the recompute path. The cases are fixed by the seed, so
 a failure names a shape that fails every time.
 
-Bar (north star): loss within 1e-3 relative, dH / dW / dBias / dGate within 2e-2 relative Frobenius.
+Bar (north star): loss within 1e-3 relative, dH / dW / dBias / dGate within 2e-2 relative Frobenius. The wide sweep
+accepts a miss only where the reference's eager formula in fp32 misses the bar too (_wide_check).
 """
 import os
 
@@ -12,6 +13,7 @@ import pytest
 import torch
 
 from cases import assert_parity, gpu_run, oracle_of, random_case
+from oracle import mce_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -178,31 +180,36 @@ def _wide_cases(count, seed=7):
     return out
 
 
-def _fp32_floors(c, fwd, go):
-    """Absolute error terms that fp32 itself puts on each output, from the one quantity a relative bar cannot see:
-    the difference x_y - lse_n of two fp32 numbers of size |lse_n|, whose error is a few ulps of |lse_n| (taken as
-    8 * 2^-23 * max(1, |lse_n|) = delta_n) however small the difference. It shifts row n's loss by up to delta_n and
-    the target entry of G's row, go * wgt_n * (p_y - 1), by up to e_n = go * wgt_n * delta_n: in dH by e_n |W_y|, in
-    dW by e_n |h_n|, in dBias by e_n, and dGate = go (p_y - hit) / P by about 2 go delta_n p_y / P. These terms are
-    about 1e-5 of the gradient of an ordinary row; they matter only where p_y is within about 1e-4 of 1, where
-    G's target entry is itself that small. torch's fp32 eager formula computes p_y = exp(x_y - lse) the same way."""
-    lse = np.asarray(fwd["lse"], np.float64)
-    wgt = np.asarray(fwd["wgt"], np.float64)
-    py = np.asarray(fwd["py"], np.float64)
-    P = np.asarray(fwd["P"], np.float64)
-    delta = 8.0 * 2.0 ** -23 * np.maximum(1.0, np.abs(lse))
-    e = go * wgt * delta
-    wy = np.linalg.norm(c["w"].double().numpy()[c["y"].numpy()], axis=1)
-    hn = np.linalg.norm(c["h"].double().numpy(), axis=1)
-    dg = np.where(P >= 1e-30, 2.0 * go * delta * py / np.maximum(P, 1e-30), 0.0)
-    return dict(loss=float(delta.sum()), dh=float(np.sqrt(((e * wy) ** 2).sum())), dw=float((e * hn).sum()),
-                dbias=float(e.sum()), dgate=float(np.sqrt((dg ** 2).sum())))
+def _eager_fp32_errors(c, bwd, fwd, go):
+    """Errors of the reference's eager formula itself in fp32: the oracle's torch restatement of `_ce_part`
+    (full2.py:1917-1929, eager_ce_part) on the same bf16-rounded operands, fp32 logits, gradients by autograd, on the
+    host; padded ids masked with a -inf bias as the fused op masks them. Absolute loss error and Frobenius error of
+    each gradient, both against the fp64 oracle."""
+    h = torch.from_numpy(orc.bf16_round(c["h"].float().numpy())).requires_grad_()
+    w = torch.from_numpy(orc.bf16_round(c["w"].float().numpy())).requires_grad_()
+    v = w.shape[0]
+    b = (c["bias"].float().clone() if c["bias"] is not None else torch.zeros(v))
+    b[c["v_real"]:] = float("-inf")
+    b.requires_grad_()
+    g = c["gate"].float().clone().requires_grad_()
+    y = c["y"]
+    c1 = torch.where(c["hit"] > 0, y, torch.full_like(y, -1))   # hit = (c1 == y)
+    loss = orc.eager_ce_part(h, w, b, y, c1, g)
+    (loss * go).backward()
+    out = dict(loss=abs(float(loss) - float(fwd["loss_sum"])))
+    for key, t in (("dh", h), ("dw", w), ("dbias", b), ("dgate", g)):
+        out[key] = float(np.linalg.norm(t.grad.double().numpy() - bwd[key]))
+    return out
 
 
 def _wide_check(case):
-    """The bar plus the fp32 terms of _fp32_floors: loss within 1e-3 relative + floor, each gradient within 2e-2
-    relative Frobenius + floor + 1e-30 (a gradient whose oracle norm is below fp32's normal range, 1.2e-38, e.g.
-    a row with wgt = 1e-41, comes out as 0)."""
+    """The north-star bar (loss within 1e-3 relative, each gradient within 2e-2 relative Frobenius, plus 1e-30 for a
+    gradient whose oracle norm is below fp32's normal range: a row with wgt = 1e-41 comes out as 0), against the fp64
+    oracle. A quantity that misses it is accepted only where fp32 itself cannot meet it: the reference's eager
+    formula evaluated in fp32 on the same operands (_eager_fp32_errors) misses the bar too, and the fused op's error
+    is at most twice the eager one. (A row's loss and its target entry of G come from x_y - lse, a difference of two
+    fp32 numbers of size |lse| whose error is a few ulps of lse: where p_y is within about 1e-4 of 1 that exceeds a
+    relative bar in any fp32 evaluation.)"""
     from memarch_amd import fused_ops
     n, k, v, vr, bias, path, h32, ws, gm, ym, seed = case
     fused_ops.RECOMPUTE = path == "recompute"
@@ -211,15 +218,37 @@ def _wide_check(case):
     go = 1.0 / n
     got = gpu_run(c, go=go, h_dtype=torch.float32 if h32 else torch.bfloat16)
     fwd, bwd = oracle_of(c, go=go)
-    fl = _fp32_floors(c, fwd, go)
     lref = float(fwd["loss_sum"])
-    assert abs(got["loss"] - lref) <= 1e-3 * abs(lref) + fl["loss"], ("loss", got["loss"], lref, fl["loss"])
+    errs = dict(loss=(abs(got["loss"] - lref), 1e-3 * abs(lref)))
     for x in ("dh", "dw", "dgate", "dbias"):
         if got.get(x) is None:
             continue
-        ref = np.linalg.norm(bwd[x])
-        err = np.linalg.norm(np.asarray(got[x], np.float64) - bwd[x])
-        assert np.isfinite(got[x]).all() and err <= 2e-2 * ref + fl[x] + 1e-30, (x, err, ref, fl[x])
+        assert np.isfinite(got[x]).all(), (x, "not finite")
+        errs[x] = (float(np.linalg.norm(np.asarray(got[x], np.float64) - bwd[x])),
+                   2e-2 * float(np.linalg.norm(bwd[x])) + 1e-30)
+    missed = {x: e for x, e in errs.items() if not e[0] <= e[1]}
+    if missed:
+        eager = _eager_fp32_errors(c, bwd, fwd, go)
+        for x, (err, bar) in missed.items():
+            print(f"  {x}: fused {err:.3e} over the bar {bar:.3e}; fp32 eager {eager[x]:.3e}", flush=True)
+            assert eager[x] > bar and err <= 2.0 * eager[x], (x, err, bar, eager[x])
+
+
+# A case of the 2800-case sweep whose loss missed the relative bar by fp32 rounding alone (two rows with p_y within
+# 1e-5 of 1): case 1241 of _wide_cases(2800).
+FP32_LIMITED_CASE = 1241
+
+
+def test_wide_sweep_fp32_limited_case():
+    from memarch_amd import fused_ops
+    case = _wide_cases(FP32_LIMITED_CASE + 1)[FP32_LIMITED_CASE]
+    assert case[-1] == 51241
+    print(f"wide sweep {case}", flush=True)
+    saved = fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS
+    try:
+        _wide_check(case)
+    finally:
+        fused_ops.RECOMPUTE, fused_ops.BLOCK_ROWS = saved
 
 
 def test_wide_sweep():
