@@ -1965,11 +1965,12 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 }
 
 // The bf16 cast of an fp32 weight and its K-blocked transpose in one pass: w16[r, c] = bf16(src[r, c]) (round to
-// nearest even) for r < R, c < C (row stride ld16), and, when dst is not null, dst as k_transpose_blocked writes it
-// from w16 (zero for R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile.
+// nearest even) for r < R, c < C (row stride ld16), and 0 for C <= c < Cpad (a zero-padded row, Cpad <= the grid's
+// columns); when dst is not null, dst as k_transpose_blocked writes it from w16 over the C columns (zero for
+// R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile.
 __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict__ src, int64_t ld32, int64_t R,
                                                         int64_t C, uint16_t* __restrict__ w16, int64_t ld16,
-                                                        uint16_t* __restrict__ dst) {
+                                                        uint16_t* __restrict__ dst, int64_t Cpad) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64][66];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
@@ -1986,6 +1987,8 @@ __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict_
       pk[2] = pack_bf16x2(b.x, b.y);
       pk[3] = pack_bf16x2(b.z, b.w);
       *reinterpret_cast<u32x4*>(w16 + r * ld16 + c) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    } else if (r < R && c < Cpad) {
+      *reinterpret_cast<u32x4*>(w16 + r * ld16 + c) = u32x4{0u, 0u, 0u, 0u};   // the zero padding columns
     }
     uint32_t* row = reinterpret_cast<uint32_t*>(&tile[rl][cl]);
 #pragma unroll
@@ -2771,7 +2774,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
     return p;
   };
   w.G = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * nb));
-  w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb * K));
+  w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb * cdiv(K, BK) * BK));  // also the exact pass's rows
   w.uperm = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb));
   w.part_m = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
   w.part_s = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
@@ -2869,7 +2872,11 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   if (!rc) rc = check_sparse(cand, cval, kc, N);
   if (!rc && kc > 0 && gate != nullptr) rc = MCE_EINVAL;  // the sparse bias is for plain cross-entropy
   if (rc) return rc;
-  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~7)) return MCE_EINVAL;
+  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~15)) return MCE_EINVAL;
+  // MCE_ZERO_PAD: the logits are reduced over kr = K rounded up to BK, the columns K .. kr-1 of H and W being zero
+  const bool zpad = (want & MCE_ZERO_PAD) != 0 && K % BK != 0;
+  const int64_t kr = zpad ? cdiv(K, BK) * BK : K;
+  if (ldh < kr || ldw < kr) return MCE_EINVAL;
   if ((want & MCE_GRAD_BIAS) && bias == nullptr) return MCE_EINVAL;
   if (W32 != nullptr && (ldw32 < K || ldw32 % 4 || (reinterpret_cast<uintptr_t>(W32) & 15))) return MCE_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -2886,13 +2893,13 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   if (more && (want & MCE_GRAD_H) && !dh_aligned(dH_part, lddh, dh_bf16)) return MCE_EALIGN;
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)(w.vp / BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, K, 0};
-  const bool kf = K % BK == 0;
+  const Operand Wop{W, ldw, V, kr, 0};
+  const bool kf = kr % BK == 0;
   // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V; with
   // W32 the bf16 W itself comes from the same pass
   if (W32 != nullptr) {
     hipLaunchKernelGGL(k_cast_transpose, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W32,
-                       ldw32, V, K, W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr);
+                       ldw32, V, K, W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr, kr);
     if ((rc = launch_status())) return rc;
   } else if (want & MCE_GRAD_H) {
     hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
@@ -2904,7 +2911,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   if ((rc = launch_status())) return rc;
   {
     // e_n: the first vocabulary tile (one tile row of k_fwd_tiles over all rows) and the target logit
-    const Operand Hop{H, ldh, N, K, 0};
+    const Operand Hop{H, ldh, N, kr, 0};
     const TargetArgs none{nullptr, nullptr, nullptr, 0, nullptr};  // k_fwd_train writes the target logits
     if (kf)
       hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
@@ -2921,7 +2928,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   for (int64_t b = 0; b < w.nblk; ++b) {
     const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
     const int tnb = (int)(rp / BN);
-    const Operand Hop{H + row0 * ldh, ldh, rows, K, 0};
+    const Operand Hop{H + row0 * ldh, ldh, rows, kr, 0};
     {
       ProfScope prof(PROF_FWD_TRAIN, st);
       const TargetArgs ta{y + row0, at(cand, row0 * kc), at(cval, row0 * kc), kc, w.xy + row0};
@@ -2950,13 +2957,13 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     if ((rc = launch_status())) return rc;
     // the flagged rows' exact E' (the block's H^T buffer, rewritten later, holds their gathered rows)
     hipLaunchKernelGGL(k_gather_rows, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, w.flag_list,
-                       w.counts + b, K, w.Ht);
+                       w.counts + b, kr, w.Ht);
     if ((rc = launch_status())) return rc;
     if (kf)
-      hipLaunchKernelGGL(k_exact_train<true>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias,
+      hipLaunchKernelGGL(k_exact_train<true>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, kr, bias,
                          w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     else
-      hipLaunchKernelGGL(k_exact_train<false>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias,
+      hipLaunchKernelGGL(k_exact_train<false>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, kr, bias,
                          w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     if ((rc = launch_status())) return rc;
     hipLaunchKernelGGL(k_exact_fix, dim3((unsigned)(rp / 256)), dim3(256), 0, st, w.counts + b, w.flag_list, y + row0,
