@@ -389,6 +389,15 @@ __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\
 // An accumulator value read from its AGPR at this point of the program (an epilogue's use). Left to itself the
 // compiler copies all 256 accumulators of a wave into VGPRs at the start of an epilogue, which then needs every
 // VGPR and spills; an explicit read per use keeps a few values live at a time.
+// An MFMA with its accumulator in VGPRs (the extra-column accumulators; the 256 AGPRs hold the tile's), as an inline
+// asm: a compiler-visible MFMA with a VGPR accumulator moves every MFMA of the kernel to the VGPR form, and the tile's
+// accumulators no longer fit. Its result is read only after gemm_tile's mfma_drain, and consecutive ones into the
+// same registers are a whole stage apart.
+__device__ __forceinline__ void mfma_vgpr(f32x16& c, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+// the extra-column accumulators (in VGPRs): a plain copy, after the same drain
+__device__ __forceinline__ float acc_read_v(float a) { return a; }
 __device__ __forceinline__ float acc_read(float a) {
   float v;
   asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
@@ -434,6 +443,12 @@ struct DotState {
   uint32_t uaddr;     // LDS byte offset of this lane's 8 u values (slice = wave) in the slot of buffer 0
   bf16x8 x[NR], u;    // the fragments and u values read for this stage
   float acc[NR];      // row rg_j*32 + lane%32, K positions of lane half lane/32 of slice `wave` of every stage
+  // extra-column mode (XM): up to 32 more rows of the B operand (output columns past the tile grid), formed for the
+  // same row groups by one 32x32x16 MFMA per group and stage (slice = wave) instead of the dot products with u
+  Stream xs;          // the extra rows: this wave's one load per stage (rows 8 wave .. +7 of the [32][64] image)
+  uint32_t xaddr;     // byte offset of this lane's B fragment of slice `wave` (row lane%32) inside a slot
+  bf16x8 bx;
+  f32x16 xacc[NR];    // C[row of group rg_j][extra column], the slices `wave` of every stage
 };
 // c + a[2q] u[2q] + a[2q+1] u[2q+1] (the pairs taken with shufflevector: a bit_cast of one 32-bit element of a
 // vector loses the element index in this compiler)
@@ -458,6 +473,33 @@ __device__ __forceinline__ void issue_ap(const i32x4& rsrc, int stage, int send,
   else
     buffer_load_lds(rsrc, (uint32_t LDS_AS*)(lds + APOFF + slot * 1024), 16, off, 0, 0, 0);
 }
+// The extra rows' image (XM): ring buffer b's slot at XOFF + XSLOT b, [32 rows][64 k] bf16 with 128-byte rows and
+// the chunk swizzle of the operand images (I::swz); every wave loads its 8 rows of a stage (one instruction).
+constexpr int XOFF = LDS_BYTES, XSLOT = 4096;
+template <bool ASM = false>
+__device__ __forceinline__ void issue_x(const Stream& xs, int stage, int send, char* lds, int slot, int wave) {
+  const StageSrc g = stage_src(xs, stage, send);
+  if constexpr (ASM)
+    dma16(g.rsrc, lds, XOFF + slot * XSLOT + wave * 1024, xs.vfull[0]);
+  else
+    buffer_load_lds(g.rsrc, (uint32_t LDS_AS*)(lds + XOFF + slot * XSLOT + wave * 1024), 16, xs.vfull[0], 0, 0, 0);
+}
+// The extra rows of operand X ([xrows <= 32][K], row-major or K-blocked like the B operand) as a stream: lane l of
+// wave w loads row 8w + l/8, logical chunk (l%8) ^ swz(row), into the 1 KiB of its instruction (rows >= xrows read
+// zeros); full stages only (KF kernels).
+__device__ __forceinline__ Stream make_xstream(const Operand& X, int wave, int lane) {
+  Stream st;
+  st.kext = X.kext;
+  st.blk = X.blk ? X.blk : BLK;
+  st.kmul = 2;
+  st.base = reinterpret_cast<uint64_t>(X.p);
+  const int row = wave * 8 + (lane >> 3), c = (lane & 7) ^ I::swz(row);
+  st.vfull[0] = row < X.mext ? (int)(row * X.ld * 2) + c * 16 : OOB;
+  st.voff[0] = st.vfull[0];
+  st.kloc[0] = 0;
+  return st;
+}
+
 // Slice 1 with the NR + 1 extra reads first; slice 2 with the 4 NR dot products, NR between each of its first MFMA
 // pairs.
 template <int NR, int AM = 0>
@@ -486,12 +528,13 @@ __device__ __forceinline__ void sched_slice_dot() {
 
 // A slice without loads: reads of slice RK of buffer RBUF into (da, db), the 16 MFMAs of (ua, ub), interleaved by
 // the compiler one read per two MFMAs.
-template <int RBUF, int RK, int DB = 0, int AM = 0>
+template <int RBUF, int RK, int DB = 0, int AM = 0, bool XM = false>
 __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&ua)[4], const bf16x8 (&ub)[4],
                                             const char* lds, const FragAddr& ad, bf16x8 (&da)[4], bf16x8 (&db)[4],
                                             DotState<DB ? DB : 1>* dp = nullptr) {
   if constexpr (DB > 0 && RK == 2) {
-    // slice 1 of the stage (reads slice 2): this wave's extra fragments and u values of the stage's buffer
+    // slice 1 of the stage (reads slice 2): this wave's extra fragments and u values (XM: B fragment of the extra
+    // rows) of the stage's buffer
 #pragma unroll
     for (int j = 0; j < DB; ++j) {
       if constexpr (AM == 2)
@@ -499,10 +542,21 @@ __device__ __forceinline__ void slice_plain(f32x16 (&acc)[4][4], const bf16x8 (&
       else
         dp->x[j] = frag_at<AOFF + RBUF * I::OPB>(lds, dp->faddr[j]);
     }
-    dp->u = frag_at<APOFF + RBUF * 1024>(lds, dp->uaddr);
+    if constexpr (XM)
+      dp->bx = frag_at<XOFF + RBUF * XSLOT>(lds, dp->xaddr);
+    else
+      dp->u = frag_at<APOFF + RBUF * 1024>(lds, dp->uaddr);
     read_frags<RBUF, RK, AM>(lds, ad, da, db);
     mma16(acc, ua, ub);
     sched_slice_rd2<DB, AM>();
+  } else if constexpr (DB > 0 && RK == 3 && XM) {
+    // slice 2 (reads slice 3): the extra columns' MFMA of each group, on the fragments read in slice 1
+    read_frags<RBUF, RK, AM>(lds, ad, da, db);
+    mma16(acc, ua, ub);
+#pragma unroll
+    for (int j = 0; j < DB; ++j) mfma_vgpr(dp->xacc[j], dp->x[j], dp->bx);
+    sched_slice<AM>();
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, DB, 0);
   } else if constexpr (DB > 0 && RK == 3) {
     // slice 2 of the stage (reads slice 3): the dot products of the fragments read in slice 1
     read_frags<RBUF, RK, AM>(lds, ad, da, db);
@@ -556,7 +610,7 @@ __device__ __forceinline__ void slice_loads(f32x16 (&acc)[4][4], const bf16x8 (&
 //   wait for this wave's loads of stage kt+1, barrier: every wave has read all of stage kt and stage kt+1 landed;
 //   slice 3: MFMAs on slice 3, reads of slice 0 of stage kt+1 (NB), loads of stage kt+2's A operand into CB.
 // A stage's loads are thus split in two halves, one load per two MFMAs, landing over three slices of MFMAs.
-template <int CB, bool KF, int DB = 0, int AM = 0>
+template <int CB, bool KF, int DB = 0, int AM = 0, bool XM = false>
 __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4][4], bf16x8 (&fa)[2][4],
                                            bf16x8 (&fb)[2][4], char* lds, const FragAddr& ad, const Stream& sa,
                                            const Stream& sb, int wave, DotState<DB ? DB : 1>* dp = nullptr) {
@@ -565,15 +619,17 @@ __device__ __forceinline__ void gemm_stage(int stage, int send, f32x16 (&acc)[4]
     const StageSrc gb = stage_src(sb, stage + 1, send);
     slice_loads<CB, 1, true, NB, KF, AM>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], sb, gb, wave);
   }
-  slice_plain<CB, 2, DB, AM>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], dp);
-  slice_plain<CB, 3, DB, AM>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], dp);
+  slice_plain<CB, 2, DB, AM, XM>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], dp);
+  slice_plain<CB, 3, DB, AM, XM>(acc, fa[0], fb[0], lds, ad, fa[1], fb[1], dp);
   wait_vmcnt<0>();
   __syncthreads();
   {
     const StageSrc ga = stage_src(sa, stage + 2, send);
     slice_loads<NB, 0, false, CB, KF, AM>(acc, fa[1], fb[1], lds, ad, fa[0], fb[0], sa, ga, wave);
   }
-  if constexpr (DB > 0) {
+  if constexpr (DB > 0 && XM) {
+    issue_x<AM == 2>(dp->xs, stage + 2, send, lds, CB, wave);
+  } else if constexpr (DB > 0) {
     if (wave == 0) issue_ap<AM == 2>(dp->rsrc, stage + 2, send, lds, CB);
   }
 }
@@ -627,11 +683,12 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool BIAS = false, int AM = 0, int DB = 0>
+template <bool KF, bool BIAS = false, int AM = 0, int DB = 0, bool XM = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
                                           int64_t Vreal = 0, DotState<DB ? DB : 1>* dp = nullptr, int rg0 = 0,
                                           int rg_step = 8) {
+  static_assert(!XM || (DB > 0 && KF), "the extra-column mode needs row groups and whole K stages");
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
@@ -670,13 +727,25 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
         dp->faddr[j] = ra * I::ROWB + ((c ^ I::swz(ra)) << 4);
       }
       dp->acc[j] = 0.f;
+      if constexpr (XM) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp->xacc[j][r] = 0.f;
+      }
     }
-    dp->uaddr = 32 * wave + 16 * (lane >> 5);
-    // u of stage s0 before the A loads of stage s0+1, so the wait below covers it
-    if (wave == 0) issue_ap<AM == 2>(dp->rsrc, s0, send, lds, 0);
+    if constexpr (XM) {
+      const int xr = lane & 31, xc = 2 * wave + (lane >> 5);
+      dp->xaddr = xr * I::ROWB + ((xc ^ I::swz(xr)) << 4);   // relative to the slot (frag_at adds XOFF)
+      issue_x<AM == 2>(dp->xs, s0, send, lds, 0, wave);   // before the A loads of stage s0+1: the wait covers it
+    } else {
+      dp->uaddr = 32 * wave + 16 * (lane >> 5);
+      // u of stage s0 before the A loads of stage s0+1, so the wait below covers it
+      if (wave == 0) issue_ap<AM == 2>(dp->rsrc, s0, send, lds, 0);
+    }
   }
   issue_stage<AM == 2>(sa, s0 + 1, send, lds, AOFF + I::OPB, wave);
-  if constexpr (DB > 0) {
+  if constexpr (DB > 0 && XM) {
+    issue_x<AM == 2>(dp->xs, s0 + 1, send, lds, 1, wave);
+  } else if constexpr (DB > 0) {
     if (wave == 0) issue_ap<AM == 2>(dp->rsrc, s0 + 1, send, lds, 1);
   }
   if constexpr (BIAS) stash_bias(bslot, btile, m0, Vreal);
@@ -698,10 +767,10 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   read_frags<0, 0, AM>(lds, ad, fa[0], fb[0]);
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    gemm_stage<0, KF, DB, AM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
-    gemm_stage<1, KF, DB, AM>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+    gemm_stage<0, KF, DB, AM, XM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+    gemm_stage<1, KF, DB, AM, XM>(s0 + kt + 1, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   }
-  if (kt < nk) gemm_stage<0, KF, DB, AM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
+  if (kt < nk) gemm_stage<0, KF, DB, AM, XM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   wait_vmcnt<0>();
   __syncthreads();
   mfma_drain();
@@ -2021,13 +2090,18 @@ __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict_
 // order). When the tile count leaves a partial last wave on the GPU, the remaining tiles are split along K:
 // block full + r*P + p computes K slice p of P of tile full + r and writes its fp32 partial tile (row-major
 // 256 x 256) to part[r*P + p]; k_tail_reduce then sums the P slices in a fixed order.
-template <bool OUT_BF16, bool KF, int AM, int DB>
+// XM (extra-column mode, DB = the row groups per tile): the output also has the columns Nx .. Nx + X.mext - 1 (at
+// most 32), the product of A with the rows of X (the B operand's rows past the tile grid), formed inside the tiles:
+// tile (tm, tn < 8) forms them for its row groups as the dot products above are formed, by one MFMA per group and
+// stage, and writes them with the epilogue below; a K-split tail tile writes its slice's values to
+// xpart[((slot * DB + j) * 32 + i) * 32 + n] (row i of group j, extra column n), which k_xtail_reduce adds up.
+template <bool OUT_BF16, bool KF, int AM, int DB, bool XM = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles_m, int tiles_n, int group,
             int full, int P, void* C, int64_t ldc, float* __restrict__ part,
             const float* __restrict__ rscale, const float* __restrict__ go, const float* cin,
-            const uint16_t* __restrict__ u, float* __restrict__ upart) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (DB > 0 ? 2048 : 0)];
+            const uint16_t* __restrict__ u, float* __restrict__ upart, Operand X, int64_t Nx) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES + (XM ? 2 * XSLOT : DB > 0 ? 2048 : 0)];
   const int b = (int)blockIdx.x;
   int lin, s0 = 0, nk = nk_total, slot = -1;
   if (b < full) {
@@ -2053,8 +2127,45 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
     // q of the split tail (T = tiles_m * tiles_n)
     DotState<DB> dp;
     dp.rsrc = make_rsrc(reinterpret_cast<uint64_t>(u));
+    if constexpr (XM) dp.xs = make_xstream(X, __builtin_amdgcn_readfirstlane(wave), lane);
     const bool active = tn < 8;  // tiles_n > 8: the tiles past the 8th column have no group
-    gemm_tile<KF, false, AM, DB>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, active ? tn : 0, tiles_n);
+    gemm_tile<KF, false, AM, DB, XM>(A, B, s0, nk, m0, n0, lds, acc, 0.f, nullptr, 0, &dp, active ? tn : 0,
+                                     tiles_n);
+    if constexpr (XM) {
+      // the extra columns: the four waves' slices of every stage added through LDS (free after gemm_tile); thread t
+      // takes C row i = t/8 of each group (register 4(i/8) + i%4 of lane half (i/4)%2) and its columns 4(t%8) .. +3
+      float* xred = reinterpret_cast<float*>(lds);
+#pragma unroll
+      for (int j = 0; j < DB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) xred[((j * 4 + wave) * 16 + r) * 64 + lane] = acc_read_v(dp.xacc[j][r]);
+      __syncthreads();
+      const int i = t >> 3, xlh = (i >> 2) & 1, xr = 4 * (i >> 3) + (i & 3);
+      const float gsx = go != nullptr ? go[0] : 1.f;
+#pragma unroll
+      for (int j = 0; j < DB; ++j) {
+        const int rg = tn + j * tiles_n;
+        if (!active || rg > 7) break;
+        const int64_t row = m0 + rg * 32 + (AM == 2 ? kperm_inv(i) : i);
+        const float sc = rscale != nullptr ? (row < M ? gsx * rscale[row] : 0.f) : gsx;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = 4 * (t & 7) + q, l = n + 32 * xlh;
+          float v = 0.f;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) v += xred[((j * 4 + w) * 16 + xr) * 64 + l];
+          if (slot >= 0) {
+            upart[(((int64_t)slot * DB + j) * 32 + i) * 32 + n] = v;
+          } else if (row < M && n < X.mext) {
+            const int64_t col = Nx + n;
+            if constexpr (OUT_BF16)
+              reinterpret_cast<__bf16*>(C)[row * ldc + col] = (__bf16)(sc * v);
+            else
+              reinterpret_cast<float*>(C)[row * ldc + col] = sc * (v + (cin != nullptr ? cin[row * ldc + col] : 0.f));
+          }
+        }
+      }
+    } else {
     // lanes l and l+32 hold the two K halves of row rg_j*32 + l%32; the four waves hold the four slices
     float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
@@ -2068,6 +2179,7 @@ void k_gemm(Operand A, Operand B, int nk_total, int64_t M, int64_t Nc, int tiles
       const int64_t row = (slot >= 0 ? (int64_t)tiles_m * tiles_n + slot : lin) * DB + j;
       const float* rj = red + j * 128;
       upart[row * 32 + (AM == 2 ? kperm_inv(r) : r)] = (rj[r] + rj[32 + r]) + (rj[64 + r] + rj[96 + r]);
+    }
     }
   } else {
     gemm_tile<KF, false, AM>(A, B, s0, nk, m0, n0, lds, acc);
@@ -2187,6 +2299,39 @@ __global__ __launch_bounds__(256) void k_tail_reduce(const float* __restrict__ p
   }
 }
 
+// The extra columns (k_gemm's XM) of the K-split tail tiles: block (tail tile r, group j) adds the P slices' values
+// of its 32 rows in a fixed order and writes them with k_gemm's epilogue (row scale, go, Cin). Thread t: row i = t/8,
+// extra columns 4(t%8) .. +3.
+template <bool OUT_BF16>
+__global__ __launch_bounds__(256) void k_xtail_reduce(const float* __restrict__ xpart, int P, int full, int nr,
+                                                      int tiles_m, int tiles_n, int group, int am2, int64_t M,
+                                                      int64_t Nx, int xcols, void* C, int64_t ldc,
+                                                      const float* __restrict__ rscale, const float* __restrict__ go,
+                                                      const float* cin) {
+  const int r = (int)blockIdx.x, j = (int)blockIdx.y, t = threadIdx.x;
+  int tm, tn;
+  tile_of(full + r, tiles_m, tiles_n, group, tm, tn);
+  const int rg = tn + j * tiles_n;
+  if (tn >= 8 || rg > 7) return;
+  const int i = t >> 3;
+  const int64_t row = (int64_t)tm * BM + rg * 32 + (am2 ? kperm_inv(i) : i);
+  if (row >= M) return;
+  const float gs = go != nullptr ? go[0] : 1.f;
+  const float sc = rscale != nullptr ? gs * rscale[row] : gs;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = 4 * (t & 7) + q;
+    if (n >= xcols) continue;
+    float v = 0.f;
+    for (int p = 0; p < P; ++p) v += xpart[((((int64_t)r * P + p) * nr + j) * 32 + i) * 32 + n];
+    const int64_t col = Nx + n;
+    if constexpr (OUT_BF16)
+      reinterpret_cast<__bf16*>(C)[row * ldc + col] = (__bf16)(sc * v);
+    else
+      reinterpret_cast<float*>(C)[row * ldc + col] = sc * (v + (cin != nullptr ? cin[row * ldc + col] : 0.f));
+  }
+}
+
 // dBias of the training path from the dW blocks' dot-product partials (k_gemm<.., DB>): row group rg = (v%256)/32
 // of tile row v/256 belongs to tile column tn = rg % tiles_n as its group j = rg / tiles_n; dbias[v] = that
 // partial at row v%32 -- or, for a tile of the split tail, the sum of its P K-slice partials in a fixed order --
@@ -2226,6 +2371,12 @@ inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
 // tile row are spread over its first min(tiles_n, 8) tiles.
 inline int fold_nr(int64_t tiles_n) { return tiles_n >= 8 ? 1 : (int)cdiv(8, tiles_n); }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+// Extra columns formed inside the tiles (k_gemm's XM) for an output width K = 256 c + x, 0 < x <= 32, c >= 4 (1 or 2
+// row groups per tile): the folded-bias layout's d + 16. Returns x, or 0 when the width takes whole tiles instead.
+inline int64_t extra_cols(int64_t K) {
+  const int64_t x = K % 256;
+  return (x > 0 && x <= 32 && K / 256 >= 4) ? x : 0;
+}
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 // dH and dH_part of the training path (k_scale_rows moves them 16 bytes at a time): null, or 16-byte aligned with a
 // row stride of whole 16-byte units (8 bf16 or 4 fp32 values)
@@ -2267,7 +2418,7 @@ FwdWs fwd_ws_layout(char* base, int64_t N, int64_t V, int kslots) {
 constexpr int TAIL_SLOTS = 256;
 struct BwdWs {
   uint16_t *G, *Wt, *Ht;
-  float *dbias_part, *xy, *part, *xc, *cb, *fix_val, *tval;
+  float *dbias_part, *xy, *part, *xpart, *xc, *cb, *fix_val, *tval;
   int *fix_col, *ty;
   int64_t np, vp;
   size_t bytes;
@@ -2290,6 +2441,7 @@ BwdWs bwd_ws_layout(char* base, int64_t N, int64_t K, int64_t V) {
   w.ty = reinterpret_cast<int*>(take(sizeof(int) * w.np));
   w.tval = reinterpret_cast<float*>(take(sizeof(float) * w.np));
   w.part = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * BM * BN));
+  w.xpart = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * 2 * 32 * 32));
   w.xc = reinterpret_cast<float*>(take(sizeof(float) * w.np * MAX_KC));
   w.cb = reinterpret_cast<float*>(take(sizeof(float) * w.np * MAX_KC));
   w.fix_col = reinterpret_cast<int*>(take(sizeof(int) * w.np * MAX_KC));
@@ -2386,8 +2538,11 @@ template <bool OUT_BF16>
 int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t Nc, int group, void* C, int64_t ldc,
                 float* part, hipStream_t st, const float* rscale = nullptr, const float* go = nullptr,
                 const float* cin = nullptr, const uint16_t* u = nullptr, float* upart = nullptr,
-                int* p_out = nullptr, int* full_out = nullptr, int pcls = PROF_NONE) {
-  const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nc, BN), T = tiles_m * tiles_n;
+                int* p_out = nullptr, int* full_out = nullptr, int pcls = PROF_NONE, const Operand* X = nullptr,
+                float* xpart = nullptr) {
+  // with X (extra-column mode), the last X->mext (<= 32) of the Nc columns are formed inside the tiles of the others
+  const int64_t Nx = X != nullptr ? Nc - X->mext : Nc;
+  const int tiles_m = (int)cdiv(M, BM), tiles_n = (int)cdiv(Nx, BN), T = tiles_m * tiles_n;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                                hipSuccess || cus <= 0)
@@ -2405,16 +2560,39 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   if (p_out) *p_out = P;
   if (full_out) *full_out = full;
   // transposed pieces (G read with the vocabulary as M, for dW): whole K stages only. Dot products with u: only
-  // with such an A operand and fp32 output
+  // with such an A operand and fp32 output. The extra-column mode: whole K stages, 1 or 2 row groups per tile, no u
   const int nr = fold_nr(tiles_n);
   if (A.cm == 2 && !kf) return MCE_EINVAL;
   if (u != nullptr && (OUT_BF16 || A.cm != 2 || upart == nullptr)) return MCE_EINVAL;
+  if (X != nullptr && (u != nullptr || !kf || A.cm == 0 || nr > 2 || X->mext < 1 || X->mext > 32 || Nx % BN != 0 ||
+                       xpart == nullptr))
+    return MCE_EINVAL;
+  const Operand none{};
   ProfScope prof(pcls, st);
-  if (u != nullptr) {
+  if (X != nullptr) {
+#define MCE_GEMM_XM(OB_, AM_, NR_)                                                                                 \
+  hipLaunchKernelGGL((k_gemm<OB_, true, AM_, NR_, true>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, \
+                     tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, xpart, *X, Nx)
+    if (A.cm == 2) {
+      if constexpr (!OUT_BF16) {
+        if (nr == 1)
+          MCE_GEMM_XM(false, 2, 1);
+        else
+          MCE_GEMM_XM(false, 2, 2);
+      } else {
+        return MCE_EINVAL;
+      }
+    } else if (nr == 1) {
+      MCE_GEMM_XM(OUT_BF16, 1, 1);
+    } else {
+      MCE_GEMM_XM(OUT_BF16, 1, 2);
+    }
+#undef MCE_GEMM_XM
+  } else if (u != nullptr) {
     if constexpr (!OUT_BF16) {
 #define MCE_GEMM_DB(NR_)                                                                                   \
   hipLaunchKernelGGL((k_gemm<false, true, 2, NR_>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, \
-                     tiles_n, group, full, P, C, ldc, part, rscale, go, cin, u, upart)
+                     tiles_n, group, full, P, C, ldc, part, rscale, go, cin, u, upart, none, Nc)
       if (nr == 1)
         MCE_GEMM_DB(1);
       else if (nr == 2)
@@ -2430,29 +2608,32 @@ int launch_gemm(const Operand& A, const Operand& B, int nk, int64_t M, int64_t N
   } else if (A.cm == 2) {
     if constexpr (!OUT_BF16)
       hipLaunchKernelGGL((k_gemm<false, true, 2, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc, tiles_m, tiles_n,
-                         group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
+                         group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr, none, Nc);
     else
       return MCE_EINVAL;
   } else if (A.cm) {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, 1, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr, none, Nc);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, 1, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr, none, Nc);
   } else {
     if (kf)
       hipLaunchKernelGGL((k_gemm<OUT_BF16, true, 0, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr, none, Nc);
     else
       hipLaunchKernelGGL((k_gemm<OUT_BF16, false, 0, 0>), grid, dim3(NTHREADS), 0, st, A, B, nk, M, Nc,
-                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr);
+                         tiles_m, tiles_n, group, full, P, C, ldc, part, rscale, go, cin, nullptr, nullptr, none, Nc);
   }
   prof.end();
   int rc = launch_status();
   if (rc || full == T) return rc;
   hipLaunchKernelGGL((k_tail_reduce<OUT_BF16>), dim3(BM / 4, T - full), dim3(256), 0, st, part, P, full, tiles_m,
-                     tiles_n, group, M, Nc, C, ldc, rscale, go, cin);
+                     tiles_n, group, M, Nx, C, ldc, rscale, go, cin);
+  if ((rc = launch_status()) || X == nullptr) return rc;
+  hipLaunchKernelGGL((k_xtail_reduce<OUT_BF16>), dim3(T - full, nr), dim3(256), 0, st, xpart, P, full, nr, tiles_m,
+                     tiles_n, group, A.cm == 2 ? 1 : 0, M, Nx, (int)X->mext, C, ldc, rscale, go, cin);
   return launch_status();
 }
 
@@ -2664,14 +2845,16 @@ int block_contractions(const BwdWs& w, const uint16_t* H, int64_t ldh, int64_t N
                        int dh_bf16, int64_t lddh, float* dW, int64_t lddw, const float* dW_in, hipStream_t st) {
   int rc;
   const int64_t np = cdiv(N, BLK) * BLK;
+  const int64_t kx = extra_cols(K);
   if (dH != nullptr) {
     const Operand Aop{w.G, 0, N, w.vp, np * BLK, 1};
     const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
+    const Operand Xop{w.Wt + (K - kx) * BLK, BLK, kx, w.vp, K * BLK};
     const int nk = (int)(w.vp / BK);
     rc = dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st, nullptr, nullptr, nullptr, nullptr,
-                                     nullptr, nullptr, nullptr, PROF_GEMM_DH)
+                                     nullptr, nullptr, nullptr, PROF_GEMM_DH, kx ? &Xop : nullptr, w.xpart)
                  : launch_gemm<false>(Aop, Bop, nk, N, K, 4, dH, lddh, w.part, st, nullptr, nullptr, nullptr, nullptr,
-                                      nullptr, nullptr, nullptr, PROF_GEMM_DH);
+                                      nullptr, nullptr, nullptr, PROF_GEMM_DH, kx ? &Xop : nullptr, w.xpart);
     if (rc) return rc;
   }
   if (dW == nullptr) return MCE_OK;
@@ -2680,8 +2863,9 @@ int block_contractions(const BwdWs& w, const uint16_t* H, int64_t ldh, int64_t N
   if ((rc = launch_status())) return rc;
   const Operand Aop{w.G, np * BLK, V, np, CM_TILE, 2};
   const Operand Bop{w.Ht, BLK, K, np, K * BLK, 0};
+  const Operand Xop{w.Ht + (K - kx) * BLK, BLK, kx, np, K * BLK, 0};
   return launch_gemm<false>(Aop, Bop, (int)(np / BK), V, K, 4, dW, lddw, w.part, st, nullptr, nullptr, dW_in, nullptr,
-                            nullptr, nullptr, nullptr, PROF_GEMM_DW);
+                            nullptr, nullptr, nullptr, PROF_GEMM_DW, kx ? &Xop : nullptr, w.xpart);
 }
 
 // The whole recompute backward of every variant, block by block: per block the logits gradient (grad_launch),
@@ -2741,7 +2925,7 @@ int bwd_blocked_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t 
 struct TrainWs {
   int64_t np, vp, nb, nblk;
   uint16_t *G, *Ht, *uperm, *Wt;
-  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *cb, *lse_est, *arow, *upart, *part, *dbias_part, *sum_part;
+  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *cb, *lse_est, *arow, *upart, *part, *xpart, *dbias_part, *sum_part;
   int *flag, *flag_list, *counts, *xlist;
   size_t bytes;
 };
@@ -2796,6 +2980,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   w.upart = reinterpret_cast<float*>(
       take(sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.vp / BM) * cdiv(K, BN) + TAIL_SLOTS)));
   w.part = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * BM * BN));
+  w.xpart = reinterpret_cast<float*>(take(sizeof(float) * TAIL_SLOTS * 2 * 32 * 32));
   w.dbias_part = reinterpret_cast<float*>(take(sizeof(float) * DBIAS_SPLITS * w.vp));
   w.sum_part = reinterpret_cast<float*>(take(sizeof(float) * cdiv(np, SUM_CHUNK)));
   w.bytes = off;
@@ -2812,16 +2997,18 @@ int train_block_grads(const TrainWs& w, int64_t b, const uint16_t* H, int64_t ld
                       const float* dW_in, float* dBias, const float* dBias_in, hipStream_t st) {
   int rc;
   const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
+  const int64_t kx = extra_cols(K);
   if (dH != nullptr) {
     const Operand Aop{w.G, 0, rows, w.vp, rp * BLK, 1};
     const Operand Bop{w.Wt, BLK, K, w.vp, K * BLK};
+    const Operand Xop{w.Wt + (K - kx) * BLK, BLK, kx, w.vp, K * BLK};   // W^T's last kx rows
     const int nk = (int)(w.vp / BK);
     rc = dh_bf16 ? launch_gemm<true>(Aop, Bop, nk, rows, K, 4, reinterpret_cast<uint16_t*>(dH) + row0 * lddh, lddh,
                                      w.part, st, w.arow + row0, go, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                     PROF_GEMM_DH)
+                                     PROF_GEMM_DH, kx ? &Xop : nullptr, w.xpart)
                  : launch_gemm<false>(Aop, Bop, nk, rows, K, 4, reinterpret_cast<float*>(dH) + row0 * lddh, lddh,
                                       w.part, st, w.arow + row0, go, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                      PROF_GEMM_DH);
+                                      PROF_GEMM_DH, kx ? &Xop : nullptr, w.xpart);
     if (rc) return rc;
   }
   if (dW == nullptr && dBias == nullptr) return MCE_OK;
@@ -2835,9 +3022,12 @@ int train_block_grads(const TrainWs& w, int64_t b, const uint16_t* H, int64_t ld
     // 65536 elements apart)
     const Operand Aop{w.G, rp * BLK, V, rp, CM_TILE, 2};
     const Operand Bop{w.Ht, BLK, K, rp, K * BLK, 0};
+    const Operand Xop{w.Ht + (K - kx) * BLK, BLK, kx, rp, K * BLK, 0};   // (a . H)^T's last kx rows
+    const bool xm = kx > 0 && dBias == nullptr;   // the dBias dot products take the extra-column slot otherwise
     int P = 1, full = 0;
     if ((rc = launch_gemm<false>(Aop, Bop, (int)(rp / BK), V, K, 4, dW, lddw, w.part, st, nullptr, go, dW_in,
-                                 dBias ? w.uperm : nullptr, w.upart, &P, &full, PROF_GEMM_DW)))
+                                 dBias ? w.uperm : nullptr, w.upart, &P, &full, PROF_GEMM_DW, xm ? &Xop : nullptr,
+                                 w.xpart)))
       return rc;
     if (dBias == nullptr) return MCE_OK;
     hipLaunchKernelGGL(k_dbias_tiles, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, w.upart, (int)cdiv(V, BM),

@@ -331,3 +331,36 @@ def test_many_blocks(monkeypatch):
     got = gpu_run(case, go=go)
     fwd, bwd = oracle_of(case, go=go)
     assert_parity(got, fwd, bwd, "20 blocks")
+
+
+EXTRA_COL_SHAPES = [
+    # K = 256 c + x: the last x columns of dH and dW formed inside the tiles of the other c (c >= 4)
+    (300, 2064, 1024, None, False),    # the folded layout's d + 16, 8 tile columns (one row group per tile)
+    (300, 1040, 3000, 2990, False),    # d = 1024 + 16: 4 tile columns, two row groups per tile
+    (513, 2056, 2051, None, False),    # x = 8
+    (513, 2080, 700, None, True),      # x = 32 (a whole MFMA width); with a bias, dW forms dBias instead
+    (260, 1048, 1300, 1290, True),     # x = 24
+]
+
+
+@pytest.mark.parametrize("path", ["one_pass", "blocks256", "recompute", "recompute_blocks"])
+@pytest.mark.parametrize("shape", EXTRA_COL_SHAPES, ids=lambda s: "N{}_K{}_V{}_vr{}_b{}".format(*s))
+def test_extra_columns_inside_the_tiles(shape, path, monkeypatch):
+    """Widths K = 256 c + x (0 < x <= 32, c >= 4): dH's and dW's last x columns come from one extra MFMA per row
+    group and stage inside the other tiles (and from k_xtail_reduce for K-split tail tiles), on the one-pass and
+    recompute paths, in one block and in 256-row blocks, with bf16 and fp32 h."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", path.startswith("recompute"))
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256 if path.endswith("blocks256") or path.endswith("_blocks") else 0)
+    N, K, V, vr, bias = shape
+    print(f"extra columns {shape} {path}", flush=True)
+    case = random_case(N, K, V, vr, bias, seed=N + K + V + 11)
+    go = 1.0 / N
+    fwd, bwd = oracle_of(case, go=go)
+    for h_dtype in (torch.bfloat16, torch.float32):
+        got = gpu_run(case, go=go, h_dtype=h_dtype)
+        assert_parity(got, fwd, bwd, f"extra columns {shape} {path} h={h_dtype}")
+        # the extra columns themselves, which a global norm over K columns could hide
+        x = K % 256
+        for key in ("dh", "dw"):
+            assert orc.rel_fro(got[key][:, K - x:], bwd[key][:, K - x:]) <= GRAD_RTOL, (key, "extra columns")
