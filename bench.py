@@ -764,8 +764,9 @@ def main():
     # class present runs one N x V x d contraction per step, over one or several launches (row blocks)
     nr = fold_nr(d) if (args.op == "fused_ce" and args.path == "one-pass" and not folded) else 0  # dBias in dW
     names = [k.format(nr=nr) for k in PROF_KERNELS]
-    if folded and args.path == "recompute":   # K = d + 16: the statistics-only logits tiles take the checked loads
-        names = [k.replace("<true>", "<false>") if k.startswith(("k_fwd_tiles", "k_bwd_grad")) else k for k in names]
+    if folded:   # K = d + 16: the logits tiles take the checked-load variant
+        names = [k.replace("<true>", "<false>") if k.startswith(("k_fwd_train", "k_fwd_tiles", "k_bwd_grad")) else k
+                 for k in names]
     kernels = {names[c]: (kern_ms[c], kern_n[c] // args.steps) for c in range(len(PROF_KERNELS)) if kern_n[c] > 0}
     tok_s = n / dt
     flops = 6.0 * n * v * d

@@ -248,11 +248,6 @@ MCE_API int mce_bwd_lse_blocked(const uint16_t* H, int64_t ldh, const uint16_t* 
 #define MCE_GRAD_H 1     /* want: dH */
 #define MCE_GRAD_W 2     /* want: dW */
 #define MCE_GRAD_BIAS 4  /* want: dBias (needs bias) */
-/* want flag of the training forward: columns K .. kr-1 of every row of H and W are zero, kr = K rounded up to a
- * multiple of 64, and ldh, ldw >= kr (when W32 is given the call writes those columns of W as zeros itself). The
- * logits are then reduced over kr, so a K that is not a multiple of 64 (the folded-bias layout's d + 16) needs no
- * per-load bound checks; results are those of K. No counterpart in the reference. */
-#define MCE_ZERO_PAD 8
 MCE_API size_t mce_train_ws_bytes(int64_t N, int64_t K, int64_t V, int64_t block_rows);
 
 /* Rows per block of the training path for this shape (the last block holds the rest). No counterpart in the

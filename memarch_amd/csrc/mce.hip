@@ -683,12 +683,48 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // loop-invariant fragment addresses (immediate offsets) and unchecked load offsets keep VALU work out of the
 // interleave; the loop is unrolled by two stages so the ring buffer of every read and load is a constant.
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
-template <bool KF, bool BIAS = false, int AM = 0, int DB = 0, bool XM = false>
+// The last K slice of a logits tile whose K extent is 64 nf + r, 0 < r <= 16 (the folded-bias layout's d + 16),
+// after its nf whole stages: the 16 k-values k0 .. k0+15 of A's and B's 256 rows (zeros past the extents) go into
+// LDS as [256 rows][16 k] images with 32-byte rows (A at 0, B at 8 KiB; the ring is free once the mainloop's last
+// barrier has passed), and each wave multiplies its 4 x 4 blocks once: one slice of MFMA work instead of a whole
+// stage of zeros. 16 load instructions of 32 rows each (lane l: row l/2, 16-byte chunk l%2), A's by waves 0-1 and
+// B's by waves 2-3. Row-major operands only.
+__device__ __forceinline__ void tail_slice(const Operand& A, const Operand& B, int64_t k0, int64_t m0, int64_t n0,
+                                           char* lds, f32x16 (&acc)[4][4], int wave, int lane, int wm, int wn) {
+  const bool isb = wave >= 2;   // uniform per wave
+  const Operand& op = isb ? B : A;
+  const int64_t r0 = isb ? n0 : m0;
+  const i32x4 rs = make_rsrc(reinterpret_cast<uint64_t>(op.p + r0 * op.ld));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int ins = wave * 4 + q;
+    const int row = (ins & 7) * 32 + (lane >> 1);
+    const int64_t k = k0 + (lane & 1) * 8;
+    const int off = (r0 + row < op.mext && k < op.kext) ? (int)(row * op.ld * 2 + k * 2) : OOB;
+    buffer_load_lds(rs, (uint32_t LDS_AS*)(lds + ins * 1024), 16, off, 0, 0, 0);
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  bf16x8 a[4], b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                          lds + (wm * 128 + 32 * i + (lane & 31)) * 32 + (lane >> 5) * 16));
+    b[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                          lds + 8192 + (wn * 128 + 32 * i + (lane & 31)) * 32 + (lane >> 5) * 16));
+  }
+  mma16(acc, a, b);
+}
+
+// T16: A.kext = B.kext = 64 nk + r with 0 < r <= 16, nk >= 1 whole stages in the mainloop (KF loads), then the
+// tail slice (tail_slice).
+template <bool KF, bool BIAS = false, int AM = 0, int DB = 0, bool XM = false, bool T16 = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
                                           int64_t Vreal = 0, DotState<DB ? DB : 1>* dp = nullptr, int rg0 = 0,
                                           int rg_step = 8) {
   static_assert(!XM || (DB > 0 && KF), "the extra-column mode needs row groups and whole K stages");
+  static_assert(!T16 || (KF && AM == 0 && DB == 0), "the tail slice follows whole stages of row-major operands");
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: LDS destinations stay scalar
@@ -773,7 +809,16 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   if (kt < nk) gemm_stage<0, KF, DB, AM, XM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   wait_vmcnt<0>();
   __syncthreads();
+  if constexpr (T16) {
+    tail_slice(A, B, (int64_t)(s0 + nk) * BK, m0, n0, lds, acc, wave, lane, wm, wn);
+    __syncthreads();   // the caller may reuse LDS
+  }
   mfma_drain();
+}
+// Whole stages of a K extent for gemm_tile: all of them, or with T16 the whole ones before the tail slice.
+template <bool T16>
+__device__ __forceinline__ int stages_of(int64_t kext) {
+  return (int)(T16 ? kext / BK : (kext + BK - 1) / BK);
 }
 
 // Tile-rows per group of the logits tile kernels (k_fwd_tiles, k_bwd_grad, k_fwd_train): an XCD's 32 resident tiles
@@ -878,7 +923,7 @@ __device__ __forceinline__ void target_pass(const TargetArgs& ta, const f32x16 (
 // Forward tile: S^T[v, n] for a 256(v) x 256(n) tile. Each wave reduces its own 128 vocabulary rows, so the
 // partials are per half-tile: part_m / part_s [2*tiles_v][N] hold the max and sum of exp of row block
 // 2*tm + wm for every column n. No LDS and no barrier after the mainloop. KF: K is a multiple of BK.
-template <bool KF>
+template <bool KF, bool T16 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64_t N, int64_t V, int64_t Vreal,
                  int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s, TargetArgs ta) {
@@ -893,7 +938,7 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
   stash_targets(ta, tslot, n0 + wn * 128, N, Vreal, v0 + wm * 128, lr, lh);
   f32x16 acc[4][4];
   // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
-  gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+  gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
                       reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
   target_pass(ta, acc, tslot, n0 + wn * 128, lr);
 
@@ -1498,7 +1543,7 @@ __device__ __forceinline__ int fix_lower_bound(const int* __restrict__ fix_col, 
   return a;
 }
 
-template <bool KF>
+template <bool KF, bool T16 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const int* __restrict__ ty,
                 const float* __restrict__ tval, const float* __restrict__ lse_rows,
@@ -1531,7 +1576,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
 
   f32x16 acc[4][4];
   // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
-  gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+  gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
                       reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
   // element (mi, r) of a block is vocabulary row vw + mi*32 + 8*(r/4) + 4*lh + r%4: the local index
   // mi*32 + 8*(r/4) + r%4 is compared with (v - vw - 4*lh), which never matches when v belongs to the other half
@@ -1721,7 +1766,7 @@ __global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_
 // elements, rounded to bf16 and stored into G exactly as k_bwd_grad stores it (store_g_block). The
 // half-tile partials are (e_n, sum of E) -- or, for a flagged row, (max, sum of exp(x - max)) -- in the part_m /
 // part_s format k_fwd_merge reads. Rows past N use e = +inf, so their E is exactly zero.
-template <bool KF>
+template <bool KF, bool T16 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const float* __restrict__ lse_est,
                  int64_t N, int64_t Np, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, float s_max,
@@ -1745,7 +1790,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
   stash_targets(ta, tslot, n0 + wn * 128, N, Vreal, v0 + wm * 128, lr, lh);
 
   f32x16 acc[4][4];
-  gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+  gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
                       reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
   target_pass(ta, acc, tslot, n0 + wn * 128, lr);
   uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
@@ -1864,7 +1909,7 @@ __global__ __launch_bounds__(256) void k_gather_rows(const uint16_t* __restrict_
   }
 }
 
-template <bool KF>
+template <bool KF, bool T16 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, const float* __restrict__ bias,
                    const int* __restrict__ count, const int* __restrict__ list, const float* __restrict__ lse_rows,
@@ -1888,7 +1933,7 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
       lb[nj] = nrow[nj] >= 0 ? lse_rows[nrow[nj]] * LOG2E : INFINITY;
     }
     f32x16 acc[4][4];
-    gemm_tile<KF, true>(Wop, Hop, 0, (int)((Wop.kext + BK - 1) / BK), v0, n0, lds, acc, btile,
+    gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
                         reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
@@ -2034,12 +2079,11 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 }
 
 // The bf16 cast of an fp32 weight and its K-blocked transpose in one pass: w16[r, c] = bf16(src[r, c]) (round to
-// nearest even) for r < R, c < C (row stride ld16), and 0 for C <= c < Cpad (a zero-padded row, Cpad <= the grid's
-// columns); when dst is not null, dst as k_transpose_blocked writes it from w16 over the C columns (zero for
-// R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile.
+// nearest even) for r < R, c < C (row stride ld16), and, when dst is not null, dst as k_transpose_blocked writes it
+// from w16 (zero for R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile.
 __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict__ src, int64_t ld32, int64_t R,
                                                         int64_t C, uint16_t* __restrict__ w16, int64_t ld16,
-                                                        uint16_t* __restrict__ dst, int64_t Cpad) {
+                                                        uint16_t* __restrict__ dst) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64][66];
   const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
@@ -2056,8 +2100,6 @@ __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict_
       pk[2] = pack_bf16x2(b.x, b.y);
       pk[3] = pack_bf16x2(b.z, b.w);
       *reinterpret_cast<u32x4*>(w16 + r * ld16 + c) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-    } else if (r < R && c < Cpad) {
-      *reinterpret_cast<u32x4*>(w16 + r * ld16 + c) = u32x4{0u, 0u, 0u, 0u};   // the zero padding columns
     }
     uint32_t* row = reinterpret_cast<uint32_t*>(&tile[rl][cl]);
 #pragma unroll
@@ -2369,6 +2411,20 @@ template <typename T>
 inline T* at(T* p, int64_t off) { return p == nullptr ? nullptr : p + off; }
 // Row groups per tile for the dot products of k_gemm<.., DB> over a grid `tiles_n` tiles wide: the 8 row groups of a
 // tile row are spread over its first min(tiles_n, 8) tiles.
+// Logits-tile variant for a K extent: whole stages only (KF), whole stages and one 16-wide tail slice (T16: K % 64 in
+// 1 .. 16, the folded-bias layout's d + 16), or per-load bound checks (any other K).
+enum { KM_CHECKED = 0, KM_WHOLE = 1, KM_TAIL16 = 2 };
+inline int kmode(int64_t K) { return K % BK == 0 ? KM_WHOLE : (K > BK && K % BK <= 16) ? KM_TAIL16 : KM_CHECKED; }
+#define MCE_LAUNCH_KM(KERNEL, K_, ...)                                                 \
+  do {                                                                                \
+    const int km_ = kmode(K_);                                                        \
+    if (km_ == KM_WHOLE)                                                              \
+      hipLaunchKernelGGL((KERNEL<true, false>), __VA_ARGS__);                        \
+    else if (km_ == KM_TAIL16)                                                        \
+      hipLaunchKernelGGL((KERNEL<true, true>), __VA_ARGS__);                         \
+    else                                                                              \
+      hipLaunchKernelGGL((KERNEL<false, false>), __VA_ARGS__);                       \
+  } while (0)
 inline int fold_nr(int64_t tiles_n) { return tiles_n >= 8 ? 1 : (int)cdiv(8, tiles_n); }
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // Extra columns formed inside the tiles (k_gemm's XM) for an output width K = 256 c + x, 0 < x <= 32, c >= 4 (1 or 2
@@ -2695,12 +2751,8 @@ int fwd_launch(const FwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* W
   {
     ProfScope prof(PROF_FWD_TILES, st);
     const TargetArgs ta{y, cand, cval, kc, xy};
-    if (K % BK == 0)
-      hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
-                         tn, w.part_m, w.part_s, ta);
-    else
-      hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv,
-                         tn, w.part_m, w.part_s, ta);
+    MCE_LAUNCH_KM(k_fwd_tiles, K, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, tv, tn,
+                  w.part_m, w.part_s, ta);
   }
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(k_fwd_merge, dim3((unsigned)cdiv(N, 32)), dim3(256), 0, st, w.part_m, w.part_s, xy, w.cb, w.xc,
@@ -2762,14 +2814,9 @@ int grad_launch(const BwdWs& w, const uint16_t* H, int64_t ldh, const uint16_t* 
   }
   {
     ProfScope prof(PROF_BWD_GRAD, st);
-    if (K % BK == 0)
-      hipLaunchKernelGGL(k_bwd_grad<true>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, np, V, w.vp, V_real, tv, tn, w.G,
-                         dBias ? w.dbias_part : nullptr);
-    else
-      hipLaunchKernelGGL(k_bwd_grad<false>, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval,
-                         lse_rows, wgt_rows, w.fix_col, w.fix_val, kc, go, N, np, V, w.vp, V_real, tv, tn, w.G,
-                         dBias ? w.dbias_part : nullptr);
+    MCE_LAUNCH_KM(k_bwd_grad, K, dim3(tv * tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.ty, w.tval, lse_rows,
+                  wgt_rows, w.fix_col, w.fix_val, kc, go, N, np, V, w.vp, V_real, tv, tn, w.G,
+                  dBias ? w.dbias_part : nullptr);
   }
   if ((rc = launch_status())) return rc;
   if (dBias) {
@@ -2958,7 +3005,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
     return p;
   };
   w.G = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * nb));
-  w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb * cdiv(K, BK) * BK));  // also the exact pass's rows
+  w.Ht = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb * K));
   w.uperm = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nb));
   w.part_m = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
   w.part_s = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
@@ -3062,11 +3109,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   if (!rc) rc = check_sparse(cand, cval, kc, N);
   if (!rc && kc > 0 && gate != nullptr) rc = MCE_EINVAL;  // the sparse bias is for plain cross-entropy
   if (rc) return rc;
-  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~15)) return MCE_EINVAL;
-  // MCE_ZERO_PAD: the logits are reduced over kr = K rounded up to BK, the columns K .. kr-1 of H and W being zero
-  const bool zpad = (want & MCE_ZERO_PAD) != 0 && K % BK != 0;
-  const int64_t kr = zpad ? cdiv(K, BK) * BK : K;
-  if (ldh < kr || ldw < kr) return MCE_EINVAL;
+  if (loss_sum == nullptr || (gate == nullptr) != (hit == nullptr) || block_rows < 0 || (want & ~7)) return MCE_EINVAL;
   if ((want & MCE_GRAD_BIAS) && bias == nullptr) return MCE_EINVAL;
   if (W32 != nullptr && (ldw32 < K || ldw32 % 4 || (reinterpret_cast<uintptr_t>(W32) & 15))) return MCE_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -3083,13 +3126,12 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   if (more && (want & MCE_GRAD_H) && !dh_aligned(dH_part, lddh, dh_bf16)) return MCE_EALIGN;
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
   const int tv = (int)(w.vp / BM), tn = (int)cdiv(N, BN);
-  const Operand Wop{W, ldw, V, kr, 0};
-  const bool kf = kr % BK == 0;
+  const Operand Wop{W, ldw, V, K, 0};
   // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V; with
   // W32 the bf16 W itself comes from the same pass
   if (W32 != nullptr) {
     hipLaunchKernelGGL(k_cast_transpose, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W32,
-                       ldw32, V, K, W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr, kr);
+                       ldw32, V, K, W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr);
     if ((rc = launch_status())) return rc;
   } else if (want & MCE_GRAD_H) {
     hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,
@@ -3101,14 +3143,10 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   if ((rc = launch_status())) return rc;
   {
     // e_n: the first vocabulary tile (one tile row of k_fwd_tiles over all rows) and the target logit
-    const Operand Hop{H, ldh, N, kr, 0};
+    const Operand Hop{H, ldh, N, K, 0};
     const TargetArgs none{nullptr, nullptr, nullptr, 0, nullptr};  // k_fwd_train writes the target logits
-    if (kf)
-      hipLaunchKernelGGL(k_fwd_tiles<true>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
-                         w.p0m, w.p0s, none);
-    else
-      hipLaunchKernelGGL(k_fwd_tiles<false>, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn,
-                         w.p0m, w.p0s, none);
+    MCE_LAUNCH_KM(k_fwd_tiles, K, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn, w.p0m, w.p0s,
+                  none);
     if ((rc = launch_status())) return rc;
   }
   hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, w.cb,
@@ -3118,17 +3156,12 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   for (int64_t b = 0; b < w.nblk; ++b) {
     const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
     const int tnb = (int)(rp / BN);
-    const Operand Hop{H + row0 * ldh, ldh, rows, kr, 0};
+    const Operand Hop{H + row0 * ldh, ldh, rows, K, 0};
     {
       ProfScope prof(PROF_FWD_TRAIN, st);
       const TargetArgs ta{y + row0, at(cand, row0 * kc), at(cval, row0 * kc), kc, w.xy + row0};
-      if (kf)
-        hipLaunchKernelGGL(k_fwd_train<true>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est + row0,
-                           rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s, w.flag + row0, ta);
-      else
-        hipLaunchKernelGGL(k_fwd_train<false>, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias,
-                           w.lse_est + row0, rows, rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s,
-                           w.flag + row0, ta);
+      MCE_LAUNCH_KM(k_fwd_train, K, dim3(tv * tnb), dim3(NTHREADS), 0, st, Wop, Hop, bias, w.lse_est + row0, rows,
+                    rp, V, V_real, tv, tnb, s_max, w.G, w.part_m, w.part_s, w.flag + row0, ta);
     }
     if ((rc = launch_status())) return rc;
     int* xcount = w.counts + w.np / BLK + b;
@@ -3147,14 +3180,10 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     if ((rc = launch_status())) return rc;
     // the flagged rows' exact E' (the block's H^T buffer, rewritten later, holds their gathered rows)
     hipLaunchKernelGGL(k_gather_rows, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, w.flag_list,
-                       w.counts + b, kr, w.Ht);
+                       w.counts + b, K, w.Ht);
     if ((rc = launch_status())) return rc;
-    if (kf)
-      hipLaunchKernelGGL(k_exact_train<true>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, kr, bias,
-                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
-    else
-      hipLaunchKernelGGL(k_exact_train<false>, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, kr, bias,
-                         w.counts + b, w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
+    MCE_LAUNCH_KM(k_exact_train, K, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias, w.counts + b,
+                  w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     if ((rc = launch_status())) return rc;
     hipLaunchKernelGGL(k_exact_fix, dim3((unsigned)(rp / 256)), dim3(256), 0, st, w.counts + b, w.flag_list, y + row0,
                        w.xy + row0, at(cand, row0 * kc), w.cb + row0 * kc, w.xc + row0 * kc, kc, lse_rows + row0,

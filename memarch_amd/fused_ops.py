@@ -30,7 +30,6 @@ MAX_KC = 64  # sparse candidates per row of linear_ce_sparse (the library's limi
 RECOMPUTE = os.environ.get("MEMARCH_AMD_RECOMPUTE", "0") == "1"   # True: the two-pass (recompute) backward
 BLOCK_ROWS = int(os.environ.get("MEMARCH_AMD_BLOCK_ROWS", "0"))   # rows per block of the one-pass path (0: library)
 GRAD_H, GRAD_W, GRAD_BIAS = 1, 2, 4   # MCE_GRAD_* of include/mce.h
-ZERO_PAD = 8                          # MCE_ZERO_PAD
 # Diagnostics: when set to a one-element int32 tensor on the device, every one-pass forward adds to it the number of
 # rows its exact fallback pass rewrote (mce_train_flagged, asynchronous).
 FLAGGED = None
@@ -57,26 +56,22 @@ def _row_stride(kp):
     return (kp + 63) // 64 * 64
 
 
-def _bf16_operand(t, kp, zero_pad=False):
+def _bf16_operand(t, kp):
     """bf16 view of a 2-D operand [R, kp] (zero-padded to kp columns when the width is not a multiple of 8) whose
     row stride is a multiple of 64 and whose base is 16-byte aligned: the operand itself when it already is one,
-    else a copy with the row stride _row_stride(kp). zero_pad: every row is zero from column kp up to the row stride
-    (the MCE_ZERO_PAD layout; always a copy when kp is not a multiple of 64)."""
+    else a copy with the row stride _row_stride(kp)."""
     t = t.detach()
     k = t.shape[1]
-    rs = _row_stride(kp)
-    if not (zero_pad and rs > kp):
-        if t.dtype == _BF16 and k == kp and t.stride(1) == 1 and t.stride(0) % 64 == 0 and t.data_ptr() % 16 == 0:
-            return t
-        if k == kp and kp % 64 == 0:
-            c = t.to(_BF16).contiguous()   # a contiguous copy already has the row stride
-            if c.data_ptr() % 16 == 0:
-                return c
-    full = torch.empty(t.shape[0], rs, dtype=_BF16, device=t.device)
-    out = full[:, :kp]
+    if t.dtype == _BF16 and k == kp and t.stride(1) == 1 and t.stride(0) % 64 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    if k == kp and kp % 64 == 0:
+        c = t.to(_BF16).contiguous()   # a contiguous copy already has the row stride
+        if c.data_ptr() % 16 == 0:
+            return c
+    out = torch.empty(t.shape[0], _row_stride(kp), dtype=_BF16, device=t.device)[:, :kp]
     out[:, :k] = t
-    if (rs if zero_pad else kp) > k:
-        full[:, k:rs if zero_pad else kp].zero_()
+    if kp > k:
+        out[:, k:].zero_()
     return out
 
 
@@ -121,21 +116,15 @@ def _fwd_launch(h, w, bias, y, gate, hit, v_real, cand=None, cval=None, train=Fa
     _check_cuda(h, w, bias, y, gate, hit, cand, cval)
     kp = (k + 7) // 8 * 8
     dev = h.device
-    # the training forward with K not a multiple of 64 (the folded layout's d + 16): zero-padded rows, so that the
-    # logits are reduced over the padded width without bound checks (MCE_ZERO_PAD)
-    zpad = train and kp % 64 != 0
-    hd = _bf16_operand(h, kp, zero_pad=zpad)
+    hd = _bf16_operand(h, kp)
     w32 = None
     if train and w.dtype == torch.float32 and k == kp and w.stride(1) == 1 and w.stride(0) % 4 == 0 \
             and w.data_ptr() % 16 == 0:
-        # the one-pass forward casts the fp32 weight itself, in the pass that also forms its transpose (and zeroes
-        # the padding columns)
+        # the one-pass forward casts the fp32 weight itself, in the pass that also forms its transpose
         w32 = w.detach()
         wd = torch.empty(v, _row_stride(kp), dtype=_BF16, device=dev)[:, :kp]
     else:
-        wd = _bf16_operand(w, kp, zero_pad=zpad)
-    if zpad:
-        want |= ZERO_PAD
+        wd = _bf16_operand(w, kp)
     y64 = _rows(y, torch.int64)
     gf = None if gate is None else _rows(gate, torch.float32)   # None: g = 0 (plain cross-entropy)
     hf = None if hit is None else _rows(hit, torch.float32)

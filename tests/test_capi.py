@@ -201,18 +201,3 @@ def test_recompute_blocks_argument_checks(lib):
     assert call(kc=65) == 1
     assert lib.mce_bwd_lse_blocked(p, 8, p, 8, None, p, p, None, p, 600, 8, 32, 32, 0, p, 1, 8, None, 8, None, p, 16,
                                    None) == 1    # g_lse missing
-
-
-def test_zero_pad_flag_checks(lib):
-    """MCE_ZERO_PAD (want bit 8): the row strides must cover K rounded up to 64; an unknown want bit is rejected."""
-    buf = ctypes.create_string_buffer(1 << 12)
-    p = ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 256
-
-    def fwd(want, K=72, ld=72):
-        return lib.mce_fwd_train(p, ld, p, ld, None, 0, None, p, p, p, 600, K, 32, 32, 0, want, p, p, p, p, p, None,
-                                 1, K, None, K, None, p, 16, None)
-
-    assert fwd(1 | 8) == 1                       # K = 72 pads to 128 > the row strides
-    assert fwd(1 | 8, ld=128) == 3               # strides cover the padding: fails on the small workspace
-    assert fwd(1 | 8, K=64, ld=64) == 3          # K a multiple of 64: nothing to pad
-    assert fwd(16) == 1                          # no such flag
