@@ -52,9 +52,20 @@ STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_
                  "mce_bwd_dweight": "dweight", "mce_fwd_sparse": "fwd", "mce_bwd_logits_grad_sparse": "logits_grad",
                  "mce_lse_fwd": "fwd", "mce_bwd_lse_grad": "logits_grad", "mce_bwd_blocked": "bwd",
                  "mce_bwd_lse_blocked": "bwd"}
-# kernel classes of mce_prof_stop (include/mce.h) -> kernel name; each class runs one N x V x d contraction per step
-PROF_KERNELS = ("k_fwd_train<true>", "k_fwd_tiles<true>", "k_bwd_grad<true>", "k_gemm<true, true, 1, 0>",
-                "k_gemm<false, true, 2, {nr}>")
+# kernel classes of mce_prof_stop (include/mce.h) -> kernel name (rocprofv3's); each class runs one N x V x d
+# contraction per step. {t16}: the logits tiles' K tail (true for K = d + 16, the folded layout); {nr}: the row
+# groups per dW tile (dBias on the one-pass path, the extra columns with {xm}); {xm}: the output columns past the
+# whole 256-wide tiles formed inside them (the folded layout's last 16 columns).
+PROF_KERNELS = ("k_fwd_train<true, {t16}>", "k_fwd_tiles<true, {t16}>", "k_bwd_grad<true, {t16}>",
+                "k_gemm<true, true, 1, {nx}, {xm}>", "k_gemm<false, true, 2, {nr}, {xm}>")
+
+
+def kernel_names(d, folded, dbias):
+    """The PROF_KERNELS names at hidden size d (a multiple of 256) for the biased call shape (dbias: dW carries
+    dBias, the one-pass path) or the folded one (K = d + 16)."""
+    nr = fold_nr(d) if (folded or dbias) else 0
+    fmt = dict(t16="true" if folded else "false", xm="true" if folded else "false", nx=nr if folded else 0, nr=nr)
+    return [k.format(**fmt) for k in PROF_KERNELS]
 # the siblings of the north-star op (--op): the same contractions on the same configuration inputs
 SIBLING_OPS = ("linear_ce", "linear_ce_sparse", "chunk_ce")
 
@@ -762,11 +773,7 @@ def main():
     stages = {k: sum(x) / args.steps for k, x in live.items()}
     # the contraction kernels, timed by the library's HIP events around each launch on the launch stream: every
     # class present runs one N x V x d contraction per step, over one or several launches (row blocks)
-    nr = fold_nr(d) if (args.op == "fused_ce" and args.path == "one-pass" and not folded) else 0  # dBias in dW
-    names = [k.format(nr=nr) for k in PROF_KERNELS]
-    if folded:   # K = d + 16: the logits tiles take the checked-load variant
-        names = [k.replace("<true>", "<false>") if k.startswith(("k_fwd_train", "k_fwd_tiles", "k_bwd_grad")) else k
-                 for k in names]
+    names = kernel_names(d, folded, args.op == "fused_ce" and args.path == "one-pass")
     kernels = {names[c]: (kern_ms[c], kern_n[c] // args.steps) for c in range(len(PROF_KERNELS)) if kern_n[c] > 0}
     tok_s = n / dt
     flops = 6.0 * n * v * d

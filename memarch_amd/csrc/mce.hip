@@ -685,12 +685,15 @@ __device__ __forceinline__ void read_bias_mask(float (&bm)[4][16], const float* 
 // The final wait + barrier lets the caller reuse LDS as soon as this returns.
 // The last K slice of a logits tile whose K extent is 64 nf + r, 0 < r <= 16 (the folded-bias layout's d + 16),
 // after its nf whole stages: the 16 k-values k0 .. k0+15 of A's and B's 256 rows (zeros past the extents) go into
-// LDS as [256 rows][16 k] images with 32-byte rows (A at 0, B at 8 KiB; the ring is free once the mainloop's last
-// barrier has passed), and each wave multiplies its 4 x 4 blocks once: one slice of MFMA work instead of a whole
-// stage of zeros. 16 load instructions of 32 rows each (lane l: row l/2, 16-byte chunk l%2), A's by waves 0-1 and
-// B's by waves 2-3. Row-major operands only.
-__device__ __forceinline__ void tail_slice(const Operand& A, const Operand& B, int64_t k0, int64_t m0, int64_t n0,
-                                           char* lds, f32x16 (&acc)[4][4], int wave, int lane, int wm, int wn) {
+// LDS as [256 rows][16 k] images with 32-byte rows (A at TAIL_OFF, B at TAIL_OFF + 8 KiB, outside the operand ring
+// and the bias / target slots) at the start of the tile, so their latency hides under the mainloop, and each wave
+// multiplies its 4 x 4 blocks once after the last stage: one slice of MFMA work instead of a whole stage of zeros.
+// 16 load instructions of 32 rows each (lane l: row l/2, 16-byte chunk l%2), A's by waves 0-1 and B's by waves 2-3.
+// Row-major operands only.
+constexpr int TAIL_OFF = LDS_BYTES + 2048, TAIL_BYTES = 2 * BM * 32;
+static_assert(TAIL_OFF + TAIL_BYTES <= 160 * 1024, "tail slice image exceeds the LDS of a CU");
+__device__ __forceinline__ void issue_tail(const Operand& A, const Operand& B, int64_t k0, int64_t m0, int64_t n0,
+                                           char* lds, int wave, int lane) {
   const bool isb = wave >= 2;   // uniform per wave
   const Operand& op = isb ? B : A;
   const int64_t r0 = isb ? n0 : m0;
@@ -701,23 +704,25 @@ __device__ __forceinline__ void tail_slice(const Operand& A, const Operand& B, i
     const int row = (ins & 7) * 32 + (lane >> 1);
     const int64_t k = k0 + (lane & 1) * 8;
     const int off = (r0 + row < op.mext && k < op.kext) ? (int)(row * op.ld * 2 + k * 2) : OOB;
-    buffer_load_lds(rs, (uint32_t LDS_AS*)(lds + ins * 1024), 16, off, 0, 0, 0);
+    buffer_load_lds(rs, (uint32_t LDS_AS*)(lds + TAIL_OFF + ins * 1024), 16, off, 0, 0, 0);
   }
-  wait_vmcnt<0>();
-  __syncthreads();
+}
+// The tail slice's MFMAs; its loads (issue_tail) precede the mainloop's, whose final wait + barrier covers them.
+__device__ __forceinline__ void tail_mma(const char* lds, f32x16 (&acc)[4][4], int lane, int wm, int wn) {
   bf16x8 a[4], b[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     a[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
-                                          lds + (wm * 128 + 32 * i + (lane & 31)) * 32 + (lane >> 5) * 16));
+                                          lds + TAIL_OFF + (wm * 128 + 32 * i + (lane & 31)) * 32 + (lane >> 5) * 16));
     b[i] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
-                                          lds + 8192 + (wn * 128 + 32 * i + (lane & 31)) * 32 + (lane >> 5) * 16));
+                                          lds + TAIL_OFF + 8192 + (wn * 128 + 32 * i + (lane & 31)) * 32 +
+                                          (lane >> 5) * 16));
   }
   mma16(acc, a, b);
 }
 
 // T16: A.kext = B.kext = 64 nk + r with 0 < r <= 16, nk >= 1 whole stages in the mainloop (KF loads), then the
-// tail slice (tail_slice).
+// tail slice (issue_tail, tail_mma); the caller's LDS then spans TAIL_OFF + TAIL_BYTES.
 template <bool KF, bool BIAS = false, int AM = 0, int DB = 0, bool XM = false, bool T16 = false>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
@@ -742,6 +747,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   const Stream sb = make_stream(B, n0, wave, lane);
   const FragAddr ad = make_frag_addr<AM>(wm, wn, lane);
   const int send = s0 + nk;
+  if constexpr (T16) issue_tail(A, B, (int64_t)send * BK, m0, n0, lds, wave, lane);
   // prologue: stage s0 in full, the A operand of stage s0+1 (its B operand goes out during stage s0's slice 0)
   issue_stage<AM == 2>(sa, s0, send, lds, AOFF, wave);
   issue_stage<AM == 2>(sb, s0, send, lds, BOFF, wave);
@@ -809,10 +815,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
   if (kt < nk) gemm_stage<0, KF, DB, AM, XM>(s0 + kt, send, acc, fa, fb, lds, ad, sa, sb, wave, dp);
   wait_vmcnt<0>();
   __syncthreads();
-  if constexpr (T16) {
-    tail_slice(A, B, (int64_t)(s0 + nk) * BK, m0, n0, lds, acc, wave, lane, wm, wn);
-    __syncthreads();   // the caller may reuse LDS
-  }
+  if constexpr (T16) tail_mma(lds, acc, lane, wm, wn);   // outside what the caller reuses
   mfma_drain();
 }
 // Whole stages of a K extent for gemm_tile: all of them, or with T16 the whole ones before the tail slice.
@@ -887,6 +890,7 @@ __device__ __forceinline__ int target_local(const TargetArgs& ta, int64_t n, int
 // the mainloop. Slot [nj][thread].
 constexpr int TSLOT_OFF = LDS_BYTES + BM * 4;
 constexpr int FWD_LDS_BYTES = TSLOT_OFF + 4 * NTHREADS;
+static_assert(FWD_LDS_BYTES <= TAIL_OFF, "target slots overlap the tail slice image");
 __device__ __forceinline__ void stash_targets(const TargetArgs& ta, signed char* tslot, int64_t nbase, int64_t N,
                                               int64_t Vreal, int64_t vw, int lr, int lh) {
 #pragma unroll
@@ -927,7 +931,7 @@ template <bool KF, bool T16 = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgpu_waves_per_eu(1, 1)))
 void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64_t N, int64_t V, int64_t Vreal,
                  int tiles_v, int tiles_n, float* __restrict__ part_m, float* __restrict__ part_s, TargetArgs ta) {
-  __shared__ __attribute__((aligned(1024))) char lds[FWD_LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[T16 ? TAIL_OFF + TAIL_BYTES : FWD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -1528,6 +1532,7 @@ __device__ __forceinline__ f32x16 transpose_block(const uint32_t (&pk)[8], const
 }
 
 constexpr int GRAD_LDS_BYTES = LDS_BYTES + BM * 4;  // operand ring + bias slot
+static_assert(GRAD_LDS_BYTES <= TAIL_OFF, "bias slot overlaps the tail slice image");
 
 // The first of row n's fix-ups (k_sparse_rows: sorted by column, INT32_MAX after the last) whose column is at
 // least lo: a binary search over the row's nfix slots (nfix <= 64: at most 7 steps).
@@ -1551,7 +1556,7 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
                 const float* __restrict__ fix_val, int nfix, const float* __restrict__ go, int64_t N, int64_t Np,
                 int64_t V, int64_t Vp, int64_t Vreal, int tiles_v, int tiles_n, uint16_t* __restrict__ G,
                 float* __restrict__ dbias_part) {
-  __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[T16 ? TAIL_OFF + TAIL_BYTES : GRAD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -1772,7 +1777,7 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
                  int64_t N, int64_t Np, int64_t V, int64_t Vreal, int tiles_v, int tiles_n, float s_max,
                  uint16_t* __restrict__ G, float* __restrict__ part_m, float* __restrict__ part_s,
                  int* __restrict__ flag, TargetArgs ta) {
-  __shared__ __attribute__((aligned(1024))) char lds[FWD_LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[T16 ? TAIL_OFF + TAIL_BYTES : FWD_LDS_BYTES];
   int tm, tn;
   tile_coords(tiles_v, tiles_n, FWD_GROUP, tm, tn);
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -1914,7 +1919,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(NTHREADS, NTHREADS), amdgp
 void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, const float* __restrict__ bias,
                    const int* __restrict__ count, const int* __restrict__ list, const float* __restrict__ lse_rows,
                    int64_t Np, int64_t V, int64_t Vreal, int tiles_v, uint16_t* __restrict__ G) {
-  __shared__ __attribute__((aligned(1024))) char lds[GRAD_LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[T16 ? TAIL_OFF + TAIL_BYTES : GRAD_LDS_BYTES];
   const int cnt = *count;
   const int items = tiles_v * ((cnt + BN - 1) / BN);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
@@ -2080,13 +2085,18 @@ __global__ __launch_bounds__(256) void k_transpose_blocked(const uint16_t* __res
 
 // The bf16 cast of an fp32 weight and its K-blocked transpose in one pass: w16[r, c] = bf16(src[r, c]) (round to
 // nearest even) for r < R, c < C (row stride ld16), and, when dst is not null, dst as k_transpose_blocked writes it
-// from w16 (zero for R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile.
+// from w16 (zero for R <= r < grid rows). C % 8 == 0, ld32 % 4 == 0. One workgroup per 64 x 64 tile, tiles_r x
+// tiles_c of them on a 1-D grid: each XCD (block b runs on XCD b % 8) takes a contiguous range of the row-major tile
+// order, so the column neighbours of a tile run on the same XCD at about the same time and the cache lines they
+// share (fp32 rows whose stride is not a multiple of 32 floats, as d + 16 columns give) come from its L2 once.
 __global__ __launch_bounds__(256) void k_cast_transpose(const float* __restrict__ src, int64_t ld32, int64_t R,
                                                         int64_t C, uint16_t* __restrict__ w16, int64_t ld16,
-                                                        uint16_t* __restrict__ dst) {
+                                                        uint16_t* __restrict__ dst, int tiles_c) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64][66];
   const int t = threadIdx.x;
-  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int total = (int)gridDim.x, q = total / 8, rem = total % 8;
+  const int xcd = (int)blockIdx.x % 8, tl = xcd * q + min(xcd, rem) + (int)blockIdx.x / 8;
+  const int64_t r0 = (int64_t)(tl / tiles_c) * 64, c0 = (int64_t)(tl % tiles_c) * 64;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int rl = (t >> 3) + 32 * h, cl = (t & 7) * 8;
@@ -3130,8 +3140,9 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
   // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V; with
   // W32 the bf16 W itself comes from the same pass
   if (W32 != nullptr) {
-    hipLaunchKernelGGL(k_cast_transpose, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W32,
-                       ldw32, V, K, W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr);
+    const int tiles_c = (int)cdiv(K, 64);
+    hipLaunchKernelGGL(k_cast_transpose, dim3((unsigned)(w.vp / 64 * tiles_c)), dim3(256), 0, st, W32, ldw32, V, K,
+                       W, ldw, (want & MCE_GRAD_H) ? w.Wt : nullptr, tiles_c);
     if ((rc = launch_status())) return rc;
   } else if (want & MCE_GRAD_H) {
     hipLaunchKernelGGL(k_transpose_blocked, dim3((unsigned)(w.vp / 64), (unsigned)cdiv(K, 64)), dim3(256), 0, st, W,

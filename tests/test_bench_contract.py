@@ -1,7 +1,7 @@
 """bench.py's bookkeeping, on the CPU: its command-line contract (one GPU only, the headline run by default); the
 dominant kernel of every stage at config 2 has a traffic line in the committed rocprofv3 summary (so the bench
-line's roofline.traffic is measured, not null); and the dW kernel's name follows the library's row-group count (the
-last template argument of k_gemm, fold_nr in mce.hip)."""
+line's roofline.traffic is measured, not null); and the kernel names it reports follow the library's template
+arguments (the dW kernel's row-group count, fold_nr in mce.hip) and exist in the built library."""
 import os
 import sys
 
@@ -25,10 +25,39 @@ def test_fold_nr(d, nr):
 def test_traffic_lines_cover_config2_kernels():
     """Every contraction kernel class the library times (mce_prof_stop) has a config-2 traffic line, under the
     name the bench gives it on either path (the dW kernel with its dBias row groups on the one-pass path)."""
-    for kern in bench.PROF_KERNELS:
-        for nr in {bench.fold_nr(2048), 0} if "{nr}" in kern else {0}:
-            name = kern.format(nr=nr)
+    for dbias in (True, False):
+        for name in bench.kernel_names(2048, False, dbias):
             assert bench.traffic_bytes(name, 2) is not None, name
+
+
+def test_kernel_names_follow_the_library_templates():
+    """The names the bench gives the timed kernels are the instantiations the library launches at config 2: the
+    whole-stage logits tiles and nr = 1 dBias row group per dW tile for the biased call shape; the 16-wide K tail
+    and the in-tile extra columns (nr = 1 group per tile) for the folded one (K = d + 16)."""
+    assert bench.kernel_names(2048, False, True) == [
+        "k_fwd_train<true, false>", "k_fwd_tiles<true, false>", "k_bwd_grad<true, false>",
+        "k_gemm<true, true, 1, 0, false>", "k_gemm<false, true, 2, 1, false>"]
+    assert bench.kernel_names(2048, False, False)[4] == "k_gemm<false, true, 2, 0, false>"
+    assert bench.kernel_names(2048, True, True) == [
+        "k_fwd_train<true, true>", "k_fwd_tiles<true, true>", "k_bwd_grad<true, true>",
+        "k_gemm<true, true, 1, 1, true>", "k_gemm<false, true, 2, 1, true>"]
+    assert bench.kernel_names(1024, True, True)[3:] == ["k_gemm<true, true, 1, 2, true>",
+                                                        "k_gemm<false, true, 2, 2, true>"]
+
+
+def test_kernel_names_are_instantiated_in_the_library():
+    """Every name the bench can report is a kernel the built library holds (its host-side launch symbols)."""
+    import shutil
+    import subprocess
+    so = os.path.join(ROOT, "memarch_amd", "libmce.so")
+    if not os.path.exists(so) or shutil.which("nm") is None:
+        pytest.skip("libmce.so not built or nm absent")
+    syms = subprocess.run(["nm", "-C", so], capture_output=True, text=True, check=True).stdout
+    for d in (1024, 2048):
+        for folded in (False, True):
+            for dbias in (False, True):
+                for name in bench.kernel_names(d, folded, dbias):
+                    assert f"::{name}(" in syms, name
 
 
 def test_more_than_one_gpu_is_refused():
