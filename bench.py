@@ -105,8 +105,9 @@ def _args():
     ap.add_argument("--gpu-reference-steps", type=int, default=3,
                     help="timed steps of the reference's method restated with torch ops on the same GPU (0: skip)")
     ap.add_argument("--folded-steps", type=int, default=5,
-                    help="timed steps of the caller's folded call shape (--layout folded) after the biased line's "
-                         "steps, reported as folded_ms_per_step (0: skip)")
+                    help="timed steps of the caller's folded call shape (--layout folded), each right after a timed "
+                         "biased step, reported as folded_ms_per_step over the interleaved biased steps' time "
+                         "(0: skip)")
     ap.add_argument("--library-steps", type=int, default=5,
                     help="timed calls of each full-size library GEMM of the step's three contractions, reported as "
                          "library_ceiling (0: skip)")
@@ -833,14 +834,23 @@ def main():
         h.grad = w.grad = b.grad = gate.grad = None
         f = make_folded(inp, cfg)
         for _ in range(2):
+            step()
             folded_step(f)
-        torch.cuda.synchronize()
-        t = time.perf_counter()
+        # biased and folded steps alternate, so that both shapes see the same clock and power state
+        tb = tf = 0.0
         for _ in range(args.folded_steps):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
             folded_step(f)
-        torch.cuda.synchronize()
-        res["folded_ms_per_step"] = round((time.perf_counter() - t) / args.folded_steps * 1e3, 3)
-        res["folded_over_biased"] = round(res["folded_ms_per_step"] / res["ms_per_step"], 4)
+            torch.cuda.synchronize()
+            tb, tf = tb + (t1 - t), tf + (time.perf_counter() - t1)
+        res["folded_ms_per_step"] = round(tf / args.folded_steps * 1e3, 3)
+        res["folded_over_biased"] = round(tf / tb, 4)
+        res["folded_biased_interleaved_ms"] = round(tb / args.folded_steps * 1e3, 3)
+        h.grad = w.grad = b.grad = gate.grad = None
         del f
         torch.cuda.empty_cache()
     if args.library_steps > 0 and args.op == "fused_ce" and not folded:
