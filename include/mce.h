@@ -240,8 +240,9 @@ MCE_API int mce_bwd_lse_blocked(const uint16_t* H, int64_t ldh, const uint16_t* 
  * (only the earlier blocks' dH rows are, once).
  *
  * Blocks: `block_rows` rows each (rounded up to a multiple of 256 and evened out over the blocks), or, with
- * block_rows = 0, as many as keep the block's E' (bf16, 2 * rows * V bytes) within 2 GiB: up to 21248 rows at
- * V = 50304 (two blocks of 16384 for 32768 rows), 8192 at V = 131072. mce_train_ws_bytes bounds the workspace by one block, whatever N is. The same
+ * block_rows = 0, as many as keep the block's E' (bf16, 2 * rows * V bytes) within 4 GiB: up to 42496 rows at
+ * V = 50304 (one block for 32768 rows), 16384 at V = 131072. mce_train_ws_bytes bounds the workspace by one block,
+ * whatever N is. The same
  * block_rows, `want` and buffers must be passed to the forward and the backward of one step, and the workspace
  * kept unchanged between them (it holds the last block's E' and the per-row state).
  */

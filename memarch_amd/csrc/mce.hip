@@ -2987,9 +2987,12 @@ struct TrainWs {
   size_t bytes;
 };
 constexpr int DBIAS_SPLITS = 8;
-// Memory for G of one row block when the caller leaves the block size to the library: 2 GiB, i.e. at most 21248
-// rows at V = 50304 (16384-row blocks for 32768 rows) and 8192 rows at V = 131072.
-constexpr int64_t TRAIN_BLOCK_BUDGET = int64_t(2) << 30;
+// Memory for G of one row block when the caller leaves the block size to the library: 4 GiB, i.e. at most 42496
+// rows at V = 50304 (one block for 32768 rows) and 16384 rows at V = 131072. Each block adds a pass of partial
+// sums and its own grid tails to the contractions: at 32768 x 2048 x 50304 one block (G 3.3 GB, 4.9 GB at the
+// step's peak) takes 15.3 ms per step against 15.6 ms in two blocks (3.6 GB), at V = 131072 16384-row blocks take
+// 40.4 ms against 41.5 ms in 8192-row blocks; the 288 GB of HBM leave room for the larger blocks.
+constexpr int64_t TRAIN_BLOCK_BUDGET = int64_t(4) << 30;
 
 // Rows per block: the requested count (0: the largest that keeps G within TRAIN_BLOCK_BUDGET) rounded up to a
 // multiple of 256, then evened out over the blocks it takes.

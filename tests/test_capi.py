@@ -47,24 +47,26 @@ def test_workspace_sizes(lib):
 
 
 def test_training_blocks_bound_the_workspace(lib):
-    """The one-pass path's rows per block (block_rows = 0: one block's E', 2 * rows * V bytes, within 2 GiB,
+    """The one-pass path's rows per block (block_rows = 0: one block's E', 2 * rows * V bytes, within 4 GiB,
     evened out over the blocks) and its workspace, which grows with N only through per-row arrays."""
     rows = lambda n, v, req=0: lib.mce_train_block_rows(n, 2048, v, req)
-    assert rows(32768, 50304) == 16384 and rows(32768, 131072) == 8192 and rows(16384, 50304) == 16384
+    assert rows(32768, 50304) == 32768 and rows(32768, 131072) == 16384 and rows(16384, 50304) == 16384
     assert rows(300, 1000) == 512                 # one block, N rounded up to 256
     assert rows(777, 1000, 300) == 512            # 300 -> 512 rows: two blocks
     assert rows(777, 1000, 256) == 256            # four blocks, the last with 9 rows
-    assert rows(65536, 50304) == 16384            # four blocks of at most 21248 rows
-    assert rows(1 << 20, 50304) == 20992          # 50 blocks
+    assert rows(65536, 50304) == 32768            # two blocks of at most 42496 rows
+    assert rows(1 << 20, 50304) == 41984          # 25 blocks
     for n in (32768, 65536, 1 << 20):
         nb = rows(n, 50304)
-        assert 2 * nb * 50432 <= 2 ** 31
+        assert 2 * nb * 50432 <= 2 ** 32
+    assert 2 * rows(32768, 131072) * 131072 <= 2 ** 32
     ws = lambda n, v, req=0: lib.mce_train_ws_bytes(n, 2048, v, req)
-    assert ws(32768, 50304) < 2.1e9 and ws(32768, 131072) < 2.9e9   # + W^T: 0.2 GB, 0.54 GB
+    assert ws(32768, 50304) < 3.9e9 and ws(32768, 131072) < 5.2e9   # + W^T: 0.2 GB, 0.54 GB
+    assert ws(32768, 50304, 16384) < 2.1e9        # a caller's smaller blocks bound it further
     per_row = (ws(65536, 50304, 8192) - ws(32768, 50304, 8192)) / 32768
     assert per_row < 600                          # bytes per extra row: per-row state only (64 candidates' logits
                                                   # and total biases: 512 bytes)
-    assert ws(1 << 20, 50304) < 3.2e9                 # 1M rows: 2.55 GB of blocks + 0.57 GB of per-row state
+    assert ws(1 << 20, 50304) < 5.5e9             # 1M rows: 4.8 GB of blocks + 0.57 GB of per-row state
 
 
 def test_argument_checks_need_no_gpu(lib):

@@ -143,13 +143,13 @@ def test_large_hidden(case, monkeypatch):
 @pytest.mark.parametrize("path", ["one_pass", "recompute"])
 def test_large_vocabulary(path, monkeypatch):
     """V = 256000 (1000 vocabulary tiles): the merge over 2000 half-tile partials per row, a 1000 x 1 dW grid
-    (each tile forming all 8 dBias row groups), and the library's row block for G shrinking to 4096 rows."""
+    (each tile forming all 8 dBias row groups), and the library's row block for G shrinking to 8192 rows."""
     from memarch_amd import fused_ops, _lib
     monkeypatch.setattr(fused_ops, "RECOMPUTE", path == "recompute")
     monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 0)
     print(f"large vocabulary {path}", flush=True)
     assert _lib.load().mce_train_block_rows(300, 256, 256000, 0) == 512  # N = 300 fits one block
-    assert _lib.load().mce_train_block_rows(32768, 256, 256000, 0) == 4096
+    assert _lib.load().mce_train_block_rows(32768, 256, 256000, 0) == 8192
     c = random_case(300, 256, 256000, 255900, True, seed=9)
     go = 1.0 / 300
     got = gpu_run(c, go=go)
