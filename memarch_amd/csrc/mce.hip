@@ -646,12 +646,16 @@ __device__ __forceinline__ constexpr int out_row(int mi, int r, int lh) {
 }
 
 // Bias + vocabulary mask of a tile's 256 vocabulary rows: tile_bias() reads bias[v0 + t] (one value per thread,
-// issued before the mainloop's first loads); stash_bias() stores bias or -inf (v >= V_real) into a 1 KiB LDS slot;
+// issued before the mainloop's first loads; rows past V read the last bias, which the mask below replaces, so no
+// instruction waits for the value before the tile's operand loads are issued); stash_bias() stores bias or -inf
+// (v >= V_real) into a 1 KiB LDS slot;
 // read_bias_mask() gives a lane the 64 values of its logit rows (v = v_lane + acc_row(mi, r, lh); r%4 = 0..3 are
 // consecutive, so 16 ds_read_b128). gemm_tile<.., BIAS> uses them to start the accumulators at the bias.
 __device__ __forceinline__ float tile_bias(const float* __restrict__ bias, int64_t v0, int64_t V) {
   const int64_t v = v0 + threadIdx.x;
-  return (bias != nullptr && v < V) ? bias[v] : 0.f;
+  float b = 0.f;
+  if (bias != nullptr) b = bias[v < V ? v : V - 1];
+  return b;
 }
 __device__ __forceinline__ void stash_bias(float* slot, float b, int64_t v0, int64_t Vreal) {
   slot[threadIdx.x] = (v0 + threadIdx.x < Vreal) ? b : -INFINITY;
@@ -723,11 +727,16 @@ __device__ __forceinline__ void tail_mma(const char* lds, f32x16 (&acc)[4][4], i
 
 // T16: A.kext = B.kext = 64 nk + r with 0 < r <= 16, nk >= 1 whole stages in the mainloop (KF loads), then the
 // tail slice (issue_tail, tail_mma); the caller's LDS then spans TAIL_OFF + TAIL_BYTES.
-template <bool KF, bool BIAS = false, int AM = 0, int DB = 0, bool XM = false, bool T16 = false>
+// `pre` runs once the prologue's loads are issued, before its wait: LDS stores of values the caller loaded before
+// the call, so that their load latency overlaps the operands' instead of preceding them.
+struct NoPre {
+  __device__ void operator()() const {}
+};
+template <bool KF, bool BIAS = false, int AM = 0, int DB = 0, bool XM = false, bool T16 = false, class Pre = NoPre>
 __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, int s0, int nk, int64_t m0, int64_t n0,
                                           char* lds, f32x16 (&acc)[4][4], float btile = 0.f, float* bslot = nullptr,
                                           int64_t Vreal = 0, DotState<DB ? DB : 1>* dp = nullptr, int rg0 = 0,
-                                          int rg_step = 8) {
+                                          int rg_step = 8, const Pre& pre = Pre{}) {
   static_assert(!XM || (DB > 0 && KF), "the extra-column mode needs row groups and whole K stages");
   static_assert(!T16 || (KF && AM == 0 && DB == 0), "the tail slice follows whole stages of row-major operands");
   static_assert(I::LPW == 8 && I::SLICES == 4, "slice_loads issues 8 loads over a 16-MFMA slice");
@@ -791,6 +800,7 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
     if (wave == 0) issue_ap<AM == 2>(dp->rsrc, s0 + 1, send, lds, 1);
   }
   if constexpr (BIAS) stash_bias(bslot, btile, m0, Vreal);
+  pre();
   wait_vmcnt<I::LPW>();  // with DB, wave 0's u of stage s0 precedes its last 8 loads
   __syncthreads();
   if constexpr (BIAS) {
@@ -874,29 +884,43 @@ struct TargetArgs {
   int kc;
   float* xy;
 };
-// Local index of row n's target among a lane's vocabulary rows of a wave (vw: the wave's first row; element (mi, r)
+// Local index of a target id yn among a lane's vocabulary rows of a wave (vw: the wave's first row; element (mi, r)
 // of lane half lh is row vw + mi*32 + 8(r/4) + 4lh + r%4, local index mi*32 + 8(r/4) + r%4), -1 when it is not
 // one of them: a row of the other lane half gives an index with bit 2 set (or a negative one), so exactly one lane
 // of the wave holds each target of its rows.
-__device__ __forceinline__ int target_local(const TargetArgs& ta, int64_t n, int64_t N, int64_t Vreal, int64_t vw,
-                                            int lh) {
-  if (ta.xy == nullptr || n >= N) return -1;
-  const int64_t yn = ta.y[n];
+__device__ __forceinline__ int target_index(int64_t yn, int64_t Vreal, int64_t vw, int lh) {
   const int64_t d = yn - vw - 4 * lh;
   return (yn >= 0 && yn < Vreal && d >= 0 && d < 128 && (d & 4) == 0) ? (int)d : -1;
 }
 // The lanes' target indices go through 1 KiB of LDS outside the operand ring and the bias slot (TSLOT_OFF; each
 // thread writes its own 4 bytes before the mainloop and reads them after it), so that no register holds them across
-// the mainloop. Slot [nj][thread].
+// the mainloop. Slot [nj][thread]. The targets are loaded before the tile (load_targets: rows past N, or no xy,
+// give -1) and stored into the slots by the mainloop's prologue hook once the operand loads are issued
+// (TargetStash), so that no wait for them precedes those loads.
 constexpr int TSLOT_OFF = LDS_BYTES + BM * 4;
 constexpr int FWD_LDS_BYTES = TSLOT_OFF + 4 * NTHREADS;
 static_assert(FWD_LDS_BYTES <= TAIL_OFF, "target slots overlap the tail slice image");
-__device__ __forceinline__ void stash_targets(const TargetArgs& ta, signed char* tslot, int64_t nbase, int64_t N,
-                                              int64_t Vreal, int64_t vw, int lr, int lh) {
+__device__ __forceinline__ void load_targets(const TargetArgs& ta, int64_t (&yv)[4], int64_t nbase, int64_t N,
+                                             int lr) {
 #pragma unroll
-  for (int nj = 0; nj < 4; ++nj)
-    tslot[nj * NTHREADS + threadIdx.x] = (signed char)target_local(ta, nbase + nj * 32 + lr, N, Vreal, vw, lh);
+  for (int nj = 0; nj < 4; ++nj) {
+    const int64_t n = nbase + nj * 32 + lr;
+    yv[nj] = -1;
+    if (ta.xy != nullptr) yv[nj] = ta.y[n < N ? n : N - 1];
+  }
 }
+struct TargetStash {
+  signed char* tslot;
+  int64_t yv[4];
+  int64_t nbase, N, Vreal, vw;
+  int lr, lh;
+  __device__ void operator()() const {
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj)
+      tslot[nj * NTHREADS + threadIdx.x] =
+          (signed char)(nbase + nj * 32 + lr < N ? target_index(yv[nj], Vreal, vw, lh) : -1);
+  }
+};
 // After the mainloop (whose final barrier makes the slots visible): the lane holding row n's target
 // (n = nbase + nj*32 + lr) writes xy[n] = its logit + the row's sparse bias on the target, summed in slot order as
 // k_row_logits sums it. The selects run only for a block where a lane of the wave has its target.
@@ -939,11 +963,14 @@ void k_fwd_tiles(Operand Wop, Operand Hop, const float* __restrict__ bias, int64
   const int lr = lane & 31, lh = lane >> 5;
   const float btile = tile_bias(bias, v0, V);
   signed char* tslot = reinterpret_cast<signed char*>(lds + TSLOT_OFF);
-  stash_targets(ta, tslot, n0 + wn * 128, N, Vreal, v0 + wm * 128, lr, lh);
+  int64_t yv[4];
+  load_targets(ta, yv, n0 + wn * 128, N, lr);
   f32x16 acc[4][4];
   // the accumulators start at the bias (masked rows at -inf): acc is the logit x_v directly
   gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
-                      reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+                                        reinterpret_cast<float*>(lds + LDS_BYTES), Vreal, nullptr, 0, 8,
+                                        TargetStash{tslot, {yv[0], yv[1], yv[2], yv[3]}, n0 + wn * 128, N, Vreal,
+                                                    v0 + wm * 128, lr, lh});
   target_pass(ta, acc, tslot, n0 + wn * 128, lr);
 
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
@@ -1563,20 +1590,21 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const int64_t vw = v0 + wm * 128;  // first vocabulary row of this wave
-  // everything the epilogue needs from memory is loaded before the mainloop: per row n of the lane (one per nj)
-  // go*wgt, lse, the target's local index (-1: none) and the target's G value
+  // everything the epilogue needs from memory is loaded before the mainloop, per row n of the lane (one per nj):
+  // wgt, lse, the target and the target's G value; the instructions that use them (go*wgt, the masks of rows past
+  // N, the target's local index) come after the mainloop, so that no wait for these loads precedes its loads
   const float btile = tile_bias(bias, v0, V);
-  const float gscale = go != nullptr ? go[0] : 1.f;
+  float gscale = 1.f;
+  if (go != nullptr) gscale = go[0];
   float cn[4], lb[4], fv[4];
   int yl[4];
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
-    const int64_t n = n0 + wn * 128 + nj * 32 + lr;
-    const bool ok = n < N;
-    cn[nj] = ok ? gscale * wgt_rows[n] : 0.f;
-    lb[nj] = ok ? lse_rows[n] * LOG2E : INFINITY;  // rows past N: exp2(-inf) = 0 whatever the logit
-    yl[nj] = ok ? ty[n] : -1;
-    fv[nj] = ok ? tval[n] : 0.f;
+    const int64_t n = n0 + wn * 128 + nj * 32 + lr, nc = n < N ? n : N - 1;
+    cn[nj] = wgt_rows[nc];
+    lb[nj] = lse_rows[nc];
+    yl[nj] = ty[nc];
+    fv[nj] = tval[nc];
   }
 
   f32x16 acc[4][4];
@@ -1587,8 +1615,12 @@ void k_bwd_grad(Operand Wop, Operand Hop, const float* __restrict__ bias, const 
   // mi*32 + 8*(r/4) + r%4 is compared with (v - vw - 4*lh), which never matches when v belongs to the other half
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
+    const bool ok = n0 + wn * 128 + nj * 32 + lr < N;
+    cn[nj] = ok ? gscale * cn[nj] : 0.f;
+    lb[nj] = ok ? lb[nj] * LOG2E : INFINITY;  // rows past N: exp2(-inf) = 0 whatever the logit
+    fv[nj] = ok ? fv[nj] : 0.f;
     const int64_t d = (int64_t)yl[nj] - vw - 4 * lh;
-    yl[nj] = (yl[nj] >= 0 && d >= 0 && d < 128) ? (int)d : -1;
+    yl[nj] = (ok && yl[nj] >= 0 && d >= 0 && d < 128) ? (int)d : -1;
   }
   bf16x8 b1, b2;
   transpose_selectors(b1, b2, lane);
@@ -1783,20 +1815,29 @@ void k_fwd_train(Operand Wop, Operand Hop, const float* __restrict__ bias, const
   const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
+  // loads whose values the prologue or the epilogue use, issued before the tile's operand loads; every
+  // dependent instruction comes after the mainloop or in its prologue hook
   const float btile = tile_bias(bias, v0, V);
   float le[4], lb[4];
 #pragma unroll
   for (int nj = 0; nj < 4; ++nj) {
     const int64_t n = n0 + wn * 128 + nj * 32 + lr;
-    le[nj] = n < N ? lse_est[n] : INFINITY;
-    lb[nj] = le[nj] * LOG2E;
+    le[nj] = lse_est[n < N ? n : N - 1];
   }
   signed char* tslot = reinterpret_cast<signed char*>(lds + TSLOT_OFF);
-  stash_targets(ta, tslot, n0 + wn * 128, N, Vreal, v0 + wm * 128, lr, lh);
+  int64_t yv[4];
+  load_targets(ta, yv, n0 + wn * 128, N, lr);
 
   f32x16 acc[4][4];
   gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
-                      reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+                                        reinterpret_cast<float*>(lds + LDS_BYTES), Vreal, nullptr, 0, 8,
+                                        TargetStash{tslot, {yv[0], yv[1], yv[2], yv[3]}, n0 + wn * 128, N, Vreal,
+                                                    v0 + wm * 128, lr, lh});
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) {
+    if (n0 + wn * 128 + nj * 32 + lr >= N) le[nj] = INFINITY;   // rows past N: E = exp2(-inf) = 0
+    lb[nj] = le[nj] * LOG2E;
+  }
   target_pass(ta, acc, tslot, n0 + wn * 128, lr);
   uint16_t* gblk = G + ((int64_t)tm * (Np / BM) + tn) * CM_TILE;
   const int64_t prow = (int64_t)(2 * tm + wm) * N;
