@@ -184,10 +184,13 @@ struct Stream {
 // (stage-local k) at P*128 in S's block; lane l of instruction i lands at LDS piece 8i + l/8, row l%8, and reads
 // the piece's row (l%8) ^ 4 sw(P) (sw(P) = (P ^ P/2) & 1), so the image holds every piece in place with its two
 // 4-row halves swapped when sw = 1 (the bank spread of make_frag_addr<2>); a k step is 512 bytes.
+// CM: the operand's layout (Operand::cm), known at compile time (gemm_tile's A has cm = AM, its B cm = 0), so the
+// prologue computes only its own offsets.
+template <int CM>
 __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int wave, int lane) {
   Stream st;
   st.kext = op.kext;
-  if (op.cm == 2) {
+  if constexpr (CM == 2) {
     st.blk = op.blk;
     st.kmul = 512;
     st.base = reinterpret_cast<uint64_t>(op.p + (m0 / BM) * op.ld);
@@ -201,7 +204,7 @@ __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int
     }
     return st;
   }
-  if (op.cm) {
+  if constexpr (CM == 1) {
     st.blk = op.blk;
     st.kmul = 16;
     st.base = reinterpret_cast<uint64_t>(op.p + (m0 / BM) * CM_TILE);
@@ -210,13 +213,16 @@ __device__ __forceinline__ Stream make_stream(const Operand& op, int64_t m0, int
     st.kmul = 2;
     st.base = reinterpret_cast<uint64_t>(op.p + m0 * op.ld);
   }
+  // rows of the tile inside the operand: at most 256 matter, so the compares stay 32-bit
+  const int64_t rem64 = op.mext - m0;
+  const int rem = rem64 < 0 ? 0 : (rem64 > BM ? BM : (int)rem64);
 #pragma unroll
   for (int j = 0; j < I::LPW; ++j) {
     const int ins = wave * I::LPW + j;
-    const int row = op.cm ? ins * 8 + (lane & 7) : ins * I::RPI + lane / I::CH;
-    const int c = op.cm ? (lane >> 3) ^ (ins & 1) : (lane % I::CH) ^ I::swz(row);
-    const bool in = m0 + row < op.mext;
-    st.voff[j] = op.cm ? ins * 4096 + c * 128 + (lane & 7) * 16 : (int)(row * op.ld * 2) + c * 16;
+    const int row = CM ? ins * 8 + (lane & 7) : ins * I::RPI + lane / I::CH;
+    const int c = CM ? (lane >> 3) ^ (ins & 1) : (lane % I::CH) ^ I::swz(row);
+    const bool in = row < rem;
+    st.voff[j] = CM ? ins * 4096 + c * 128 + (lane & 7) * 16 : (int)(row * op.ld * 2) + c * 16;
     st.kloc[j] = in ? c * 8 : OOB;
     st.vfull[j] = in ? st.voff[j] : OOB;
   }
@@ -752,8 +758,8 @@ __device__ __forceinline__ void gemm_tile(const Operand& A, const Operand& B, in
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   }
 
-  const Stream sa = make_stream(A, m0, wave, lane);
-  const Stream sb = make_stream(B, n0, wave, lane);
+  const Stream sa = make_stream<AM>(A, m0, wave, lane);
+  const Stream sb = make_stream<0>(B, n0, wave, lane);
   const FragAddr ad = make_frag_addr<AM>(wm, wn, lane);
   const int send = s0 + nk;
   if constexpr (T16) issue_tail(A, B, (int64_t)send * BK, m0, n0, lds, wave, lane);
