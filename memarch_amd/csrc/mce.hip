@@ -1947,8 +1947,9 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
 // lse, so E'[n, v] = exp(x_v - lse_n) (<= 1; a_n = wgt_n for these rows), and stores it in place in G, 16 bytes per
 // lane (the lane's own row); k_exact_fix then writes the target's exp(x_y - lse) - 1 and, with a sparse bias, the
 // candidates' exp(x_c + B_c - lse) over those entries. The work is that of F rows of the forward tile pass, so the
-// fallback costs in proportion to the flagged rows; k_exact_train is a persistent loop whose item count it reads on
-// the device.
+// fallback costs in proportion to the flagged rows. k_exact_train's grid covers every row tile the block could flag
+// (vocabulary tile fastest); a workgroup past the count, read on the device, ends at once, so the pass costs one
+// near-empty launch when nothing is flagged.
 
 // Hf[i, :] = H[list[i], :] for i < *count (K % 8 == 0), 16 bytes per thread, grid-stride.
 __global__ __launch_bounds__(256) void k_gather_rows(const uint16_t* __restrict__ H, int64_t ldh,
@@ -1968,12 +1969,13 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
                    int64_t Np, int64_t V, int64_t Vreal, int tiles_v, uint16_t* __restrict__ G) {
   __shared__ __attribute__((aligned(1024))) char lds[T16 ? TAIL_OFF + TAIL_BYTES : GRAD_LDS_BYTES];
   const int cnt = *count;
-  const int items = tiles_v * ((cnt + BN - 1) / BN);
+  const int it = (int)blockIdx.x;
+  const int tm = it % tiles_v, tn = it / tiles_v;
+  if (tn * BN >= cnt) return;   // past the flagged rows (uniform per workgroup)
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
   const Operand Hop{Hf, K, cnt, K, 0};
-  for (int it = blockIdx.x; it < items; it += gridDim.x) {
-    const int tm = it % tiles_v, tn = it / tiles_v;
+  {
     const int64_t v0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const float btile = tile_bias(bias, v0, V);
     int64_t nrow[4];
@@ -1981,12 +1983,21 @@ void k_exact_train(Operand Wop, const uint16_t* __restrict__ Hf, int64_t K, cons
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       const int64_t s = n0 + wn * 128 + nj * 32 + lr;   // slot in Hf
-      nrow[nj] = s < cnt ? list[s] : -1;
-      lb[nj] = nrow[nj] >= 0 ? lse_rows[nrow[nj]] * LOG2E : INFINITY;
+      nrow[nj] = list[s < cnt ? s : cnt - 1];
     }
+    // the rows' lse, loaded (from the rows' indices) once the operand loads are issued
+    auto load_lse = [&] {
+#pragma unroll
+      for (int nj = 0; nj < 4; ++nj) {
+        if (n0 + wn * 128 + nj * 32 + lr >= cnt) nrow[nj] = -1;
+        lb[nj] = lse_rows[nrow[nj] >= 0 ? nrow[nj] : 0];
+      }
+    };
     f32x16 acc[4][4];
     gemm_tile<KF, true, 0, 0, false, T16>(Wop, Hop, 0, stages_of<T16>(Wop.kext), v0, n0, lds, acc, btile,
-                        reinterpret_cast<float*>(lds + LDS_BYTES), Vreal);
+                                          reinterpret_cast<float*>(lds + LDS_BYTES), Vreal, nullptr, 0, 8, load_lse);
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj) lb[nj] = nrow[nj] >= 0 ? lb[nj] * LOG2E : INFINITY;
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       const bool ok = nrow[nj] >= 0;
@@ -2779,7 +2790,6 @@ int launch_sum(const float* x, int64_t count, float* part, float* out, hipStream
 // The exact pass over the rows k_fwd_merge listed (count and list on the device): k_exact_tiles, k_exact_rows.
 // part_m / part_s (the merged partials, [>= tiles_v][N]) are reused as its scratch.
 constexpr int REPAIR_BLOCKS = 1024;
-constexpr int EXACT_BLOCKS = 256;  // workgroups of the persistent k_exact_train (one per CU)
 int launch_exact(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t ldw, const float* bias,
                  const int64_t* cand, const float* cval, int kc, int64_t N, int64_t K, int64_t V, int64_t V_real,
                  int tv, const int* count, const int* list, float* part_m, float* part_s, const float* xy,
@@ -3243,7 +3253,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     hipLaunchKernelGGL(k_gather_rows, dim3(REPAIR_BLOCKS), dim3(256), 0, st, H + row0 * ldh, ldh, w.flag_list,
                        w.counts + b, K, w.Ht);
     if ((rc = launch_status())) return rc;
-    MCE_LAUNCH_KM(k_exact_train, K, dim3(EXACT_BLOCKS), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias, w.counts + b,
+    MCE_LAUNCH_KM(k_exact_train, K, dim3((unsigned)(tv * tnb)), dim3(NTHREADS), 0, st, Wop, w.Ht, K, bias, w.counts + b,
                   w.flag_list, lse_rows + row0, rp, V, V_real, tv, w.G);
     if ((rc = launch_status())) return rc;
     hipLaunchKernelGGL(k_exact_fix, dim3((unsigned)(rp / 256)), dim3(256), 0, st, w.counts + b, w.flag_list, y + row0,
