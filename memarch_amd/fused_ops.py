@@ -12,8 +12,9 @@ the forward, row block by row block, never storing the logits: each block's logi
 block x V buffer of exp(x - e_n) with one per-row factor applied in the contractions, and every block but the last
 adds its dH rows, dW and dBias to partial sums (for go = 1); the backward runs the last block's contractions with
 go, adds the partial sums in their epilogues and scales the earlier dH rows (and forms the candidates' gradient
-from the per-row state). The rows per block come from the library (a 2 GiB bound on the block's buffer, or
-BLOCK_ROWS, environment MEMARCH_AMD_BLOCK_ROWS); `chunk` is accepted and ignored. Otherwise -- no gradient needed,
+from the per-row state). The rows per block come from the library (a 4 GiB bound on the block's buffer: one block
+of 32768 rows at V = 50304), or from BLOCK_ROWS (environment MEMARCH_AMD_BLOCK_ROWS; smaller blocks take less memory
+and more time); `chunk` is accepted and ignored. Otherwise -- no gradient needed,
 or RECOMPUTE set (environment MEMARCH_AMD_RECOMPUTE=1) -- the forward computes only the per-row statistics and the
 backward recomputes the logits tile by tile to form the gradient. Logits are fp32 in both paths (never rounded to
 bf16), and rows with P below the 1e-30 clamp get zero gradient, as the reference's eager formula does
