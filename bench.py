@@ -5,8 +5,9 @@ over one batch of the configuration's synthetic inputs (default: config 2, N = 3
 accumulation), with every input resident in HBM before the timed region. Prints one JSON line:
   value         tokens/s of the whole step: N*K / (wall time of K steps between two synchronisations)
   roofline      the dominant kernel of the step: its algorithmic FLOPs per launch (one N x V x d contraction,
-                2*N*V*d) over its average duration in the timed steps, from HIP events recorded around each C-ABI
-                stage on the stream it is launched on (torch's current stream);
+                2*N*V*d) over its average duration in the timed steps, from the HIP events the library records
+                around each launch of its contraction kernels on the stream it is launched on (mce_prof_start /
+                mce_prof_stop);
                 `traffic` is its HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary in
                 profiles/ (null when that summary does not cover this kernel and configuration)
   op_roofline   the whole step against the bf16 MFMA peak on the op's 6*N*V*d algorithmic FLOPs (the
@@ -47,6 +48,7 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 # then mce_bwd_blocked (per row block: the logits recomputed into G, its dH rows, dW and dBias accumulated) or, for
 # chunk_ce, mce_lse_fwd and mce_bwd_lse_blocked; --stage-reps times the separate steps mce_bwd_logits_grad,
 # mce_bwd_dhidden, mce_bwd_dweight.
+STAGE_STEPS = 3   # steps after the timed ones that carry the per-stage stream events (`stages_ms`)
 STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_sparse": "fwd",
                  "mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
                  "mce_bwd_dweight": "dweight", "mce_fwd_sparse": "fwd", "mce_bwd_logits_grad_sparse": "logits_grad",
@@ -493,9 +495,29 @@ def bench_config0(args):
             return fused_ops.linear_ce_mix_biased(inp.h, inp.w, inp.bias, inp.y, inp.gate, inp.hit,
                                                   v_real=cfg.v_real)
 
+    lib = _lib.load()
+    lib.mce_prof_start()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    _lib.check(lib.mce_prof_stop(None, None, 0), "mce_prof_stop")
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    # the timed steps carry only the library's kernel-class events (class 1: the logits tiles k_fwd_tiles)
+    lib.mce_prof_start()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    kern_ms = (ctypes.c_double * 2)()
+    kern_n = (ctypes.c_int64 * 2)()
+    _lib.check(lib.mce_prof_stop(kern_ms, kern_n, 2), "mce_prof_stop")
+    peak = torch.cuda.max_memory_allocated(dev)
+    if kern_n[1] != args.steps:
+        raise RuntimeError(f"expected one k_fwd_tiles launch per step, got {kern_n[1]} in {args.steps} steps")
+    tiles_ms = kern_ms[1] / kern_n[1]
+    # the whole forward call (all of its kernels), from stream events around it in STAGE_STEPS more steps
     marks = []
 
     def hook(name, phase):
@@ -504,17 +526,13 @@ def bench_config0(args):
             ev.record()
             marks.append(ev)
 
-    torch.cuda.reset_peak_memory_stats(dev)
-    base = torch.cuda.memory_allocated(dev)
+    n_stage = min(STAGE_STEPS, args.steps)
     _lib.set_call_hook(hook)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        loss = step()
+    for _ in range(n_stage):
+        step()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
     _lib.set_call_hook(None)
-    peak = torch.cuda.max_memory_allocated(dev)
-    fwd_ms = sum(a.elapsed_time(b) for a, b in zip(marks[0::2], marks[1::2])) / args.steps
+    fwd_ms = sum(a.elapsed_time(b) for a, b in zip(marks[0::2], marks[1::2])) / max(n_stage, 1)
     kflops = 2.0 * n * v * d
     res = {
         "metric": f"tokens/s fused out+CE+pointer fwd (config 0: N={n}, d={d}, V={v}); % bf16 MFMA peak",
@@ -523,10 +541,11 @@ def bench_config0(args):
         "dtype": "bf16", "data": "synthetic (seeded config 0 distributions, random-init weights)",
         "config": {"workload": "config 0: fused linear+CE+pointer forward loss only", "N": n, "d": d, "V": v,
                    "V_real": cfg.v_real, "operands": "bf16 (cast from fp32 inputs)", "accumulate": "fp32"},
-        "roofline": {"bound": "mfma", "kernel": "k_fwd_tiles<true>", "stage": "fwd",
-                     "achieved": round(kflops / (fwd_ms * 1e-3) / 1e12, 2), "peak": PEAK_BF16 / 1e12,
-                     "unit": "TFLOP/s", "frac": round(kflops / (fwd_ms * 1e-3) / PEAK_BF16, 4),
-                     "flops_per_launch": kflops, "traffic": None},
+        "roofline": {"bound": "mfma", "kernel": "k_fwd_tiles<true, false>",
+                     "achieved": round(kflops / (tiles_ms * 1e-3) / 1e12, 2), "peak": PEAK_BF16 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(kflops / (tiles_ms * 1e-3) / PEAK_BF16, 4),
+                     "flops_per_launch": kflops, "launches_per_step": 1, "avg_launch_ms": round(tiles_ms, 4),
+                     "traffic": None},
         "stages_ms": {"fwd": round(fwd_ms, 4)},
         "peak_mem_gb": round(peak / 1e9, 4), "step_mem_gb": round((peak - base) / 1e9, 4),
         "path": "forward (statistics only)",
@@ -734,7 +753,26 @@ def main():
     torch.cuda.synchronize()
     _lib.check(lib.mce_prof_stop(None, None, 0), "mce_prof_stop")
     flagged.zero_()
-    # HIP events around every C-ABI stage of the timed steps, on the stream the stages are launched on
+    # the timed steps carry the library's kernel-class events only; the per-stage and per-step stream events (each
+    # a marker packet between kernels, some 5 us of GPU time) are recorded in a few further steps after them
+    print("[bench] timed steps", file=sys.stderr, flush=True)
+    h.grad = w.grad = b.grad = gate.grad = cval.grad = None
+    torch.cuda.synchronize()
+    mem_base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    lib.mce_prof_start()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    fused_ops.FLAGGED = None
+    kern_ms = (ctypes.c_double * len(PROF_KERNELS))()
+    kern_n = (ctypes.c_int64 * len(PROF_KERNELS))()
+    _lib.check(lib.mce_prof_stop(kern_ms, kern_n, len(PROF_KERNELS)), "mce_prof_stop")
+    mem_peak = torch.cuda.max_memory_allocated(dev)
+    # HIP events around every C-ABI stage and every step, on the stream the stages are launched on, over
+    # STAGE_STEPS more steps (not part of `value`)
     marks = []
 
     def hook(name, phase):
@@ -743,35 +781,23 @@ def main():
             ev.record()
             marks.append((name, phase, ev))
 
-    print("[bench] timed steps", file=sys.stderr, flush=True)
-    h.grad = w.grad = b.grad = gate.grad = cval.grad = None
-    torch.cuda.synchronize()
-    mem_base = torch.cuda.memory_allocated(dev)
-    torch.cuda.reset_peak_memory_stats(dev)
+    n_stage = min(STAGE_STEPS, args.steps)
     _lib.set_call_hook(hook)
-    lib.mce_prof_start()
-    step_ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    t0 = time.perf_counter()
+    step_ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_stage + 1)]
     step_ev[0].record()
-    for i in range(args.steps):
+    for i in range(n_stage):
         step()
         step_ev[i + 1].record()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
-    print("[bench] per-step ms (stream events): " +
-          " ".join(f"{step_ev[i].elapsed_time(step_ev[i + 1]):.2f}" for i in range(args.steps)), file=sys.stderr,
-          flush=True)
     _lib.set_call_hook(None)
-    fused_ops.FLAGGED = None
-    kern_ms = (ctypes.c_double * len(PROF_KERNELS))()
-    kern_n = (ctypes.c_int64 * len(PROF_KERNELS))()
-    _lib.check(lib.mce_prof_stop(kern_ms, kern_n, len(PROF_KERNELS)), "mce_prof_stop")
-    mem_peak = torch.cuda.max_memory_allocated(dev)
+    print("[bench] per-step ms (stream events, steps after the timed ones): " +
+          " ".join(f"{step_ev[i].elapsed_time(step_ev[i + 1]):.2f}" for i in range(n_stage)), file=sys.stderr,
+          flush=True)
     live = {}
     for (name, ph0, e0), (name1, ph1, e1) in zip(marks[0::2], marks[1::2]):
         assert name == name1 and ph0 == "begin" and ph1 == "end"
         live.setdefault(STAGE_OF_CALL[name], []).append(e0.elapsed_time(e1))
-    stages = {k: sum(x) / args.steps for k, x in live.items()}
+    stages = {k: sum(x) / max(n_stage, 1) for k, x in live.items()}
     # the contraction kernels, timed by the library's HIP events around each launch on the launch stream: every
     # class present runs one N x V x d contraction per step, over one or several launches (row blocks)
     names = kernel_names(d, folded, args.op == "fused_ce" and args.path == "one-pass")
