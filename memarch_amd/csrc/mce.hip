@@ -1089,25 +1089,40 @@ __device__ __forceinline__ void row_dot4(const uint16_t* hr, const uint16_t* con
 // One wave per row; lane k holds candidate k for the row's summary (kc <= 64 = the wave), and the candidates' dot
 // products run four at a time. The tile kernels compute the same sums in another order; the two agree to fp32
 // rounding.
+// With lse_est (the one-pass training forward; the grid then covers Np rows): also e_n, the shift of the training
+// tiles, = the largest true logit the row already has -- the target's (with its sparse bias) and each distinct
+// valid candidate's x_c + B_c; id 0's logit when none of them is finite -- which is at most lse_n (+inf for rows
+// N .. Np-1, whose E is then exactly 0); flag[n] = 0 for every row below Np and counts[0 .. ncount-1] = 0.
 __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__ H, int64_t ldh,
                                                     const uint16_t* __restrict__ W, int64_t ldw,
                                                     const float* __restrict__ bias, const int64_t* __restrict__ y,
                                                     const int64_t* __restrict__ cand, const float* __restrict__ cval,
                                                     int kc, int64_t N, int64_t K, int64_t Vreal,
                                                     float* __restrict__ xy, float* __restrict__ xc,
-                                                    float* __restrict__ cb, int* __restrict__ zero = nullptr) {
+                                                    float* __restrict__ cb, int* __restrict__ zero = nullptr,
+                                                    float* __restrict__ lse_est = nullptr, int* __restrict__ flag = nullptr,
+                                                    int* __restrict__ counts = nullptr, int ncount = 0,
+                                                    int64_t Np = 0) {
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *zero = 0;  // k_fwd_merge's exact-row counter
-  if (n >= N) return;
+  if (lse_est != nullptr && blockIdx.x == 0)
+    for (int i = threadIdx.x; i < ncount; i += 256) counts[i] = 0;
+  if (n >= N) {
+    if (lse_est != nullptr && n < Np && lane == 0) {
+      lse_est[n] = INFINITY;
+      flag[n] = 0;
+    }
+    return;
+  }
   const uint16_t* hr = H + n * ldh;
   const int64_t yn = y[n];
   float by = 0.f;  // the sparse bias on the target (slot order, as sparse_bias sums it)
+  float btot = 0.f;
+  int first = -1;
   if (kc > 0) {
     const int64_t ck = lane < kc ? cand[n * kc + lane] : -1;
     const float vk = lane < kc ? cval[n * kc + lane] : 0.f;
-    float btot;
-    int first;
     cand_summary(ck, vk, kc, lane, btot, first);
     for (int j = 0; j < kc; ++j)
       if (shfl_i64(ck, j) == yn) by += __shfl(vk, j);
@@ -1116,6 +1131,7 @@ __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__
   float x = -INFINITY;
   if (yn >= 0 && yn < Vreal) x = row_dot(hr, W + yn * ldw, K, lane) + (bias != nullptr ? bias[yn] : 0.f) + by;
   if (lane == 0) xy[n] = x;
+  float e = x;   // e_n: the largest true logit seen so far
   for (int k0 = 0; k0 < kc; k0 += 4) {
     const uint16_t* wr[4];
     int64_t c[4];
@@ -1126,12 +1142,23 @@ __global__ __launch_bounds__(256) void k_row_logits(const uint16_t* __restrict__
     }
     float sq[4];
     row_dot4(hr, wr, K, lane, sq);
-    if (lane == 0) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (k0 + q < kc)
-          xc[n * kc + k0 + q] =
-              (c[q] >= 0 && c[q] < Vreal) ? sq[q] + (bias != nullptr ? bias[c[q]] : 0.f) : -INFINITY;
+    for (int q = 0; q < 4; ++q) {
+      const int slot = (k0 + q) & 63;
+      const float tb = __shfl(btot, slot);          // the total sparse bias of the slot's id
+      const int fs = __shfl(first, slot);           // the first slot of that id
+      const bool valid = k0 + q < kc && c[q] >= 0 && c[q] < Vreal;
+      const float xq = valid ? sq[q] + (bias != nullptr ? bias[c[q]] : 0.f) : -INFINITY;
+      if (lane == 0 && k0 + q < kc) xc[n * kc + k0 + q] = xq;
+      if (valid && fs == slot) e = fmaxf(e, xq + tb);
+    }
+  }
+  if (lse_est != nullptr) {
+    // no finite known logit (an ignored or masked target and no candidate): id 0's logit, another term of the sum
+    if (!(e > -INFINITY)) e = row_dot(hr, W, K, lane) + (bias != nullptr ? bias[0] : 0.f);
+    if (lane == 0) {
+      lse_est[n] = e;
+      flag[n] = 0;
     }
   }
 }
@@ -1736,8 +1763,8 @@ __global__ __launch_bounds__(256) void k_dgate(const float* __restrict__ dgr, co
 // by a backward pass over the logits:
 //   G[n, v] = go * wgt_n * (exp(x_v - lse_n) - [v = y_n]) = go * a_n * E'[n, v],
 //   E[n, v] = exp(x_v - e_n),  a_n = wgt_n * exp(e_n - lse_n),  E'[n, y_n] = (exp(x_y - lse_n) - 1) exp(lse_n - e_n)
-// with e_n a lower bound of lse_n that is known before the tiles run: the logsumexp of the first vocabulary tile
-// and of the target logit (k_lse_est). E' (= E except at the target) goes into the G buffer in the
+// with e_n a lower bound of lse_n that is known before the tiles run: the largest true logit among the target and
+// the row's sparse candidates (k_row_logits). E' (= E except at the target) goes into the G buffer in the
 // tile-blocked layout; the per-row factor a_n, which needs the final lse, is applied by the backward
 // (dH = go a . (E' W) in the GEMM epilogue, dW = E'^T (go a . H) through a row-scaled H^T copy, dBias = E'^T (go a)).
 // Because e_n <= lse_n, E underflows only where the softmax is below e^-87 anyway. It could overflow only where a
@@ -1757,53 +1784,6 @@ __device__ __forceinline__ int64_t cm_index(int64_t m, int64_t k, int64_t Mp) {
          (kp & 7);
 }
 __device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xFFFFu); }
-
-// e_n per row from the two half-tile partials of vocabulary tile 0 (part_m / part_s rows 0 and 1) and the target
-// logit when the target lies outside tile 0; also clears the flags and the ncount flagged-row counters.
-__global__ __launch_bounds__(256) void k_lse_est(const float* __restrict__ part_m, const float* __restrict__ part_s,
-                                                 const float* __restrict__ xy, const int64_t* __restrict__ y,
-                                                 const int64_t* __restrict__ cand, const float* __restrict__ cb,
-                                                 const float* __restrict__ xc, int kc, int64_t N,
-                                                 int64_t Np, float* __restrict__ lse_est, int* __restrict__ flag,
-                                                 int* __restrict__ counts, int ncount) {
-  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (n < ncount) counts[n] = 0;
-  if (n >= Np) return;
-  flag[n] = 0;
-  if (n >= N) {
-    lse_est[n] = INFINITY;
-    return;
-  }
-  const float m0 = part_m[n], m1 = part_m[N + n];
-  const float m = fmaxf(m0, m1);
-  float l = -INFINITY;
-  if (m != -INFINITY) {
-    float s = 0.f;
-    if (m0 != -INFINITY) s += part_s[n] * expf(m0 - m);
-    if (m1 != -INFINITY) s += part_s[N + n] * expf(m1 - m);
-    l = m + logf(s);
-  }
-  const float x = xy[n];
-  if (y[n] >= BM && x != -INFINITY) {
-    const float mm = fmaxf(l, x);
-    l = mm + logf(expf(l - mm) + expf(x - mm));
-  }
-  if (kc > 0) {
-    // sparse bias: the tile saw the logits without it, so its logsumexp bounds lse_n from below only while no
-    // candidate of the first tile has a negative total bias; otherwise the largest true logit among the target
-    // and the candidates is the bound
-    bool neg = false;
-    float mx = x;
-    for (int k = 0; k < kc; ++k) {
-      const float B = cb[n * kc + k];
-      if (cb_skip(B)) continue;  // not the first slot of a valid id
-      if (cand[n * kc + k] < BM && B < 0.f) neg = true;
-      mx = fmaxf(mx, xc[n * kc + k] + B);
-    }
-    if (neg) l = mx;
-  }
-  lse_est[n] = l;
-}
 
 // Forward tile of the training path: the logits tile as in k_fwd_tiles, then E = exp(x - e_n) for its 256 x 256
 // elements, rounded to bf16 and stored into G exactly as k_bwd_grad stores it (store_g_block). The
@@ -1918,8 +1898,9 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   }
   const float w = wgt_rows[n];
   const float e = lse_est[n], l = lse_rows[n];
-  // every E' value of the row is at most exp(lse - e_n): a row whose lse exceeds e_n by more than 60 (possible
-  // only through a large sparse bias, which the tiles do not see) also takes the exact pass
+  // every E' value of the row is at most exp(lse - e_n): a row whose lse exceeds e_n by more than 60 also takes
+  // the exact pass (the half-tile bound flags such rows for the logits the tiles see; this catches what they do
+  // not see, the sparse bias)
   if (flag[n] || !(l - e <= 60.f)) {
     arow[n] = w;
     flag_list[atomicAdd(flag_count, 1)] = (int)n;
@@ -1940,8 +1921,8 @@ __global__ __launch_bounds__(256) void k_train_rows(const int64_t* __restrict__ 
   }
 }
 
-// The exact E' rows of the flagged rows (rows whose logits exceed e_n by about 44 or more, which the bound from
-// the first vocabulary tile and the target makes rare, or whose lse exceeds e_n by more than 60). Three kernels:
+// The exact E' rows of the flagged rows (rows whose logits exceed e_n by about 44 or more, which a shift by the
+// row's largest known true logit makes rare, or whose lse exceeds e_n by more than 60). Three kernels:
 // k_gather_rows copies the flagged rows of H into a dense operand Hf [F][K] (F = the flagged-row count); k_exact_train
 // runs the logits tile mainloop over (vocabulary tile, 256 gathered rows) items with each row shifted by its exact
 // lse, so E'[n, v] = exp(x_v - lse_n) (<= 1; a_n = wgt_n for these rows), and stores it in place in G, 16 bytes per
@@ -3033,13 +3014,12 @@ int bwd_blocked_impl(const uint16_t* H, int64_t ldh, const uint16_t* W, int64_t 
 // Training-path workspace. The rows are processed in blocks of `nb` rows (a multiple of 256; the last block may be
 // shorter): per block E' in G (tile-blocked, the block's rows padded to a multiple of 256), the row-scaled
 // H^T copy and go*a in bf16 (natural row order), the half-tile partials and the flagged-row list, all reused block after
-// block (the last block's stay for the backward); once per call W^T (for dH), the first vocabulary tile's partials,
-// the target / candidate logits, e_n, a_n, the flags and the per-block flagged-row counts over all rows, the loss
+// block (the last block's stay for the backward); once per call W^T (for dH), the target / candidate logits, e_n, a_n, the flags and the per-block flagged-row counts over all rows, the loss
 // partials, the dW blocks' dBias partials, the K-split tail tiles and the dBias GEMV partials.
 struct TrainWs {
   int64_t np, vp, nb, nblk;
   uint16_t *G, *Ht, *uperm, *Wt;
-  float *part_m, *part_s, *p0m, *p0s, *xy, *xc, *cb, *lse_est, *arow, *upart, *part, *xpart, *dbias_part, *sum_part;
+  float *part_m, *part_s, *xy, *xc, *cb, *lse_est, *arow, *upart, *part, *xpart, *dbias_part, *sum_part;
   int *flag, *flag_list, *counts, *xlist;
   size_t bytes;
 };
@@ -3081,8 +3061,6 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   w.part_s = reinterpret_cast<float*>(take(sizeof(float) * T * nb));
   w.flag_list = reinterpret_cast<int*>(take(sizeof(int) * nb));
   w.Wt = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * w.vp * K));
-  w.p0m = reinterpret_cast<float*>(take(sizeof(float) * 2 * np));
-  w.p0s = reinterpret_cast<float*>(take(sizeof(float) * 2 * np));
   w.xy = reinterpret_cast<float*>(take(sizeof(float) * np));
   w.xc = reinterpret_cast<float*>(take(sizeof(float) * np * MAX_KC));
   w.cb = reinterpret_cast<float*>(take(sizeof(float) * np * MAX_KC));
@@ -3195,7 +3173,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
     return MCE_EINVAL;
   if (more && (want & MCE_GRAD_H) && !dh_aligned(dH_part, lddh, dh_bf16)) return MCE_EALIGN;
   if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
-  const int tv = (int)(w.vp / BM), tn = (int)cdiv(N, BN);
+  const int tv = (int)(w.vp / BM);
   const Operand Wop{W, ldw, V, K, 0};
   // W^T for the dH contractions: element (k, v) at Wt[(v/256)*K*256 + k*256 + kperm(v%256)], zero for v >= V; with
   // W32 the bf16 W itself comes from the same pass
@@ -3209,19 +3187,11 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
                        ldw, V, K, w.Wt, nullptr, nullptr, nullptr);
     if ((rc = launch_status())) return rc;
   }
-  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand,
-                     cval, kc, N, K, V_real, w.xy, w.xc, w.cb);
-  if ((rc = launch_status())) return rc;
-  {
-    // e_n: the first vocabulary tile (one tile row of k_fwd_tiles over all rows) and the target logit
-    const Operand Hop{H, ldh, N, K, 0};
-    const TargetArgs none{nullptr, nullptr, nullptr, 0, nullptr};  // k_fwd_train writes the target logits
-    MCE_LAUNCH_KM(k_fwd_tiles, K, dim3(tn), dim3(NTHREADS), 0, st, Wop, Hop, bias, N, V, V_real, 1, tn, w.p0m, w.p0s,
-                  none);
-    if ((rc = launch_status())) return rc;
-  }
-  hipLaunchKernelGGL(k_lse_est, dim3((unsigned)cdiv(w.np, 256)), dim3(256), 0, st, w.p0m, w.p0s, w.xy, y, cand, w.cb,
-                     w.xc, kc, N, w.np, w.lse_est, w.flag, w.counts, (int)(2 * w.np / BLK));
+  // the target and candidate logits, and e_n (the largest of the row's true logits among them), the cleared flags
+  // and flagged-row counters
+  hipLaunchKernelGGL(k_row_logits, dim3((unsigned)cdiv(w.np, 4)), dim3(256), 0, st, H, ldh, W, ldw, bias, y, cand,
+                     cval, kc, N, K, V_real, w.xy, w.xc, w.cb, nullptr, w.lse_est, w.flag, w.counts,
+                     (int)(2 * w.np / BLK), w.np);
   if ((rc = launch_status())) return rc;
   const float s_max = g_train_s_max.load(std::memory_order_relaxed);
   for (int64_t b = 0; b < w.nblk; ++b) {

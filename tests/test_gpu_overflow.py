@@ -32,8 +32,8 @@ def _need_gpu():
 
 def _overflow_case(mode, n=600, k=128, v=1500, seed=91):
     """Rows SPIKED get h[:, 0] = 150 against vocabulary row 1000 (w = 1: logit ~150) and target 1001 (w = 0.1: logit
-    ~15); every other row has a zero first coordinate. e_n ~ 15 (the target logit dominates the first tile's
-    logsumexp), so the spiked rows' largest logit sits ~135 above e_n: exp overflows. mode: "plain" (no gate),
+    ~15); every other row has a zero first coordinate. e_n ~ 15 (the target logit, the row's only known
+    logit), so the spiked rows' largest logit sits ~135 above e_n: exp overflows. mode: "plain" (no gate),
     "clamped" (g = 0 on those rows), "pointer" (hit = 1, g = 0.5 on those rows)."""
     case = random_case(n, k, v, None, True, seed=seed)
     case["h"][:, 0] = 0.0

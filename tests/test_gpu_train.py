@@ -74,6 +74,21 @@ def test_capi_parity_blocks(shape):
     assert_parity(got, dict(fwd, loss_sum=fwd["loss_sum"] * go), bwd, f"train {shape} blocks")
 
 
+@pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
+def test_ignored_targets_stay_off_the_fallback(block_rows):
+    """Rows with y = -100 have no target logit; their e_n comes from id 0's logit instead, so they take no exact
+    pass (flagged == 0), and the results match the oracle's (which drops those rows' one-hot term)."""
+    print(f"ignored targets block_rows={block_rows}", flush=True)
+    case = random_case(600, 256, 1300, 1250, True, seed=31)
+    case["y"][::7] = -100
+    case["hit"][::7] = 0.0
+    go = 1.0 / 600
+    got = capi_train(case, go=go, block_rows=block_rows)
+    fwd, bwd = oracle_of(case, go=go)
+    assert got["flagged"] == 0
+    assert_parity(got, dict(fwd, loss_sum=fwd["loss_sum"] * go), bwd, "ignored targets")
+
+
 @pytest.mark.parametrize("shape", SHAPES[1:4], ids=lambda s: "N{}_K{}_V{}".format(*s[:3]))
 @pytest.mark.parametrize("block_rows", [0, 256], ids=["one_block", "blocks256"])
 def test_forced_fallback_every_row(shape, block_rows):
@@ -101,8 +116,8 @@ def test_forced_fallback_with_clamped_rows():
 def _peaked_case(n=600, k=128, v=1500, rows=(3, 4, 100, 255, 256, 599), seed=17):
     """Rows `rows` carry h[:, 0] = 150 against vocabulary rows 1000 and 1001, the only ones with a nonzero first
     coordinate (0.5 and 2/15): their logits ~75 and ~20. The target is 1001 and the gate 0, so py ~ e^-55 stays
-    above the 1e-30 clamp and the gradient is the full softmax minus onehot; e_n (the first tile's logsumexp and
-    the target logit, ~20) is ~55 below the largest logit, beyond the default fallback bound of 2^64 ~ e^44."""
+    above the 1e-30 clamp and the gradient is the full softmax minus onehot; e_n (the target logit, ~20) is ~55
+    below the largest logit, beyond the default fallback bound of 2^64 ~ e^44."""
     case = random_case(n, k, v, None, True, seed=seed)
     case["w"][:, 0] = 0.0
     case["w"][1000, 0] = 0.5

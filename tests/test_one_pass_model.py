@@ -1,7 +1,7 @@
 """CPU model of the one-pass training path's algebra (mce_fwd_train / mce_bwd_train), checked against the oracle.
 
 The kernels form G = go * wgt * (softmax - onehot) without a second pass over the logits as
-    e_n  = logsumexp(x_n[0:256] ++ [x_{n,y_n} when y_n >= 256])     (k_lse_est; e_n <= lse_n)
+    e_n  = x_{n,y_n}, the target logit (x_{n,0} for an invalid target) (k_row_logits; e_n <= lse_n)
     E    = exp(x - e_n)                                              (k_fwd_train, half-tile sums S)
     row flagged  <=>  some half tile has S > s_max (or e_n not finite) (its partial is then (max, sum exp(x - max)))
     lse  = the merge of the half-tile partials
@@ -33,9 +33,7 @@ def one_pass(h, w, y, gate, hit, bias, v_real, go, s_max=S_MAX, round_bf16=False
     vr = V if v_real is None else v_real
     ok = (y >= 0) & (y < vr)
     xy = np.where(ok, x[np.arange(N), np.clip(y, 0, V - 1)], -np.inf)
-    e = _lse_rows(x[:, :256])
-    late = ok & (y >= 256)
-    e = np.where(late, np.logaddexp(e, xy), e)
+    e = np.where(np.isfinite(xy), xy, x[:, 0])
     with np.errstate(over="ignore", invalid="ignore"):
         E = np.exp(x - e[:, None])
         halves = [E[:, i:i + 128].sum(axis=1) for i in range(0, V, 128)]
@@ -75,7 +73,7 @@ def one_pass(h, w, y, gate, hit, bias, v_real, go, s_max=S_MAX, round_bf16=False
                     dgate=go * dgr, flagged=int(flag.sum()))
 
 
-def _case(seed, N=300, K=48, V=700, v_real=None, gate_mode="mixed", peaked=(), bias=True):
+def _case(seed, N=300, K=48, V=700, v_real=None, gate_mode="mixed", peaked=(), bias=True, ignored=()):
     rng = np.random.default_rng(seed)
     h = rng.standard_normal((N, K))
     w = rng.standard_normal((V, K)) * 0.2
@@ -97,6 +95,8 @@ def _case(seed, N=300, K=48, V=700, v_real=None, gate_mode="mixed", peaked=(), b
         y[r] = 601
         if gate is not None:
             gate[r] = 0.0
+    if ignored:
+        y[np.array(ignored)] = -100   # ignored rows: no target logit, e_n from id 0
     return h, w, y, gate, hit, b, v_real
 
 
@@ -112,10 +112,11 @@ def _check(got, ref, tol):
 CASES = [
     dict(seed=1),
     dict(seed=2, v_real=650),
-    dict(seed=3, V=200),                    # the whole vocabulary inside the first tile
+    dict(seed=3, V=200),                    # the whole vocabulary inside one tile
     dict(seed=4, gate_mode="none"),         # plain cross-entropy
     dict(seed=5, bias=False),
     dict(seed=6, peaked=(3, 4, 100, 255)),  # rows that take the exact fallback without forcing
+    dict(seed=10, ignored=(0, 17, 299)),    # ignored targets (y = -100) stay off the fallback
 ]
 
 
