@@ -231,11 +231,11 @@ MCE_API int mce_bwd_lse_blocked(const uint16_t* H, int64_t ldh, const uint16_t* 
  * One-pass training path (mixture or plain cross-entropy, optionally a sparse bias). The reference computes its
  * gradients during the forward, 4096 rows at a time (fused_ops.py:148-155); so does this path, in row blocks,
  * without materialising logits and without a second pass over them. For each block the forward's tile kernel
- * writes E'[n, v] = G[n, v] / (go a_n), a_n = wgt_n exp(e_n - lse_n), where e_n <= lse_n is the logsumexp of the
- * first vocabulary tile and the target logit (rows whose logits exceed e_n by too much for the exponent range are
- * detected on the device and written exactly by a fallback pass, with a_n = wgt_n), then the block's gradient
- * contractions dH = a . (E' W), dW += E'^T (a . H), dBias += E'^T a run with go = 1 into caller-owned partial
- * sums. The last block's contractions wait for the backward (mce_bwd_train), where go is known: its epilogues
+ * writes E'[n, v] = G[n, v] / (go a_n), a_n = wgt_n exp(e_n - lse_n), where e_n <= lse_n is the row's largest true
+ * logit known before the tiles run: the target's, a sparse candidate's, or id 0's (rows whose logits exceed e_n by
+ * too much for the exponent range are detected on the device and written exactly by a fallback pass, with
+ * a_n = wgt_n), then the block's gradient contractions dH = a . (E' W), dW += E'^T (a . H), dBias += E'^T a run
+ * with go = 1 into caller-owned partial sums. The last block's contractions wait for the backward (mce_bwd_train), where go is known: its epilogues
  * write go * (partial + last block) into the outputs, so the partial sums are never rescaled in a separate pass
  * (only the earlier blocks' dH rows are, once).
  *
