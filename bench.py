@@ -53,7 +53,7 @@ STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_
                  "mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
                  "mce_bwd_dweight": "dweight", "mce_fwd_sparse": "fwd", "mce_bwd_logits_grad_sparse": "logits_grad",
                  "mce_lse_fwd": "fwd", "mce_bwd_lse_grad": "logits_grad", "mce_bwd_blocked": "bwd",
-                 "mce_bwd_lse_blocked": "bwd"}
+                 "mce_bwd_lse_blocked": "bwd", "mce_bwd_lse_train": "bwd"}
 # kernel classes of mce_prof_stop (include/mce.h) -> kernel name (rocprofv3's); each class runs one N x V x d
 # contraction per step. {t16}: the logits tiles' K tail (true for K = d + 16, the folded layout); {nr}: the row
 # groups per dW tile (dBias on the one-pass path, the extra columns with {xm}); {xm}: the output columns past the
@@ -800,7 +800,7 @@ def main():
     stages = {k: sum(x) / max(n_stage, 1) for k, x in live.items()}
     # the contraction kernels, timed by the library's HIP events around each launch on the launch stream: every
     # class present runs one N x V x d contraction per step, over one or several launches (row blocks)
-    names = kernel_names(d, folded, args.op == "fused_ce" and args.path == "one-pass")
+    names = kernel_names(d, folded, args.op in ("fused_ce", "chunk_ce") and args.path == "one-pass")
     kernels = {names[c]: (kern_ms[c], kern_n[c] // args.steps) for c in range(len(PROF_KERNELS)) if kern_n[c] > 0}
     tok_s = n / dt
     flops = 6.0 * n * v * d

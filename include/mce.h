@@ -314,6 +314,29 @@ MCE_API int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const flo
                                 int64_t V, int64_t V_real, int64_t block_rows, float* dCval, void* ws, size_t ws_bytes,
                                 void* stream);
 
+/*
+ * chunk_ce on the one-pass path. After mce_fwd_train with gate = hit = NULL (plain cross-entropy) over a single row
+ * block (mce_train_block_rows(N, K, V, block_rows) >= N), the workspace holds E'[n, v] = exp(x_v - s_n) for all rows
+ * (s_n = e_n, or lse_n for rows of the exact pass), as the reference's CE_SAVE mode keeps the forward's bf16 logits
+ * for its backward (full2.py:773-774, 799-800) instead of recomputing them.
+ * mce_train_target_logits copies the target logits x_y [N] of that forward (fp32, from the logits tiles' own
+ * accumulators; -inf for targets outside [0, V_real)) into `out`: the `ly` output of `_ChunkCE.forward`
+ * (full2.py:780-786), whose `lse` is the forward's lse_rows.
+ * mce_bwd_lse_train is `_ChunkCE.backward` (full2.py:792-830) on that workspace: G = g_lse softmax + g_ly onehot(y)
+ * as a_n E' (a_n = g_lse exp(s_n - lse_n), the target entry of E' rewritten to G[n, y] / a_n; a row whose one-hot
+ * term cannot be folded so -- a_n = 0, or a quotient beyond bf16 -- has its E' rewritten as onehot(y) with
+ * a_n = g_ly), then dH = a . (E' W), dW = E'^T (a . H), dBias = E'^T a. g_lse / g_ly may be NULL (zeros); dH (bf16
+ * or fp32, stride lddh, 16-byte aligned), dW (fp32 [V, K], stride lddw) and dBias may each be NULL. It rewrites
+ * entries of E' in the workspace, so it runs at most once per forward: a second backward of the same forward goes
+ * through mce_bwd_lse_blocked. MCE_EINVAL if the forward took more than one row block.
+ */
+MCE_API int mce_train_target_logits(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, float* out,
+                                    void* stream);
+MCE_API int mce_bwd_lse_train(const uint16_t* H, int64_t ldh, const int64_t* y, const float* lse_rows,
+                              const float* g_lse, const float* g_ly, int64_t N, int64_t K, int64_t V, int64_t V_real,
+                              int64_t block_rows, void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw,
+                              float* dBias, void* ws, size_t ws_bytes, void* stream);
+
 /* Copies the number of rows the last mce_fwd_train on this workspace wrote by the exact fallback pass (all
  * blocks) into *out (a device int), on `stream`. No counterpart in the reference (diagnostics and tests). */
 MCE_API int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, int* out,

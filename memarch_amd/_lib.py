@@ -51,6 +51,8 @@ SIGNATURES = {
     "mce_bwd_train": (_INT, [_P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _INT, _I, _P, _I, _P, _P, _P, _S, _P]),
     "mce_bwd_train_dcval": (_INT, [_P, _P, _P, _INT, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _S, _P]),
     "mce_train_flagged": (_INT, [_P, _I, _I, _I, _I, _P, _P]),
+    "mce_train_target_logits": (_INT, [_P, _I, _I, _I, _I, _P, _P]),
+    "mce_bwd_lse_train": (_INT, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _INT, _I, _P, _I, _P, _P, _S, _P]),
     "mce_train_set_threshold": (None, [ctypes.c_float]),
     "mce_prof_start": (_INT, []),
     "mce_prof_stop": (_INT, [_P, _P, _INT]),

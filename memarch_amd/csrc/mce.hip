@@ -1785,6 +1785,77 @@ __device__ __forceinline__ int64_t cm_index(int64_t m, int64_t k, int64_t Mp) {
 }
 __device__ __forceinline__ uint16_t to_bf16(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xFFFFu); }
 
+// chunk_ce on the one-pass path (memarch full2.py:806-830: G = g_lse softmax(x) + g_ly onehot(y), the upstream
+// gradients arriving in the backward). The plain cross-entropy forward left E'[n, v] = exp(x_v - s_n) in G for
+// every v but the target, with s_n = e_n, or s_n = lse_n for a row of the exact pass. Per row this kernel forms
+// a_n = g_lse exp(s_n - lse_n) and writes the target entry E'[n, y] = (g_lse exp(x_y - lse) + g_ly) / a_n, so that
+// G = a . E' (the contractions' row scale) holds both terms. Where the one-hot term cannot be folded in that way
+// (a_n = 0, or the quotient past the bf16 range: the softmax term is then below 2^-64 of it), the row takes
+// a_n = g_ly and is listed for k_onehot_rows, which rewrites its E' as onehot(y). A target outside [0, V_real)
+// has no one-hot term. Rows N .. Np-1 get a_n = 0.
+__global__ __launch_bounds__(256) void k_lse_train_rows(const int64_t* __restrict__ y, const float* __restrict__ xy,
+                                                        const float* __restrict__ lse_rows,
+                                                        const float* __restrict__ lse_est,
+                                                        const int* __restrict__ flag, const float* __restrict__ g_lse,
+                                                        const float* __restrict__ g_ly, int64_t N, int64_t Np,
+                                                        int64_t Vreal, float* __restrict__ arow,
+                                                        int* __restrict__ ocount, int* __restrict__ olist,
+                                                        uint16_t* __restrict__ G) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= Np) return;
+  if (n >= N) {
+    arow[n] = 0.f;
+    return;
+  }
+  const float l = lse_rows[n], e = lse_est[n];
+  const float sh = (flag[n] || !(l - e <= 60.f)) ? l : e;   // k_train_rows' choice: the exact pass used lse
+  const float gl = g_lse != nullptr ? g_lse[n] : 0.f, gy = g_ly != nullptr ? g_ly[n] : 0.f;
+  const float a = gl * expf(sh - l);
+  const int64_t yn = y[n];
+  if (!(yn >= 0 && yn < Vreal)) {
+    arow[n] = a;
+    return;
+  }
+  const float x = xy[n];
+  const float t = __builtin_fmaf(gl, expf(x - l), gy) / a;
+  const bool folded = a != 0.f && fabsf(t) <= 3.0e38f;
+  if (folded || gy == 0.f || a != a) {
+    arow[n] = a;
+    G[cm_index(n, yn, Np)] = to_bf16(folded ? t : expf(x - sh));
+  } else {
+    arow[n] = gy;
+    olist[atomicAdd(ocount, 1)] = (int)n;
+  }
+}
+
+// E' rows listed by k_lse_train_rows rewritten as onehot(y): block (tm, r) writes vocabulary tile tm of listed rows
+// r*8 + j, r*8 + j + 8*R, ... (j = thread / 32); each of 32 lanes one 16-byte piece of the row's 256 positions.
+__global__ __launch_bounds__(256) void k_onehot_rows(const int* __restrict__ ocount, const int* __restrict__ olist,
+                                                     const int64_t* __restrict__ y, int64_t Np,
+                                                     uint16_t* __restrict__ G) {
+  const int cnt = *ocount;
+  const int tm = (int)blockIdx.x, piece = (int)threadIdx.x & 31;
+  for (int i = (int)blockIdx.y * 8 + ((int)threadIdx.x >> 5); i < cnt; i += (int)gridDim.y * 8) {
+    const int64_t n = olist[i], yn = y[n];
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (yn / BM == tm) {
+      const int kp = kperm((int)(yn % BM));
+      if (kp >> 3 == piece) {
+        const int e = kp & 7;   // bf16 1.0 in element e of the piece
+        const uint32_t one = 0x3F80u << (16 * (e & 1));
+        if ((e >> 1) == 0) v.x = one;
+        else if ((e >> 1) == 1) v.y = one;
+        else if ((e >> 1) == 2) v.z = one;
+        else v.w = one;
+      }
+    }
+    *reinterpret_cast<u32x4*>(G + (int64_t)tm * (Np / BM) * CM_TILE + (n / BM) * CM_TILE +
+                              ((((n % BM) >> 3) * 32 + piece) * 64) + (n & 7) * 8) = v;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_zero_i32(int* __restrict__ p) { if (threadIdx.x == 0) *p = 0; }
+
 // Forward tile of the training path: the logits tile as in k_fwd_tiles, then E = exp(x - e_n) for its 256 x 256
 // elements, rounded to bf16 and stored into G exactly as k_bwd_grad stores it (store_g_block). The
 // half-tile partials are (e_n, sum of E) -- or, for a flagged row, (max, sum of exp(x - max)) -- in the part_m /
@@ -3020,7 +3091,7 @@ struct TrainWs {
   int64_t np, vp, nb, nblk;
   uint16_t *G, *Ht, *uperm, *Wt;
   float *part_m, *part_s, *xy, *xc, *cb, *lse_est, *arow, *upart, *part, *xpart, *dbias_part, *sum_part;
-  int *flag, *flag_list, *counts, *xlist;
+  int *flag, *flag_list, *counts, *xlist, *olist, *ocount;
   size_t bytes;
 };
 constexpr int DBIAS_SPLITS = 8;
@@ -3071,6 +3142,9 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   // (counts[np/256 + b]); the list of the latter, reused block after block
   w.counts = reinterpret_cast<int*>(take(sizeof(int) * 2 * (np / BLK)));
   w.xlist = reinterpret_cast<int*>(take(sizeof(int) * nb));
+  // chunk_ce's one-pass backward: the rows whose gradient is the one-hot term alone, and their count
+  w.olist = reinterpret_cast<int*>(take(sizeof(int) * nb));
+  w.ocount = reinterpret_cast<int*>(take(sizeof(int)));
   // dW blocks' dBias partials: 32 values per row group, tile of the dW grid and tail K slice
   w.upart = reinterpret_cast<float*>(
       take(sizeof(float) * 32 * fold_nr(cdiv(K, BN)) * ((w.vp / BM) * cdiv(K, BN) + TAIL_SLOTS)));
@@ -3286,6 +3360,40 @@ int bwd_train_impl(const uint16_t* H, int64_t ldh, const float* go, const float*
     return launch_status();
   }
   return MCE_OK;
+}
+
+// chunk_ce's backward on the one-pass path: after mce_fwd_train (plain cross-entropy, one row block) the workspace
+// holds E' for all rows; k_lse_train_rows folds (g_lse, g_ly) into a_n and the target entries (k_onehot_rows for
+// the rows that take the one-hot term alone), then the block's contractions run with go = 1.
+int bwd_lse_train_impl(const uint16_t* H, int64_t ldh, const int64_t* y, const float* lse_rows, const float* g_lse,
+                       const float* g_ly, int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows,
+                       void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw, float* dBias, void* ws,
+                       size_t ws_bytes, hipStream_t st) {
+  int rc = check_hidden(H, ldh, N, K, V);
+  if (rc) return rc;
+  if (block_rows < 0 || V_real < 1 || V_real > V || (dH && lddh < K) || (dW && lddw < K)) return MCE_EINVAL;
+  if (dH && !dh_aligned(dH, lddh, dh_bf16)) return MCE_EALIGN;
+  if (N == 0) {
+    if (dW) {
+      hipLaunchKernelGGL(k_fill2d_f32, dim3((unsigned)cdiv(V * K, 256)), dim3(256), 0, st, dW, lddw, V, K, 0.f);
+      if ((rc = launch_status())) return rc;
+    }
+    if (dBias) hipLaunchKernelGGL(k_fill_f32, dim3((unsigned)cdiv(V, 256)), dim3(256), 0, st, dBias, V, 0.f);
+    return launch_status();
+  }
+  if (!ws || !y || !lse_rows) return MCE_EINVAL;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(ws), N, K, V, block_rows);
+  if (ws_bytes < w.bytes) return MCE_EWORKSPACE;
+  if (w.nblk != 1) return MCE_EINVAL;   // E' of every row must still be in the workspace
+  hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(64), 0, st, w.ocount);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_lse_train_rows, dim3((unsigned)(w.np / 256)), dim3(256), 0, st, y, w.xy, lse_rows, w.lse_est,
+                     w.flag, g_lse, g_ly, N, w.np, V_real, w.arow, w.ocount, w.olist, w.G);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(k_onehot_rows, dim3((unsigned)(w.vp / BM), 8), dim3(256), 0, st, w.ocount, w.olist, y, w.np,
+                     w.G);
+  if ((rc = launch_status())) return rc;
+  return train_block_grads(w, 0, H, ldh, N, K, V, nullptr, dH, dh_bf16, lddh, dW, lddw, nullptr, dBias, nullptr, st);
 }
 
 }  // namespace
@@ -3580,6 +3688,28 @@ int mce_bwd_train_dcval(const int64_t* y, const int64_t* cand, const float* cval
   hipLaunchKernelGGL(k_sparse_rows, dim3((unsigned)cdiv(N, 4)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
                      y, cand, cval, kc, w.xy, w.xc, lse_rows, wgt_rows, go, N, V_real, nullptr, nullptr, dCval);
   return launch_status();
+}
+
+int mce_bwd_lse_train(const uint16_t* H, int64_t ldh, const int64_t* y, const float* lse_rows, const float* g_lse,
+                      const float* g_ly, int64_t N, int64_t K, int64_t V, int64_t V_real, int64_t block_rows,
+                      void* dH, int dh_bf16, int64_t lddh, float* dW, int64_t lddw, float* dBias, void* ws,
+                      size_t ws_bytes, void* stream) {
+  return bwd_lse_train_impl(H, ldh, y, lse_rows, g_lse, g_ly, N, K, V, V_real, block_rows, dH, dh_bf16, lddh, dW,
+                            lddw, dBias, ws, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int mce_train_target_logits(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, float* out,
+                            void* stream) {
+  if (ws == nullptr || out == nullptr || N < 0 || K <= 0 || V <= 0 || block_rows < 0) return MCE_EINVAL;
+  if (N == 0) return MCE_OK;
+  const TrainWs w = train_ws_layout(reinterpret_cast<char*>(const_cast<void*>(ws)), N, K, V, block_rows);
+  const hipError_t e = hipMemcpyAsync(out, w.xy, sizeof(float) * N, hipMemcpyDeviceToDevice,
+                                      reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) {
+    g_last_hip_error = (int)e;
+    return MCE_ELAUNCH;
+  }
+  return MCE_OK;
 }
 
 int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, int* out, void* stream) {

@@ -60,16 +60,76 @@ def _check(what, lse, ly, h, w, b, fwd, g):
             assert errs[k] <= GRAD_RTOL, (what, k, errs)
 
 
+def _paths(mode, monkeypatch):
+    """one_pass: the default (E' kept from the forward); recompute: RECOMPUTE; blocks: 256-row blocks, so a case of
+    more than 256 rows takes the recompute path block by block."""
+    from memarch_amd import fused_ops
+    monkeypatch.setattr(fused_ops, "RECOMPUTE", mode == "recompute")
+    monkeypatch.setattr(fused_ops, "BLOCK_ROWS", 256 if mode == "blocks" else 0)
+
+
+def _classes(fn):
+    """Launch counts of the library's kernel classes (mce_prof_stop) while fn() runs."""
+    import ctypes
+    from memarch_amd import _lib
+    lib = _lib.load()
+    _lib.check(lib.mce_prof_start(), "mce_prof_start")
+    out = fn()
+    torch.cuda.synchronize()
+    ms = (ctypes.c_double * 5)()
+    n = (ctypes.c_int64 * 5)()
+    _lib.check(lib.mce_prof_stop(ms, n, 5), "mce_prof_stop")
+    return out, [n[i] for i in range(5)]
+
+
+@pytest.mark.parametrize("mode", ["one_pass", "recompute", "blocks"])
 @pytest.mark.parametrize("shape", [(256, 128, 512, True), (300, 72, 1000, False), (777, 520, 2051, True),
                                    (64, 2048, 1025, True)], ids=lambda s: "N{}_K{}_V{}_b{}".format(*s))
-def test_chunk_ce_parity(shape):
+def test_chunk_ce_parity(shape, mode, monkeypatch):
     N, K, V, bias = shape
-    print(f"chunk_ce {shape}", flush=True)
+    _paths(mode, monkeypatch)
+    print(f"chunk_ce {shape} {mode}", flush=True)
     c = _case(N, K, V, seed=N + V, bias=bias)
-    lse, ly, h, w, b = _run(c)
+    (lse, ly, h, w, b), counts = _classes(lambda: _run(c))
     assert lse.dtype == ly.dtype == torch.float32 and h.grad.dtype == torch.bfloat16
+    # classes: 0 the one-pass logits tiles, 1 the statistics-only tiles, 2 the recomputed logits-gradient tiles
+    one_pass = mode == "one_pass" or (mode == "blocks" and N <= 256)
+    assert (counts[0] > 0, counts[2] > 0) == (one_pass, not one_pass), counts
     fwd, g = _oracle(c)
-    _check(f"chunk_ce {shape}", lse, ly, h, w, b, fwd, g)
+    _check(f"chunk_ce {shape} {mode}", lse, ly, h, w, b, fwd, g)
+
+
+def test_chunk_ce_second_backward():
+    """retain_graph: the first backward of a one-pass forward rewrites entries of E', so a second backward of the
+    same forward (other upstream gradients) takes the recompute path; both match the oracle."""
+    from memarch_amd.chunk_ce import chunk_ce
+    c = _case(300, 256, 1100, seed=41)
+    h = c["h"].cuda().bfloat16().requires_grad_()
+    w = c["w"].cuda().requires_grad_()
+    b = c["b"].cuda().requires_grad_()
+    lse, ly = chunk_ce(h, w, b, c["y"].cuda())
+    for i in range(2):
+        gl = torch.randn(300, generator=torch.Generator().manual_seed(50 + i))
+        gy = torch.randn(300, generator=torch.Generator().manual_seed(60 + i))
+        h.grad = w.grad = b.grad = None
+        ((lse * gl.cuda()).sum() + (ly * gy.cuda()).sum()).backward(retain_graph=True)
+        torch.cuda.synchronize()
+        ci = dict(c, gl=gl, gy=gy)
+        fwd, g = _oracle(ci)
+        _check(f"second backward {i}", lse, ly, h, w, b, fwd, g)
+
+
+def test_chunk_ce_one_hot_rows():
+    """Rows where the one-hot term cannot be folded into the target entry: g_lse = 0 with g_ly != 0 (the row's
+    gradient is g_ly onehot(y) alone), a denormal g_lse (a_n underflows), and g_lse = g_ly = 0 rows beside them."""
+    c = _case(513, 192, 1300, seed=43)
+    c["gl"][::3] = 0.0
+    c["gl"][1::7] = 1e-42
+    c["gl"][2::11] = 0.0
+    c["gy"][2::11] = 0.0
+    lse, ly, h, w, b = _run(c)
+    fwd, g = _oracle(c)
+    _check("one-hot rows", lse, ly, h, w, b, fwd, g)
 
 
 def test_chunk_ce_dtypes_and_masked_bias():
