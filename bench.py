@@ -344,10 +344,11 @@ def make_folded(inp, cfg):
 
 
 def peak_rows(inp, frac, vid=1000, seed=5):
-    """A seeded fraction of rows gets one logit 50-100 above its e_n (the first vocabulary tile's logsumexp and
-    the target logit, about -0.5 here): coordinate 0 of every hidden state and of every vocabulary row is set to 0,
-    then w[vid, 0] = 1 and h[n, 0] = gap_n - bias[vid] - 0.5 on the chosen rows (vid outside the first tile), so their
-    logit at vid is about gap_n above e_n, gap_n ~ U(50, 100). The other logits move by one of d coordinates."""
+    """A seeded fraction of rows gets one logit 50-100 above -0.5 (about the logsumexp of the first 256 ids, the
+    head of the Zipf bias), so at least that far above its e_n (the row's target logit, which lies below it):
+    coordinate 0 of every hidden state and of every vocabulary row is set to 0, then w[vid, 0] = 1 and
+    h[n, 0] = gap_n - bias[vid] - 0.5 on the chosen rows, so their logit at vid is gap_n - 0.5, gap_n ~ U(50, 100).
+    The other logits move by one of d coordinates."""
     g = torch.Generator().manual_seed(seed)
     n = inp.h.shape[0]
     rows = torch.randperm(n, generator=g)[:int(round(frac * n))]
