@@ -44,10 +44,10 @@ METRIC = "tokens/s fused out+CE+pointer fwd+bwd, d=2048 V=50304; % bf16 MFMA pea
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_ce_cfg2_hbm_traffic.md")
 
 # C-ABI call -> stage. One-pass path (default): mce_fwd_train (row blocks: logits tiles, merge, and every block
-# but the last its dH / dW contractions), mce_bwd_train (the last block's contractions); recompute path: mce_fwd,
-# then mce_bwd_blocked (per row block: the logits recomputed into G, its dH rows, dW and dBias accumulated) or, for
-# chunk_ce, mce_lse_fwd and mce_bwd_lse_blocked; --stage-reps times the separate steps mce_bwd_logits_grad,
-# mce_bwd_dhidden, mce_bwd_dweight.
+# but the last its dH / dW contractions), mce_bwd_train (the last block's contractions), or for chunk_ce
+# mce_bwd_lse_train; recompute path: mce_fwd, then mce_bwd_blocked (per row block: the logits recomputed into G, its
+# dH rows, dW and dBias accumulated) or, for chunk_ce, mce_lse_fwd and mce_bwd_lse_blocked; --stage-reps times the
+# separate steps mce_bwd_logits_grad, mce_bwd_dhidden, mce_bwd_dweight.
 STAGE_STEPS = 3   # steps after the timed ones that carry the per-stage stream events (`stages_ms`)
 STAGE_OF_CALL = {"mce_fwd_train": "fwd", "mce_bwd_train": "bwd", "mce_fwd_train_sparse": "fwd",
                  "mce_fwd": "fwd", "mce_bwd_logits_grad": "logits_grad", "mce_bwd_dhidden": "dhidden",
@@ -843,9 +843,8 @@ def main():
     if args.peaked > 0:
         res["config"]["peaked_rows"] = args.peaked
         res["fallback_rows_per_step"] = int(flagged.item()) // args.steps if args.path == "one-pass" else None
-    one_pass_ops = ("fused_ce", "linear_ce", "linear_ce_sparse")   # chunk_ce: gradient coefficients known only in the backward
-    res["path"] = args.path if args.op in one_pass_ops else "recompute"
-    if args.other_path_steps > 0 and args.op in one_pass_ops:
+    res["path"] = args.path
+    if args.other_path_steps > 0:
         other = "recompute" if args.path == "one-pass" else "one-pass"
         print(f"[bench] {other} path for comparison", file=sys.stderr, flush=True)
         res["other_path"] = {"path": other,
