@@ -1048,6 +1048,8 @@ __device__ __forceinline__ void cand_summary(int64_t ck, float vk, int kc, int l
 // h_n . w_c over K (fp32 products of the bf16 values), reduced over the wave; every lane gets the sum.
 __device__ __forceinline__ float row_dot(const uint16_t* hr, const uint16_t* wr, int64_t K, int lane) {
   float s = 0.f;
+  // unrolled so that the loads of several K steps are in flight at once (the sums keep their order)
+#pragma unroll 4
   for (int64_t k = (int64_t)lane * 8; k < K; k += 512) {
     const u16x8 a = *reinterpret_cast<const u16x8*>(hr + k);
     const u16x8 b = *reinterpret_cast<const u16x8*>(wr + k);
