@@ -1187,8 +1187,30 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
   float m = -INFINITY, s = 0.f;
   if (n < N) {
     int tb = sl;
-    // four partials per step (independent loads), folded into (m, s) against their common maximum; a partial
+    // four partials per fold (independent loads), folded into (m, s) against their common maximum; a partial
     // with max -inf has sum 0 and contributes 0 * exp(-inf) = 0
+    auto fold4 = [&](const float (&mm)[4], const float (&ss)[4]) {
+      const float M4 = fmaxf(fmaxf(m, fmaxf(mm[0], mm[1])), fmaxf(mm[2], mm[3]));
+      if (M4 == -INFINITY) return;
+      float acc = m == -INFINITY ? 0.f : s * expf(m - M4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc += ss[q] * expf(mm[q] - M4);
+      s = acc;
+      m = M4;
+    };
+    // two folds' loads issued together (16 in flight per thread: the merge is bound by their latency)
+    for (; tb + 56 < T; tb += 64) {
+      float mm[2][4], ss[2][4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          mm[h][q] = part_m[(int64_t)(tb + 32 * h + 8 * q) * N + n];
+          ss[h][q] = part_s[(int64_t)(tb + 32 * h + 8 * q) * N + n];
+        }
+      fold4(mm[0], ss[0]);
+      fold4(mm[1], ss[1]);
+    }
     for (; tb + 24 < T; tb += 32) {
       float mm[4], ss[4];
 #pragma unroll
@@ -1196,13 +1218,7 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
         mm[q] = part_m[(int64_t)(tb + 8 * q) * N + n];
         ss[q] = part_s[(int64_t)(tb + 8 * q) * N + n];
       }
-      const float M4 = fmaxf(fmaxf(m, fmaxf(mm[0], mm[1])), fmaxf(mm[2], mm[3]));
-      if (M4 == -INFINITY) continue;
-      float acc = m == -INFINITY ? 0.f : s * expf(m - M4);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc += ss[q] * expf(mm[q] - M4);
-      s = acc;
-      m = M4;
+      fold4(mm, ss);
     }
     for (; tb < T; tb += 8) {
       const float mm = part_m[(int64_t)tb * N + n];
@@ -2672,8 +2688,10 @@ hipEvent_t prof_event() {  // with g_prof_mu held
     g_prof_pool.pop_back();
     return e;
   }
+  // timing only: no system-scope fence (cache writeback and invalidation) at each record, which would otherwise put
+  // some 5 us of idle time before and after every timed launch
   hipEvent_t e = nullptr;
-  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+  return hipEventCreateWithFlags(&e, hipEventDisableSystemFence) == hipSuccess ? e : nullptr;
 }
 
 class ProfScope {
