@@ -866,8 +866,6 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group,
   tile_of(xcd_lin((int)blockIdx.x, (int)gridDim.x), tiles_m, tiles_n, group, tm, tn);
 }
 
-__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * LOG2E); }
-
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 // two floats -> two bf16 (round to nearest even) in one 32-bit word, lo in the low half (one v_cvt_pk_bf16_f32)
