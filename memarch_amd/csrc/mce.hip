@@ -1376,6 +1376,24 @@ __global__ __launch_bounds__(256) void k_sum_chunks(const float* __restrict__ x,
   if (t == 0) part[blockIdx.x] = red[0];
 }
 
+// The same sum in one block when count <= SUM_ONE_BLOCK (one launch instead of two): thread t adds values t, t+1024,
+// ... (loads unrolled so that several are in flight), then a fixed-order tree over the 1024 threads.
+constexpr int64_t SUM_ONE_BLOCK = 65536;
+__global__ __launch_bounds__(1024) void k_sum_one(const float* __restrict__ x, int64_t count, float* __restrict__ out) {
+  __shared__ float red[1024];
+  const int t = threadIdx.x;
+  float s = 0.f;
+#pragma unroll 8
+  for (int64_t k = t; k < count; k += 1024) s += x[k];
+  red[t] = s;
+  __syncthreads();
+  for (int k = 512; k > 0; k >>= 1) {
+    if (t < k) red[t] += red[t + k];
+    __syncthreads();
+  }
+  if (t == 0) out[0] = red[0];
+}
+
 __global__ __launch_bounds__(256) void k_sum(const float* __restrict__ part, int64_t count, float* __restrict__ out) {
   __shared__ float red[256];
   const int t = threadIdx.x;
@@ -2849,6 +2867,10 @@ int check_sparse(const int64_t* cand, const float* cval, int kc, int64_t N) {
 
 // out[0] = the sum of x[0 .. count-1] (k_sum_chunks, then k_sum over its partials).
 int launch_sum(const float* x, int64_t count, float* part, float* out, hipStream_t st) {
+  if (count <= SUM_ONE_BLOCK) {
+    hipLaunchKernelGGL(k_sum_one, dim3(1), dim3(1024), 0, st, x, count, out);
+    return launch_status();
+  }
   const int64_t chunks = cdiv(count, SUM_CHUNK);
   hipLaunchKernelGGL(k_sum_chunks, dim3((unsigned)chunks), dim3(256), 0, st, x, count, part);
   int rc = launch_status();
