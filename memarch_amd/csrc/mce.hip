@@ -1196,7 +1196,7 @@ __global__ __launch_bounds__(256) void k_fwd_merge(const float* __restrict__ par
       s = acc;
       m = M4;
     };
-    // two folds' loads issued together (16 in flight per thread: the merge is bound by their latency)
+    // two folds' loads issued together (16 per thread in flight), folded in the same order as one at a time
     for (; tb + 56 < T; tb += 64) {
       float mm[2][4], ss[2][4];
 #pragma unroll
