@@ -343,17 +343,18 @@ MCE_API int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, i
                               void* stream);
 
 /* Test hook: the bound on a row's sum of E over one half tile (128 vocabulary rows) above which the row takes
- * the exact fallback pass; s_max <= 0 restores the default 2^64. Process-wide; affects later mce_fwd_train
- * calls. No counterpart in the reference. */
+ * the exact fallback pass; s_max <= 0 restores the default 2^64. Per host thread: affects the later mce_fwd_train
+ * calls of the calling thread only. No counterpart in the reference. */
 MCE_API void mce_train_set_threshold(float s_max);
 
 /*
  * Kernel timing for benchmarks. No counterpart in the reference. After mce_prof_start(), every launch of the
  * library's contraction kernels records a pair of HIP events on its stream; mce_prof_stop() waits for them and
  * writes, per class c < nclass, the summed kernel time in ms (ms[c]) and the number of launches (launches[c]), then
- * stops recording. Classes: 0 the one-pass logits tiles (k_fwd_train), 1 the statistics-only logits tiles
- * (k_fwd_tiles over all vocabulary tiles), 2 the recompute logits-gradient tiles (k_bwd_grad), 3 dH GEMMs, 4 dW
- * GEMMs. Not for use inside graph capture.
+ * stops recording. Process-wide, from any host thread (an autograd backward runs on the engine's own thread).
+ * Classes: 0 the one-pass logits tiles (k_fwd_train), 1 the statistics-only logits tiles (k_fwd_tiles over all
+ * vocabulary tiles), 2 the recompute logits-gradient tiles (k_bwd_grad), 3 dH GEMMs, 4 dW GEMMs. Not for use inside
+ * graph capture.
  */
 MCE_API int mce_prof_start(void);
 MCE_API int mce_prof_stop(double* ms, int64_t* launches, int nclass);

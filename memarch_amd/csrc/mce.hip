@@ -2686,7 +2686,8 @@ int check_common(const void* H, int64_t ldh, const void* W, int64_t ldw, int64_t
 int check_bias(const float* bias) { return (bias != nullptr && (reinterpret_cast<uintptr_t>(bias) & 3)) ? MCE_EALIGN : MCE_OK; }
 
 // Kernel-class timing for benchmarks (mce_prof_start / mce_prof_stop): while enabled, a pair of HIP events is
-// recorded on the launch stream around every launch of the classes below.
+// recorded on the launch stream around every launch of the classes below. Process-wide: an autograd backward makes
+// its launches on the engine's own thread.
 enum { PROF_FWD_TRAIN = 0, PROF_FWD_TILES = 1, PROF_BWD_GRAD = 2, PROF_GEMM_DH = 3, PROF_GEMM_DW = 4, PROF_NONE = 5,
        PROF_CLASSES = 5 };
 struct ProfRec {
@@ -3196,7 +3197,7 @@ TrainWs train_ws_layout(char* base, int64_t N, int64_t K, int64_t V, int64_t req
   return w;
 }
 
-std::atomic<float> g_train_s_max{TRAIN_S_MAX};  // test hook: mce_train_set_threshold
+thread_local float t_train_s_max = TRAIN_S_MAX;  // test hook: mce_train_set_threshold, per host thread
 
 // The gradient contractions of row block b: dH rows = s * a_n (E' W) into dH (bf16 or fp32, row stride lddh);
 // dW = s (E'^T (a . H) + dW_in) and dBias = s (E'^T a + dBias_in), with s = go[0] (1 when go is null); any output may
@@ -3307,7 +3308,7 @@ int fwd_train_impl(const uint16_t* H, int64_t ldh, uint16_t* W, int64_t ldw, con
                      cval, kc, N, K, V_real, w.xy, w.xc, w.cb, nullptr, w.lse_est, w.flag, w.counts,
                      (int)(2 * w.np / BLK), w.np);
   if ((rc = launch_status())) return rc;
-  const float s_max = g_train_s_max.load(std::memory_order_relaxed);
+  const float s_max = t_train_s_max;
   for (int64_t b = 0; b < w.nblk; ++b) {
     const int64_t row0 = b * w.nb, rows = std::min(w.nb, N - row0), rp = cdiv(rows, BLK) * BLK;
     const int tnb = (int)(rp / BN);
@@ -3797,7 +3798,7 @@ int mce_prof_stop(double* ms, int64_t* launches, int nclass) {
 }
 
 void mce_train_set_threshold(float s_max) {
-  g_train_s_max.store(s_max > 0.f ? s_max : TRAIN_S_MAX, std::memory_order_relaxed);
+  t_train_s_max = s_max > 0.f ? s_max : TRAIN_S_MAX;
 }
 
 }  // extern "C"

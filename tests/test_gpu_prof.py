@@ -2,14 +2,19 @@
 launch of a contraction class is bracketed by a pair of HIP events recorded on its stream. Checked on the one-pass
 path (one block, 256-row blocks) and the recompute path: the step's outputs and gradients are bit-identical with
 and without the timing, each class counts its launches per step, every class's summed time is positive and within
-the wall time of the timed steps, and nothing is recorded once it is off."""
+the wall time of the timed steps, and nothing is recorded once it is off.
+
+The timing is process-wide (an autograd backward makes its launches on the engine's own thread, and the one-block
+cases above count them); the test hook mce_train_set_threshold moves the exact-pass bound of the calling thread's
+later calls only."""
 import ctypes
+import threading
 import time
 
 import pytest
 import torch
 
-from cases import random_case
+from cases import capi_train, random_case
 
 pytestmark = pytest.mark.gpu
 
@@ -78,3 +83,38 @@ def test_kernel_class_events(mode, monkeypatch):
     torch.cuda.synchronize()
     _lib.check(lib.mce_prof_stop(ms, n, NCLASS), "mce_prof_stop")
     assert all(n[i] == 0 for i in range(NCLASS))
+
+
+def test_threshold_is_per_thread():
+    """A threshold that a second thread sets (1e-30: every row takes the exact pass there) leaves the main thread's
+    calls at the default bound (no row flagged), while that thread's own call flags every row."""
+    from memarch_amd import _lib
+    print("threshold per thread", flush=True)
+    lib = _lib.load()
+    case = random_case(N, K, V, VR, True, seed=78)
+    ready, done = threading.Event(), threading.Event()
+    errs, flagged_other = [], []
+
+    def other():
+        try:
+            lib.mce_train_set_threshold(1e-30)
+            ready.set()
+            done.wait(60)
+            flagged_other.append(capi_train(case)["flagged"])
+        except Exception as e:  # noqa: BLE001 - reported by the main thread
+            errs.append(e)
+            ready.set()
+        finally:
+            lib.mce_train_set_threshold(0.0)
+
+    th = threading.Thread(target=other)
+    th.start()
+    assert ready.wait(60)
+    try:
+        flagged_main = capi_train(case)["flagged"]
+    finally:
+        done.set()
+        th.join()
+    assert not errs, errs
+    assert flagged_main == 0, flagged_main
+    assert flagged_other == [N], flagged_other
