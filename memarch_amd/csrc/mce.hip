@@ -1305,6 +1305,12 @@ __global__ __launch_bounds__(256) void k_fill_f32(float* __restrict__ p, int64_t
   if (i < n) p[i] = v;
 }
 
+// dst[0 .. n-1] = src[0 .. n-1] (a kernel rather than hipMemcpyAsync, so that a captured call records no copy node).
+__global__ __launch_bounds__(256) void k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
 // p[r * ld + c] = v for r < rows, c < cols.
 __global__ __launch_bounds__(256) void k_fill2d_f32(float* __restrict__ p, int64_t ld, int64_t rows, int64_t cols,
                                                     float v) {
@@ -3744,13 +3750,9 @@ int mce_train_target_logits(const void* ws, int64_t N, int64_t K, int64_t V, int
   if (ws == nullptr || out == nullptr || N < 0 || K <= 0 || V <= 0 || block_rows < 0) return MCE_EINVAL;
   if (N == 0) return MCE_OK;
   const TrainWs w = train_ws_layout(reinterpret_cast<char*>(const_cast<void*>(ws)), N, K, V, block_rows);
-  const hipError_t e = hipMemcpyAsync(out, w.xy, sizeof(float) * N, hipMemcpyDeviceToDevice,
-                                      reinterpret_cast<hipStream_t>(stream));
-  if (e != hipSuccess) {
-    g_last_hip_error = (int)e;
-    return MCE_ELAUNCH;
-  }
-  return MCE_OK;
+  hipLaunchKernelGGL(k_copy_f32, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     w.xy, out, N);
+  return launch_status();
 }
 
 int mce_train_flagged(const void* ws, int64_t N, int64_t K, int64_t V, int64_t block_rows, int* out, void* stream) {
